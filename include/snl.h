@@ -1,0 +1,185 @@
+/*
+ * snl.h -- C ABI of the MI355X-native MTP speculative decode step.
+ *
+ * The reference (dparnell/sense-nova-server, crate `sensenova-loop`) has no FFI: its
+ * worker calls the Rust `Engine` directly.  The engine entry points below replace those
+ * methods one for one, with the reference's argument meaning and error classes; each
+ * cites the method it replaces.  All pointers are plain host pointers unless a comment
+ * says "device"; no call keeps a pointer after it returns.  One engine handle is used by
+ * one thread at a time (the reference's Engine is owned by a single generation thread,
+ * src/worker.rs:76-105).  Every engine call has finished on the device when it returns.
+ */
+#ifndef SNL_H
+#define SNL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  After any error other than SNL_EARG the caller resets the engine, as the
+ * reference worker does after a failed request (src/worker.rs:94-101). */
+enum {
+    SNL_OK = 0,
+    SNL_EARG = 1,     /* bad argument (src/engine.rs:810-818, :716-718) */
+    SNL_ECTX = 2,     /* context length exceeded (src/engine.rs:819-821) */
+    SNL_ETOKEN = 3,   /* token id out of range (src/engine.rs:784-786) */
+    SNL_EDEVICE = 4,  /* HIP runtime error */
+    SNL_ENOMEM = 5,   /* device allocation failed */
+    SNL_ESTATE = 6    /* call not valid in the engine's state (e.g. rollback without a checkpoint) */
+};
+
+/* Model hyper-parameters: ModelConfig (src/config.rs:6-37).  mhc_streams = 0 means no mHC. */
+typedef struct snl_config {
+    int32_t hidden, intermediate, vocab, n_layers;
+    int32_t n_heads, n_kv_heads, head_dim, rot_dim;
+    float rope_theta, eps;
+    int32_t mrope_section[3];
+    int32_t lin_k_heads, lin_v_heads, lin_k_dim, lin_v_dim, conv_kernel;
+    int32_t loop_start, loop_end, loop_count;
+    int32_t mhc_start, mhc_end, mhc_streams, mhc_iterations;
+    int32_t has_mtp;
+    int32_t n_eos;
+    uint32_t eos[4];
+    uint8_t full_attention[64];
+} snl_config;
+
+/* Greedy pick of one logits row: first index of the maximum (src/sampler.rs:169-177),
+ * the maximum and the second largest value (top1 - top2 is the argmax tie margin). */
+typedef struct snl_pick {
+    uint32_t token;
+    float top1;
+    float top2;
+    uint32_t _pad;
+} snl_pick;
+
+typedef struct snl_engine snl_engine;
+
+/* ---- lifecycle ------------------------------------------------------------------------ */
+
+/* Engine::load (src/engine.rs:230-644) with weights drawn on the device from `seed`
+ * (quant 0 = Q8_0, 1 = Q4_0 for the matrices a Q4_0 file quantises; embedding, LM head,
+ * DeltaNet in_proj and the MTP head stay Q8_0 as in src/convert.rs:228-311).
+ * ctx = KV positions per attention layer.  Returns SNL_OK and *out, or an error. */
+int snl_engine_create(const snl_config* cfg, uint64_t seed, int quant, int ctx, snl_engine** out);
+void snl_engine_destroy(snl_engine* e);
+/* Message of the last failed call on this handle ("" if none). */
+const char* snl_last_error(const snl_engine* e);
+/* Message of the last snl_engine_create failure in this process. */
+const char* snl_create_error(void);
+
+/* ---- Engine API (src/engine.rs) --------------------------------------------------------- */
+
+/* Engine::forward_mm (src/engine.rs:801-936) for text tokens: feed `tokens[n]` at the
+ * current position.  pos3 gives each token's rotary (t, h, w) position ([n][3]) or NULL
+ * for the cache position.  logit_rows (0..2) rows of logits are produced for the last
+ * tokens; ckpt (requires n == 2) saves the recurrent state after the first token so that
+ * snl_rollback can undo the second.  logits_out (nullable) receives rows x vocab floats,
+ * picks_out (nullable) one snl_pick per row. */
+int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows, int ckpt,
+                float* logits_out, snl_pick* picks_out);
+
+/* One forward pass (n <= 2 tokens, same semantics as snl_forward) launched op by op with
+ * a device timestamp between ops, as the reference's per-op profile mode
+ * (SENSENOVA_PROFILE, src/engine.rs:859-886).  recs[max_recs] receives, per op, its name,
+ * its algorithmic HBM bytes (GEMV: quants + scales + input rows + output; 0 where not
+ * counted) and its duration in ms; *n_recs the number of records. */
+typedef struct snl_op_time {
+    char name[24];
+    double bytes;
+    double ms;
+} snl_op_time;
+int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows,
+                         int ckpt, snl_op_time* recs, int max_recs, int* n_recs);
+
+/* Engine::mtp (src/engine.rs:713-774): run the MTP head on pairs (hidden row r0+i of the
+ * last step, tokens[i]) into MTP cache slots slot0+i with rotary positions pos3[i].  With
+ * draft != 0, *draft_out receives the draft token, pick_out (nullable) its pick and
+ * logits_out (nullable) the vocab logits. */
+int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t* pos3, int slot0, int draft,
+            uint32_t* draft_out, snl_pick* pick_out, float* logits_out);
+
+/* Engine::rollback (src/engine.rs:688-697): undo the second token of the last 2-token
+ * checkpointed forward. */
+int snl_rollback(snl_engine* e);
+/* Engine::snapshot / restore / reset (src/engine.rs:646-683). slot < 4. */
+int snl_snapshot(snl_engine* e, int slot);
+int snl_restore(snl_engine* e, int slot, int pos);
+int snl_reset(snl_engine* e);
+/* Fields and getters the worker reads (src/engine.rs:700-706, src/worker.rs:124, :292). */
+int snl_pos(const snl_engine* e);
+int snl_ctx(const snl_engine* e);
+int snl_hid_rows(const snl_engine* e);
+int snl_has_mtp(const snl_engine* e);
+int snl_prefill_chunk(const snl_engine* e);
+
+/* ---- the greedy MTP decode loop (src/worker.rs:123-255) ---------------------------------- */
+
+typedef struct snl_gen_stats {
+    int32_t generated, drafted, accepted, _pad;
+    double prefill_s, decode_s, draft_s, verify_s;
+} snl_gen_stats;
+
+/* Worker::run for one text prompt with greedy sampling (temperature 0, no penalties) and no
+ * prefix cache: prefill, then draft / verify / accept-or-rollback until max_tokens tokens
+ * (or an EOS id).  spec = 0 decodes one token per forward.  The speculation self-pause of
+ * src/worker.rs:222-234 is off.  out[max_tokens] receives the tokens; gaps (nullable) the
+ * top-2 margin of the logits row each token was taken from. */
+int snl_generate(snl_engine* e, const uint32_t* prompt, int n, int max_tokens, int spec, uint32_t* out,
+                 float* gaps, snl_gen_stats* stats);
+
+/* The same loop one step at a time: snl_decoder_create prefills the prompt (Worker::feed,
+ * src/worker.rs:291-323) and holds the first sampled token; each snl_decoder_step emits the
+ * pending token and runs one speculative step (draft, 2-token verify, accept or rollback),
+ * emitting the draft too when it is accepted.  out[2] / gaps[2] (nullable) receive the
+ * emitted tokens, *n_out their number (1 or 2). */
+typedef struct snl_decoder snl_decoder;
+int snl_decoder_create(snl_engine* e, const uint32_t* prompt, int n, int spec, snl_decoder** out);
+int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out);
+int snl_decoder_stats(const snl_decoder* d, snl_gen_stats* out);
+void snl_decoder_destroy(snl_decoder* d);
+
+/* ---- inspection (tests) ------------------------------------------------------------------- */
+
+/* Shape of a generated tensor: layer -1 = embed(1)/lm_head(2)/norm(3); layer 0xFFF = MTP
+ * head.  Returns the type (0 Q8_0, 1 Q4_0, 2 f32 vector) or -1. */
+int snl_tensor_info(const snl_engine* e, int layer, int kind, int* rows, int* cols);
+/* Copy a tensor to host memory: q (quants or f32 values) and s (scales; NULL for vectors). */
+int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s);
+/* Copy an engine buffer to host: 0 x [2, 2H], 1 hid [3, H], 2 hlast [H], 3 DeltaNet state
+ * (current slot, all visits), 4 conv state (current slot), 5 MTP residual [2, 2H]. */
+int snl_buffer_read(snl_engine* e, int id, void* out, size_t bytes);
+size_t snl_buffer_size(const snl_engine* e, int id);
+
+/* ---- kernel-level entry points (device pointers; `stream` is a hipStream_t or NULL) ------ */
+
+/* y[m*y_stride + n] = sum_k x[m*x_stride + k] * W[n, k], M in 1..4 (matmul.wgsl matvec1/2).
+ * wq/ws: reference layout quants [N, K] (Q8) or [N, K/2] (Q4), f32 scales [N, K/32]. */
+int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K,
+             int x_stride, int y_stride, void* stream);
+
+/* One Gated DeltaNet step over M = 1..4 tokens (linear.wgsl conv + delta).  conv_state and
+ * state hold three slots each ([3][3, conv_dim] and [3][n_v, 128, 128]); the call reads
+ * slot s_in, writes slot s_out and, if ckpt > 0, the state after token ckpt-1 to slot s_ck. */
+int snl_deltanet(const float* proj, int proj_stride, const float* lw, float* conv_state, float* state, float* out,
+                 int conv_dim, int n_k, int n_v, float eps, int M, int ckpt, int s_in, int s_out, int s_ck,
+                 void* stream);
+
+/* Gated attention for M = 1, 2 or 4 tokens at cache positions pos0..pos0+M-1
+ * (attention.wgsl prep + attend + combine).  rpos: host [M][3] rotary positions.
+ * partial: device scratch of M * n_heads * ceil(ctx/128) * 258 floats. */
+int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kcache, uint16_t* vcache,
+                  const float* norms, float* out, float* partial, int n_heads, int n_kv, int rot_dim,
+                  float rope_theta, float eps, const int32_t* mrope_section, int ctx, int M, int pos0,
+                  const uint32_t* rpos, void* stream);
+
+/* Greedy pick of `rows` device logits rows of length V into device picks_out. */
+int snl_pick_rows(const float* logits, int V, int rows, snl_pick* picks_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SNL_H */

@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
         if not os.path.exists(path):
             raise RuntimeError(f"{path} is missing: run `make -C oracle` (or __graft_entry__.build())")
         L = ctypes.CDLL(path)
+        L.orc_threads.restype = ctypes.c_int
         L.orc_stream_key.restype = ctypes.c_uint64
         L.orc_stream_key.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         L.orc_randn.restype = ctypes.c_float
@@ -104,6 +105,10 @@ def _p(a: np.ndarray, t):
 
 def f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def threads() -> int:
+    return int(lib().orc_threads())
 
 
 # ---------------------------------------------------------------- generator / quant

@@ -24,6 +24,19 @@
 
 #define ORC_API __attribute__((visibility("default")))
 
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* Threads the OpenMP loops of this file use. */
+ORC_API int orc_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
 /* ------------------------------------------------------------------------ */
 /* Seeded generator shared with the device-side initialiser.                 */
 /* splitmix64 (Vigna) as a counter-based hash; normals from an Irwin-Hall    */

@@ -1,0 +1,1188 @@
+// The decode engine behind the C ABI: device-resident weights, KV caches and recurrent
+// state, the per-visit op sequence of the reference's Engine, and one captured hipGraph
+// per pass shape (forward M=1/M=2 with 0..2 logit rows and optional checkpoint, MTP head
+// M=1/M=2 with or without a draft).  Mirrors src/engine.rs (op graph :383-493, MTP
+// :495-580 and :713-774, forward_mm :801-936, rollback/snapshot/restore/reset :646-697)
+// and the greedy loop of src/worker.rs:123-255.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "../../include/snl.h"
+#include "kernels.h"
+
+namespace snl {
+
+int device_error(hipError_t e, const char* what) {
+    (void)e;
+    (void)what;
+    return SNL_EDEVICE;
+}
+
+namespace {
+
+constexpr int kSnapshots = 4;
+constexpr int kLogitRows = 2;
+// Token rows per captured pass.  The kernels take up to SNL_MAX_M; passes use 1 or 2.
+constexpr int kMaxM = 2;
+
+// Tensor kinds of the seeded initialiser: stream id = ((layer + 1) << 8) | kind for layer
+// tensors (layer 0xFFF is the MTP head), kind alone for the globals.
+enum Kind {
+    K_EMBED = 1, K_LM_HEAD = 2, K_NORM = 3,
+    K_IN_LN = 1, K_POST_LN = 2, K_QK_NORM = 3, K_LIN = 4, K_QKV = 5, K_O_PROJ = 6, K_IN_PROJ = 7,
+    K_OUT_PROJ = 8, K_GATE_UP = 9, K_DOWN = 10, K_MHC_ATTN = 11, K_MHC_FFN = 12,
+    K_FC_E = 20, K_FC_H = 21, K_NORM_E = 22, K_NORM_H = 23, K_MTP_NORM = 24
+};
+constexpr int kMtpLayer = 0xFFF;
+
+uint64_t host_smix(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+uint64_t stream_key(uint64_t seed, int layer, int kind) {
+    uint64_t stream = layer < 0 ? (uint64_t)kind : (((uint64_t)(layer + 1) << 8) | (uint64_t)kind);
+    return host_smix(seed ^ host_smix(stream * 0xD1B54A32D192ED03ull));
+}
+
+struct QW {
+    void* q = nullptr;
+    float* s = nullptr;
+    int rows = 0, cols = 0, quant = 0;
+};
+
+struct Vec {
+    float* p = nullptr;
+    int n = 0;
+};
+
+struct Layer {
+    bool full = false;
+    Vec in_ln, post_ln, small, mhc_attn, mhc_ffn;
+    QW mix_in, mix_out, gate_up, down;
+};
+
+std::string g_create_error;
+
+}  // namespace
+}  // namespace snl
+
+using namespace snl;
+
+struct snl_engine {
+    snl_config cfg{};
+    int ctx = 0, quant = 0;
+    uint64_t seed = 0;
+    hipStream_t stream = nullptr;
+    std::vector<void*> allocs;
+
+    QW embed, lm_head;
+    Vec final_norm;
+    std::vector<Layer> layers;
+    QW fc_e, fc_h, m_qkv, m_o, m_gate_up, m_down;
+    Vec norm_e, norm_h, m_norm, m_in_ln, m_post_ln, m_qk_norm;
+
+    std::vector<int> plan;
+    int n_full = 0, n_lin = 0;
+    int h = 0, q_dim = 0, kv_dim = 0, conv_dim = 0, lin_proj_rows = 0, attn_proj_rows = 0, lin_value_dim = 0;
+
+    float *x = nullptr, *xn = nullptr, *proj = nullptr, *act = nullptr, *attn_out = nullptr, *qbuf = nullptr;
+    float *coef = nullptr, *mhc_raw = nullptr, *partial = nullptr, *logits = nullptr, *hid = nullptr,
+          *hlast = nullptr;
+    float *mx = nullptr, *hn = nullptr, *m_logits = nullptr;
+    uint16_t *kcache = nullptr, *vcache = nullptr, *m_kc = nullptr, *m_vc = nullptr;
+    float *lin_state = nullptr, *conv_state = nullptr;
+    size_t state_floats = 0, conv_floats = 0;  // per visit
+    float *snap_lin[kSnapshots] = {}, *snap_conv[kSnapshots] = {}, *snap_h[kSnapshots] = {};
+    float* pick_scratch = nullptr;
+    Pick *d_picks = nullptr, *d_mpick = nullptr;
+    Pick* h_picks = nullptr;  // pinned, 3 entries: 2 forward rows + 1 draft
+    StepDev *d_step = nullptr, *d_mstep = nullptr, *h_step = nullptr;  // h_step: pinned, 2 records
+
+    int cur = 0, ck_slot = -1;
+    int pos = 0, hid_rows = 0;
+    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
+    std::string err;
+
+    // Per-op timing of an eagerly launched pass (the reference's SENSENOVA_PROFILE mode,
+    // src/engine.rs:859-886, with device timestamps instead of host wall clock).
+    struct Mark {
+        const char* name;
+        double bytes;
+        hipEvent_t ev;
+    };
+    std::vector<Mark>* marks = nullptr;
+    void mark(const char* name, double bytes) {
+        if (!marks) return;
+        hipEvent_t ev = nullptr;
+        hipEventCreate(&ev);
+        hipEventRecord(ev, stream);
+        marks->push_back({name, bytes, ev});
+    }
+    // Algorithmic HBM bytes of one GEMV launch: quants + f32 scales + the M input rows +
+    // the output (read and written back for the residual epilogues).
+    static double gemv_bytes(const QW& w, int M, int epi, int inter) {
+        const double n = w.rows, k = w.cols;
+        double b = n * k * (w.quant == 0 ? 1.0 : 0.5) + n * (k / 32) * 4 + (double)M * k * 4;
+        if (epi == GEMV_STORE) b += (double)M * n * 4;
+        else if (epi == GEMV_ADD) b += 2.0 * M * n * 4;
+        else if (epi == GEMV_MHC) b += 4.0 * M * n * 4;
+        else b += (double)M * inter * 4;
+        return b;
+    }
+
+    int fail(int code, const char* fmt, ...) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        err = buf;
+        return code;
+    }
+
+    template <class T>
+    int dalloc(T** p, size_t count) {
+        void* v = nullptr;
+        if (hipMalloc(&v, count * sizeof(T) > 0 ? count * sizeof(T) : 16) != hipSuccess) {
+            *p = nullptr;
+            return fail(SNL_ENOMEM, "hipMalloc of %zu bytes failed", count * sizeof(T));
+        }
+        allocs.push_back(v);
+        *p = static_cast<T*>(v);
+        return SNL_OK;
+    }
+
+    int gen_q(QW& w, int layer, int kind, int rows, int cols, int qt) {
+        w.rows = rows;
+        w.cols = cols;
+        w.quant = qt;
+        const size_t n = (size_t)rows * cols;
+        uint8_t* q;
+        int rc = dalloc(&q, qt == 0 ? n : n / 2);
+        if (rc) return rc;
+        w.q = q;
+        if ((rc = dalloc(&w.s, n / 32))) return rc;
+        if (launch_gen_matrix(stream_key(seed, layer, kind), rows, cols, 0.02f, qt, w.q, w.s, stream))
+            return fail(SNL_EDEVICE, "weight init launch failed");
+        return SNL_OK;
+    }
+
+    int gen_v(Vec& v, int layer, int kind, int n, int vkind, float stdv, int aux0 = 0, int aux1 = 0) {
+        v.n = n;
+        int rc = dalloc(&v.p, n);
+        if (rc) return rc;
+        if (launch_gen_vector(stream_key(seed, layer, kind), n, vkind, stdv, aux0, aux1, v.p, stream))
+            return fail(SNL_EDEVICE, "vector init launch failed");
+        return SNL_OK;
+    }
+
+    bool is_mhc(int l) const { return cfg.mhc_streams > 0 && cfg.mhc_start <= l && l < cfg.mhc_end; }
+
+    int init();
+    int record_forward(int M, int rows, int ckpt);
+    int record_mtp(int M, int draft);
+    int run(int kind, int M, int a, int b);
+    int gemv(const char* name, const QW& w, const float* xin, int x_stride, float* y, int y_stride, int M, int epi,
+             int merge_mode = 0) {
+        mark(name, gemv_bytes(w, M, epi, cfg.intermediate));
+        GemvArgs g{};
+        g.wq = w.q;
+        g.ws = w.s;
+        g.x = xin;
+        g.x_stride = x_stride;
+        g.y = y;
+        g.y_stride = y_stride;
+        g.N = w.rows;
+        g.K = w.cols;
+        g.epi = epi;
+        g.coef = coef;
+        g.merge_mode = merge_mode;
+        g.h = h;
+        g.inter = cfg.intermediate;
+        return launch_gemv(g, w.quant, M, stream);
+    }
+    int norm(const float* xin, int x_stride, const int32_t* row_base, int mode, const float* w, float* out,
+             int first, int count) {
+        NormArgs a{};
+        a.x = xin;
+        a.x_stride = x_stride;
+        a.row_base = row_base;
+        a.coef = coef;
+        a.w = w;
+        a.out = out;
+        a.out_stride = h;
+        a.h = h;
+        a.mode = mode;
+        a.first = first;
+        a.count = count;
+        a.eps = cfg.eps;
+        a.one = 1.0f;
+        mark("norm", 0.0);
+        return launch_branch_norm(a, stream);
+    }
+    AttnArgs attn_args(const StepDev* st, uint16_t* kc, uint16_t* vc, const float* norms) const {
+        AttnArgs a{};
+        a.proj = proj;
+        a.proj_stride = attn_proj_rows;
+        a.qbuf = qbuf;
+        a.kcache = kc;
+        a.vcache = vc;
+        a.norms = norms;
+        a.out = attn_out;
+        a.partial = partial;
+        a.n_heads = cfg.n_heads;
+        a.n_kv = cfg.n_kv_heads;
+        a.rot_dim = cfg.rot_dim;
+        a.rope_theta = cfg.rope_theta;
+        a.eps = cfg.eps;
+        a.scale = 1.0f / sqrtf((float)cfg.head_dim);
+        a.mrope = ((uint32_t)(3 * cfg.mrope_section[1]) << 16) | (uint32_t)(3 * cfg.mrope_section[2]);
+        a.ctx = ctx;
+        a.step = st;
+        return a;
+    }
+};
+
+// config.rs:195-240
+static const char* validate(const snl_config* c) {
+    if (c->head_dim != 256) return "head_dim must be 256";
+    if (c->lin_k_dim != 128 || c->lin_v_dim != 128) return "linear head dims must be 128";
+    if (c->conv_kernel != 4) return "linear conv kernel must be 4";
+    if (c->hidden % 256 != 0 || c->hidden > 8192) return "hidden size must be a multiple of 256 (at most 8192)";
+    if (c->n_layers < 1 || c->n_layers > 64) return "layer count must be 1..64";
+    if (c->n_heads != 4 * c->n_kv_heads) return "attention must have 4 query heads per KV head";
+    if (c->lin_k_heads < 1 || c->lin_v_heads % c->lin_k_heads != 0)
+        return "linear value heads must be a multiple of key heads";
+    if (c->rot_dim % 2 != 0 || c->rot_dim > c->head_dim || c->rot_dim < 2) return "invalid rotary dim";
+    if (c->mrope_section[0] + c->mrope_section[1] + c->mrope_section[2] != c->rot_dim / 2)
+        return "M-RoPE sections must cover the rotary dims";
+    if (!(c->loop_start < c->loop_end && c->loop_end <= c->n_layers && c->loop_count >= 1)) return "invalid loop range";
+    if (c->intermediate % 32 != 0 || c->vocab < 2) return "invalid intermediate size or vocab";
+    if (c->mhc_streams != 0) {
+        if (c->mhc_streams != 2) return "only 2 mHC streams are supported";
+        const int s = c->mhc_start, e = c->mhc_end;
+        const bool ok = (0 <= s && e <= c->loop_start) || (c->loop_start <= s && e <= c->loop_end) ||
+                        (c->loop_end <= s && e <= c->n_layers);
+        if (!ok || s >= e) return "mHC range crosses a loop boundary";
+    }
+    if (c->n_eos < 0 || c->n_eos > 4) return "at most 4 EOS ids";
+    return nullptr;
+}
+
+int snl_engine::init() {
+    const snl_config& c = cfg;
+    h = c.hidden;
+    q_dim = c.n_heads * c.head_dim;
+    kv_dim = c.n_kv_heads * c.head_dim;
+    lin_value_dim = c.lin_v_heads * c.lin_v_dim;
+    conv_dim = 2 * c.lin_k_heads * c.lin_k_dim + lin_value_dim;
+    lin_proj_rows = conv_dim + lin_value_dim + 2 * c.lin_v_heads;
+    attn_proj_rows = 2 * q_dim + 2 * kv_dim;
+    for (int i = 0; i < c.loop_start; ++i) plan.push_back(i);
+    for (int r = 0; r < c.loop_count; ++r)
+        for (int i = c.loop_start; i < c.loop_end; ++i) plan.push_back(i);
+    for (int i = c.loop_end; i < c.n_layers; ++i) plan.push_back(i);
+    for (int l : plan) (c.full_attention[l] ? n_full : n_lin)++;
+
+    if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess)
+        return fail(SNL_EDEVICE, "hipStreamCreate failed");
+    int rc;
+    // ---- weights (convert.rs:228-311 layout; seeded values) ----
+    if ((rc = gen_q(embed, -1, K_EMBED, c.vocab, h, 0))) return rc;
+    if ((rc = gen_q(lm_head, -1, K_LM_HEAD, c.vocab, h, 0))) return rc;
+    if ((rc = gen_v(final_norm, -1, K_NORM, h, 0, 0.1f))) return rc;
+    layers.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; ++l) {
+        Layer& L = layers[l];
+        L.full = c.full_attention[l] != 0;
+        if ((rc = gen_v(L.in_ln, l, K_IN_LN, h, 0, 0.1f))) return rc;
+        if ((rc = gen_v(L.post_ln, l, K_POST_LN, h, 0, 0.1f))) return rc;
+        if (L.full) {
+            if ((rc = gen_v(L.small, l, K_QK_NORM, 2 * c.head_dim, 0, 0.1f))) return rc;
+            if ((rc = gen_q(L.mix_in, l, K_QKV, attn_proj_rows, h, quant))) return rc;
+            if ((rc = gen_q(L.mix_out, l, K_O_PROJ, h, q_dim, quant))) return rc;
+        } else {
+            const int n = conv_dim * 4 + 2 * c.lin_v_heads + c.lin_v_dim;
+            if ((rc = gen_v(L.small, l, K_LIN, n, 2, 0.0f, conv_dim, c.lin_v_heads))) return rc;
+            if ((rc = gen_q(L.mix_in, l, K_IN_PROJ, lin_proj_rows, h, 0))) return rc;
+            if ((rc = gen_q(L.mix_out, l, K_OUT_PROJ, h, lin_value_dim, quant))) return rc;
+        }
+        if ((rc = gen_q(L.gate_up, l, K_GATE_UP, 2 * c.intermediate, h, quant))) return rc;
+        if ((rc = gen_q(L.down, l, K_DOWN, h, c.intermediate, quant))) return rc;
+        if (is_mhc(l)) {
+            if ((rc = gen_v(L.mhc_attn, l, K_MHC_ATTN, 16 * h + 8, 3, 0.0f, h))) return rc;
+            if ((rc = gen_v(L.mhc_ffn, l, K_MHC_FFN, 16 * h + 8, 3, 0.0f, h))) return rc;
+        }
+    }
+    if (c.has_mtp) {
+        const int L = kMtpLayer;
+        if ((rc = gen_q(fc_e, L, K_FC_E, h, h, 0))) return rc;
+        if ((rc = gen_q(fc_h, L, K_FC_H, h, h, 0))) return rc;
+        if ((rc = gen_q(m_qkv, L, K_QKV, attn_proj_rows, h, 0))) return rc;
+        if ((rc = gen_q(m_o, L, K_O_PROJ, h, q_dim, 0))) return rc;
+        if ((rc = gen_q(m_gate_up, L, K_GATE_UP, 2 * c.intermediate, h, 0))) return rc;
+        if ((rc = gen_q(m_down, L, K_DOWN, h, c.intermediate, 0))) return rc;
+        if ((rc = gen_v(norm_e, L, K_NORM_E, h, 0, 0.1f))) return rc;
+        if ((rc = gen_v(norm_h, L, K_NORM_H, h, 0, 0.1f))) return rc;
+        if ((rc = gen_v(m_norm, L, K_MTP_NORM, h, 0, 0.1f))) return rc;
+        if ((rc = gen_v(m_in_ln, L, K_IN_LN, h, 0, 0.1f))) return rc;
+        if ((rc = gen_v(m_post_ln, L, K_POST_LN, h, 0, 0.1f))) return rc;
+        if ((rc = gen_v(m_qk_norm, L, K_QK_NORM, 2 * c.head_dim, 0, 0.1f))) return rc;
+    }
+
+    // ---- activations (src/engine.rs:244-256), sized for kMaxM rows ----
+    const int proj_w = std::max(std::max(2 * c.intermediate, lin_proj_rows), attn_proj_rows);
+    const int act_w = std::max(c.intermediate, conv_dim);
+    const int attn_w = std::max(q_dim, lin_value_dim);
+    const int M = SNL_MAX_M;
+    const int parts_max = (ctx + 127) / 128;
+    if ((rc = dalloc(&x, (size_t)M * 2 * h)) || (rc = dalloc(&xn, (size_t)M * h)) ||
+        (rc = dalloc(&proj, (size_t)M * proj_w)) || (rc = dalloc(&act, (size_t)M * act_w)) ||
+        (rc = dalloc(&attn_out, (size_t)M * attn_w)) || (rc = dalloc(&qbuf, (size_t)M * q_dim)) ||
+        (rc = dalloc(&coef, (size_t)M * 8)) || (rc = dalloc(&mhc_raw, (size_t)M * 9)) ||
+        (rc = dalloc(&partial, (size_t)M * c.n_heads * parts_max * (c.head_dim + 2))) ||
+        (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)(M + 1) * h)) ||
+        (rc = dalloc(&hlast, (size_t)h)) || (rc = dalloc(&mx, (size_t)M * 2 * h)) ||
+        (rc = dalloc(&hn, (size_t)M * h)) || (rc = dalloc(&m_logits, (size_t)c.vocab)) ||
+        (rc = dalloc(&pick_scratch, pick_scratch_floats(c.vocab, kLogitRows))) || (rc = dalloc(&d_picks, 2)) ||
+        (rc = dalloc(&d_mpick, 1)) || (rc = dalloc(&d_step, 1)) || (rc = dalloc(&d_mstep, 1)))
+        return rc;
+    // ---- caches and recurrent state ----
+    const size_t kvn = (size_t)ctx * kv_dim;
+    if ((rc = dalloc(&kcache, kvn * std::max(n_full, 1))) || (rc = dalloc(&vcache, kvn * std::max(n_full, 1))) ||
+        (rc = dalloc(&m_kc, c.has_mtp ? kvn : 1)) || (rc = dalloc(&m_vc, c.has_mtp ? kvn : 1)))
+        return rc;
+    state_floats = (size_t)c.lin_v_heads * c.lin_k_dim * c.lin_v_dim;
+    conv_floats = (size_t)3 * conv_dim;
+    const size_t nl = std::max(n_lin, 1);
+    if ((rc = dalloc(&lin_state, 3 * nl * state_floats)) || (rc = dalloc(&conv_state, 3 * nl * conv_floats)))
+        return rc;
+    for (int i = 0; i < kSnapshots; ++i)
+        if ((rc = dalloc(&snap_lin[i], nl * state_floats)) || (rc = dalloc(&snap_conv[i], nl * conv_floats)) ||
+            (rc = dalloc(&snap_h[i], (size_t)h)))
+            return rc;
+    if (hipHostMalloc((void**)&h_picks, 3 * sizeof(Pick), hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void**)&h_step, 2 * sizeof(StepDev), hipHostMallocDefault) != hipSuccess)
+        return fail(SNL_ENOMEM, "pinned host allocation failed");
+    // zero everything a pass may read before writing (the reference's buffers start zeroed)
+    if (hipMemsetAsync(x, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
+        hipMemsetAsync(mx, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
+        hipMemsetAsync(hid, 0, sizeof(float) * (M + 1) * h, stream) != hipSuccess ||
+        hipMemsetAsync(hlast, 0, sizeof(float) * h, stream) != hipSuccess ||
+        hipMemsetAsync(lin_state, 0, sizeof(float) * 3 * nl * state_floats, stream) != hipSuccess ||
+        hipMemsetAsync(conv_state, 0, sizeof(float) * 3 * nl * conv_floats, stream) != hipSuccess ||
+        hipMemsetAsync(kcache, 0, 2 * kvn * std::max(n_full, 1), stream) != hipSuccess ||
+        hipMemsetAsync(vcache, 0, 2 * kvn * std::max(n_full, 1), stream) != hipSuccess ||
+        hipMemsetAsync(m_kc, 0, 2 * (c.has_mtp ? kvn : 1), stream) != hipSuccess ||
+        hipMemsetAsync(m_vc, 0, 2 * (c.has_mtp ? kvn : 1), stream) != hipSuccess)
+        return fail(SNL_EDEVICE, "hipMemset failed");
+    if (hipStreamSynchronize(stream) != hipSuccess) return fail(SNL_EDEVICE, "weight initialisation failed");
+    return SNL_OK;
+}
+
+// One decoder pass over the execution plan (src/engine.rs:389-493), M token rows, then the
+// final norm into hid rows 1..M and `rows` rows of LM head + greedy pick.
+int snl_engine::record_forward(int M, int rows, int ckpt) {
+    // the checkpoint request itself travels in the step record
+    const snl_config& c = cfg;
+    int rc = 0;
+    mark("embed", 0.0);
+    rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream);
+    mark("copy", 0.0);
+    rc |= launch_copy(hid, hlast, h, stream);  // row 0 = hidden of the token before this step
+    int fslot = 0, lslot = 0;
+    const size_t kvn = (size_t)ctx * kv_dim;
+    const size_t nl = std::max(n_lin, 1);
+    for (int li : plan) {
+        const Layer& L = layers[li];
+        const bool mhc = is_mhc(li);
+        if (mhc && li == c.mhc_start) {
+            mark("expand", 0.0);
+            rc |= launch_expand(x, h, M, stream);
+        }
+        if (mhc) {
+            mark("mhc", 0.0);
+            rc |= launch_mhc(x, L.mhc_attn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
+        }
+        rc |= norm(x, 2 * h, nullptr, mhc ? 1 : 0, L.in_ln.p, xn, 0, M);
+        if (L.full) {
+            rc |= gemv("gemv_qkv", L.mix_in, xn, h, proj, attn_proj_rows, M, GEMV_STORE);
+            AttnArgs a = attn_args(d_step, kcache + kvn * fslot, vcache + kvn * fslot, L.small.p);
+            mark("attention", 0.0);
+            rc |= launch_attention(a, M, stream);
+            rc |= gemv("gemv_o", L.mix_out, attn_out, q_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, 1);
+            ++fslot;
+        } else {
+            rc |= gemv("gemv_in_proj", L.mix_in, xn, h, proj, lin_proj_rows, M, GEMV_STORE);
+            DeltaArgs d{};
+            d.proj = proj;
+            d.proj_stride = lin_proj_rows;
+            d.lw = L.small.p;
+            d.conv_state = conv_state + conv_floats * lslot;
+            d.state = lin_state + state_floats * lslot;
+            d.conv_slot = nl * conv_floats;
+            d.state_slot = nl * state_floats;
+            d.out = attn_out;
+            d.conv_dim = conv_dim;
+            d.n_k = c.lin_k_heads;
+            d.n_v = c.lin_v_heads;
+            d.eps = c.eps;
+            d.step = d_step;
+            mark("deltanet", 2.0 * 4.0 * (double)state_floats + (ckpt ? 4.0 * (double)state_floats : 0.0));
+            rc |= launch_deltanet(d, M, stream);
+            rc |= gemv("gemv_out_proj", L.mix_out, attn_out, lin_value_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD,
+                       1);
+            ++lslot;
+        }
+        if (mhc) {
+            mark("mhc", 0.0);
+            rc |= launch_mhc(x, L.mhc_ffn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
+        }
+        rc |= norm(x, 2 * h, nullptr, mhc ? 1 : 0, L.post_ln.p, xn, 0, M);
+        rc |= gemv("gemv_gate_up", L.gate_up, xn, h, act, c.intermediate, M, GEMV_SWIGLU);
+        const int mode = !mhc ? 0 : (li + 1 == c.mhc_end ? 2 : 1);
+        rc |= gemv("gemv_down", L.down, act, c.intermediate, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, mode);
+    }
+    rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M);
+    if (rows > 0) {
+        rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
+        mark("pick", 0.0);
+        rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
+    }
+    mark("copy", 0.0);
+    rc |= launch_copy(hlast, hid + (size_t)M * h, h, stream);
+    mark("end", 0.0);
+    return rc ? SNL_EDEVICE : SNL_OK;
+}
+
+// The MTP head (src/engine.rs:549-570, :736-761) over M pairs.
+int snl_engine::record_mtp(int M, int draft) {
+    const snl_config& c = cfg;
+    int rc = 0;
+    rc |= launch_embed(d_mstep, (const int8_t*)embed.q, embed.s, c.vocab, h, mx, M, stream);
+    rc |= norm(mx, 2 * h, nullptr, 0, norm_e.p, xn, 0, M);
+    rc |= norm(hid, h, &d_mstep->r0, 0, norm_h.p, hn, 0, M);
+    rc |= gemv("gemv_fc_e", fc_e, xn, h, mx, 2 * h, M, GEMV_STORE);
+    rc |= gemv("gemv_fc_h", fc_h, hn, h, mx, 2 * h, M, GEMV_ADD);
+    rc |= norm(mx, 2 * h, nullptr, 0, m_in_ln.p, xn, 0, M);
+    rc |= gemv("gemv_mtp_qkv", m_qkv, xn, h, proj, attn_proj_rows, M, GEMV_STORE);
+    AttnArgs a = attn_args(d_mstep, m_kc, m_vc, m_qk_norm.p);
+    rc |= launch_attention(a, M, stream);
+    rc |= gemv("gemv_mtp_o", m_o, attn_out, q_dim, mx, 2 * h, M, GEMV_ADD);
+    rc |= norm(mx, 2 * h, nullptr, 0, m_post_ln.p, xn, 0, M);
+    rc |= gemv("gemv_mtp_gate_up", m_gate_up, xn, h, act, c.intermediate, M, GEMV_SWIGLU);
+    rc |= gemv("gemv_mtp_down", m_down, act, c.intermediate, mx, 2 * h, M, GEMV_ADD);
+    if (draft) {
+        rc |= norm(mx, 2 * h, nullptr, 0, m_norm.p, xn, M - 1, 1);
+        rc |= gemv("gemv_lm_head", lm_head, xn, h, m_logits, c.vocab, 1, GEMV_STORE);
+        rc |= launch_pick(m_logits, c.vocab, 1, pick_scratch, d_mpick, stream);
+    }
+    return rc ? SNL_EDEVICE : SNL_OK;
+}
+
+// Replay (capturing on first use) the pass (kind, M, a, b): kind 0 forward (a = rows,
+// b = ckpt), kind 1 MTP (a = draft).  The step record is copied first.
+int snl_engine::run(int kind, int M, int a, int b) {
+    StepDev* hs = h_step + kind;
+    if (hipMemcpyAsync(kind == 0 ? d_step : d_mstep, hs, sizeof(StepDev), hipMemcpyHostToDevice, stream) !=
+        hipSuccess)
+        return fail(SNL_EDEVICE, "step upload failed");
+    auto key = std::make_tuple(kind, M, a, b);
+    auto it = graphs.find(key);
+    if (it == graphs.end()) {
+        hipGraph_t g = nullptr;
+        if (hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
+            return fail(SNL_EDEVICE, "hipStreamBeginCapture failed");
+        int rc = kind == 0 ? record_forward(M, a, b) : record_mtp(M, a);
+        hipError_t ce = hipStreamEndCapture(stream, &g);
+        if (rc || ce != hipSuccess) {
+            if (g) hipGraphDestroy(g);
+            return fail(SNL_EDEVICE, "pass capture failed (kind %d, M %d)", kind, M);
+        }
+        hipGraphExec_t ex = nullptr;
+        hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+        hipGraphDestroy(g);
+        if (ie != hipSuccess) return fail(SNL_EDEVICE, "hipGraphInstantiate failed");
+        it = graphs.emplace(key, ex).first;
+    }
+    if (hipGraphLaunch(it->second, stream) != hipSuccess) return fail(SNL_EDEVICE, "hipGraphLaunch failed");
+    return SNL_OK;
+}
+
+extern "C" {
+
+const char* snl_create_error(void) { return g_create_error.c_str(); }
+
+int snl_engine_create(const snl_config* cfg, uint64_t seed, int quant, int ctx, snl_engine** out) {
+    if (!out) return SNL_EARG;
+    *out = nullptr;
+    if (!cfg) {
+        g_create_error = "null config";
+        return SNL_EARG;
+    }
+    if (const char* why = validate(cfg)) {
+        g_create_error = std::string("unsupported model configuration: ") + why;
+        return SNL_EARG;
+    }
+    if ((quant != 0 && quant != 1) || ctx < 2 || ctx > (1 << 22)) {
+        g_create_error = "bad quant or ctx";
+        return SNL_EARG;
+    }
+    snl_engine* e = new snl_engine();
+    e->cfg = *cfg;
+    e->ctx = ctx;
+    e->quant = quant;
+    e->seed = seed;
+    int rc = e->init();
+    if (rc) {
+        g_create_error = e->err;
+        snl_engine_destroy(e);
+        return rc;
+    }
+    *out = e;
+    return SNL_OK;
+}
+
+void snl_engine_destroy(snl_engine* e) {
+    if (!e) return;
+    if (e->stream) hipStreamSynchronize(e->stream);
+    for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+    for (void* p : e->allocs) hipFree(p);
+    if (e->h_picks) hipHostFree(e->h_picks);
+    if (e->h_step) hipHostFree(e->h_step);
+    if (e->stream) hipStreamDestroy(e->stream);
+    delete e;
+}
+
+const char* snl_last_error(const snl_engine* e) { return e ? e->err.c_str() : ""; }
+
+int snl_pos(const snl_engine* e) { return e->pos; }
+int snl_ctx(const snl_engine* e) { return e->ctx; }
+int snl_hid_rows(const snl_engine* e) { return e->hid_rows; }
+int snl_has_mtp(const snl_engine* e) { return e->cfg.has_mtp != 0; }
+int snl_prefill_chunk(const snl_engine* e) {
+    (void)e;
+    return kMaxM;
+}
+
+int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows, int ckpt,
+                float* logits_out, snl_pick* picks_out) {
+    if (!e) return SNL_EARG;
+    e->err.clear();
+    // src/engine.rs:810-821
+    if (logit_rows < 0 || logit_rows > kLogitRows || (ckpt && n != 2))
+        return e->fail(SNL_EARG, "forward: unsupported logits or checkpoint request");
+    if (n <= 0 || !tokens) return e->fail(SNL_EARG, "forward called with no tokens");
+    if (e->pos + n > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + n, e->ctx);
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tokens[i]);
+    // chunks of at most kMaxM rows; the last chunk holds the logit rows
+    int last = n <= kMaxM ? n : std::max(logit_rows, n % kMaxM ? n % kMaxM : kMaxM);
+    int rows = 0;
+    for (int c0 = 0; c0 < n;) {
+        const int rem = n - c0;
+        const int m = rem == last ? last : std::min(kMaxM, rem - last);
+        const bool is_last = c0 + m == n;
+        rows = is_last ? std::min(logit_rows, m) : 0;
+        StepDev& st = e->h_step[0];
+        memset(&st, 0, sizeof st);
+        st.pos0 = e->pos;
+        st.m = m;
+        st.ckpt = ckpt ? 1 : 0;
+        st.s_in = e->cur;
+        st.s_ck = (e->cur + 1) % 3;
+        st.s_out = ckpt ? (e->cur + 2) % 3 : (e->cur + 1) % 3;
+        for (int i = 0; i < m; ++i) {
+            st.tokens[i] = tokens[c0 + i];
+            for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[(c0 + i) * 3 + k] : (uint32_t)(e->pos + i);
+            st.rpos[i][3] = 0;
+        }
+        int rc = e->run(0, m, rows, ckpt ? 1 : 0);
+        if (rc) return rc;
+        // the step record is reused by the next call: wait for this one
+        if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "forward failed on device");
+        e->ck_slot = ckpt ? st.s_ck : -1;
+        e->cur = st.s_out;
+        e->pos += m;
+        e->hid_rows = m;
+        c0 += m;
+    }
+    if (rows > 0) {
+        if (logits_out &&
+            hipMemcpy(logits_out, e->logits, sizeof(float) * rows * e->cfg.vocab, hipMemcpyDeviceToHost) != hipSuccess)
+            return e->fail(SNL_EDEVICE, "logits readback failed");
+        if (picks_out &&
+            hipMemcpy(picks_out, e->d_picks, sizeof(snl_pick) * rows, hipMemcpyDeviceToHost) != hipSuccess)
+            return e->fail(SNL_EDEVICE, "pick readback failed");
+    }
+    return SNL_OK;
+}
+
+int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows,
+                         int ckpt, snl_op_time* recs, int max_recs, int* n_recs) {
+    if (!e || !recs || !n_recs) return SNL_EARG;
+    e->err.clear();
+    *n_recs = 0;
+    if (logit_rows < 0 || logit_rows > kLogitRows || (ckpt && n != 2) || n <= 0 || n > kMaxM || !tokens)
+        return e->fail(SNL_EARG, "forward_profiled: one pass of 1..%d tokens", kMaxM);
+    if (e->pos + n > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + n, e->ctx);
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tokens[i]);
+    const int rows = std::min(logit_rows, n);
+    StepDev& st = e->h_step[0];
+    memset(&st, 0, sizeof st);
+    st.pos0 = e->pos;
+    st.m = n;
+    st.ckpt = ckpt ? 1 : 0;
+    st.s_in = e->cur;
+    st.s_ck = (e->cur + 1) % 3;
+    st.s_out = ckpt ? (e->cur + 2) % 3 : (e->cur + 1) % 3;
+    for (int i = 0; i < n; ++i) {
+        st.tokens[i] = tokens[i];
+        for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[i * 3 + k] : (uint32_t)(e->pos + i);
+    }
+    if (hipMemcpyAsync(e->d_step, &st, sizeof(StepDev), hipMemcpyHostToDevice, e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "step upload failed");
+    std::vector<snl_engine::Mark> marks;
+    marks.reserve(2048);
+    e->marks = &marks;
+    int rc = e->record_forward(n, rows, ckpt ? 1 : 0);
+    e->marks = nullptr;
+    hipError_t se = hipStreamSynchronize(e->stream);
+    int k = 0;
+    for (size_t i = 0; i + 1 < marks.size(); ++i) {
+        if (k < max_recs) {
+            float ms = 0.0f;
+            hipEventElapsedTime(&ms, marks[i].ev, marks[i + 1].ev);
+            snprintf(recs[k].name, sizeof recs[k].name, "%s", marks[i].name);
+            recs[k].bytes = marks[i].bytes;
+            recs[k].ms = ms;
+            ++k;
+        }
+    }
+    for (auto& m : marks) hipEventDestroy(m.ev);
+    *n_recs = k;
+    if (rc || se != hipSuccess) return e->fail(SNL_EDEVICE, "profiled pass failed");
+    e->ck_slot = ckpt ? st.s_ck : -1;
+    e->cur = st.s_out;
+    e->pos += n;
+    e->hid_rows = n;
+    return SNL_OK;
+}
+
+int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t* pos3, int slot0, int draft,
+            uint32_t* draft_out, snl_pick* pick_out, float* logits_out) {
+    if (!e) return SNL_EARG;
+    e->err.clear();
+    if (!e->cfg.has_mtp) return e->fail(SNL_ESTATE, "this model has no MTP head");
+    if (n <= 0 || !tokens || !pos3 || r0 < 0 || r0 + n > e->hid_rows + 1 || slot0 < 0 || slot0 + n > e->ctx)
+        return e->fail(SNL_EARG, "mtp: rows out of range");
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tokens[i]);
+    for (int c0 = 0; c0 < n; c0 += kMaxM) {
+        const int m = std::min(kMaxM, n - c0);
+        const bool last = c0 + m == n;
+        StepDev& st = e->h_step[1];
+        memset(&st, 0, sizeof st);
+        st.pos0 = slot0 + c0;
+        st.m = m;
+        st.r0 = r0 + c0;
+        for (int i = 0; i < m; ++i) {
+            st.tokens[i] = tokens[c0 + i];
+            for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3[(c0 + i) * 3 + k];
+        }
+        int rc = e->run(1, m, last && draft ? 1 : 0, 0);
+        if (rc) return rc;
+        if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "mtp failed on device");
+    }
+    if (draft) {
+        if (hipMemcpy(e->h_picks + 2, e->d_mpick, sizeof(Pick), hipMemcpyDeviceToHost) != hipSuccess)
+            return e->fail(SNL_EDEVICE, "draft readback failed");
+        if (draft_out) *draft_out = e->h_picks[2].token;
+        if (pick_out) memcpy(pick_out, e->h_picks + 2, sizeof(snl_pick));
+        if (logits_out &&
+            hipMemcpy(logits_out, e->m_logits, sizeof(float) * e->cfg.vocab, hipMemcpyDeviceToHost) != hipSuccess)
+            return e->fail(SNL_EDEVICE, "logits readback failed");
+    }
+    return SNL_OK;
+}
+
+int snl_rollback(snl_engine* e) {
+    if (!e) return SNL_EARG;
+    if (e->ck_slot < 0) return e->fail(SNL_ESTATE, "rollback without a checkpointed 2-token step");
+    e->cur = e->ck_slot;
+    e->ck_slot = -1;
+    if (launch_copy(e->hlast, e->hid + e->h, e->h, e->stream) || hipStreamSynchronize(e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "rollback failed");
+    e->pos -= 1;
+    e->hid_rows = 1;
+    return SNL_OK;
+}
+
+int snl_snapshot(snl_engine* e, int slot) {
+    if (!e || slot < 0 || slot >= kSnapshots) return SNL_EARG;
+    const size_t nl = std::max(e->n_lin, 1);
+    const size_t sb = nl * e->state_floats * 4, cb = nl * e->conv_floats * 4;
+    if (hipMemcpyAsync(e->snap_lin[slot], e->lin_state + (size_t)e->cur * nl * e->state_floats, sb,
+                       hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
+        hipMemcpyAsync(e->snap_conv[slot], e->conv_state + (size_t)e->cur * nl * e->conv_floats, cb,
+                       hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
+        hipMemcpyAsync(e->snap_h[slot], e->hlast, (size_t)e->h * 4, hipMemcpyDeviceToDevice, e->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "snapshot failed");
+    return SNL_OK;
+}
+
+int snl_restore(snl_engine* e, int slot, int pos) {
+    if (!e || slot < 0 || slot >= kSnapshots || pos < 0 || pos > e->ctx) return SNL_EARG;
+    const size_t nl = std::max(e->n_lin, 1);
+    const size_t sb = nl * e->state_floats * 4, cb = nl * e->conv_floats * 4;
+    if (hipMemcpyAsync(e->lin_state + (size_t)e->cur * nl * e->state_floats, e->snap_lin[slot], sb,
+                       hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
+        hipMemcpyAsync(e->conv_state + (size_t)e->cur * nl * e->conv_floats, e->snap_conv[slot], cb,
+                       hipMemcpyDeviceToDevice, e->stream) != hipSuccess ||
+        hipMemcpyAsync(e->hlast, e->snap_h[slot], (size_t)e->h * 4, hipMemcpyDeviceToDevice, e->stream) !=
+            hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "restore failed");
+    e->pos = pos;
+    e->hid_rows = 0;
+    e->ck_slot = -1;
+    return SNL_OK;
+}
+
+int snl_reset(snl_engine* e) {
+    if (!e) return SNL_EARG;
+    const size_t nl = std::max(e->n_lin, 1);
+    if (hipMemsetAsync(e->lin_state + (size_t)e->cur * nl * e->state_floats, 0, nl * e->state_floats * 4,
+                       e->stream) != hipSuccess ||
+        hipMemsetAsync(e->conv_state + (size_t)e->cur * nl * e->conv_floats, 0, nl * e->conv_floats * 4,
+                       e->stream) != hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "reset failed");
+    e->pos = 0;
+    e->hid_rows = 0;
+    e->ck_slot = -1;
+    e->err.clear();
+    return SNL_OK;
+}
+
+}  // extern "C"
+
+// Host-side state of the greedy MTP loop of Worker::run (src/worker.rs:182-255).
+struct snl_decoder {
+    snl_engine* e = nullptr;
+    bool spec = false;
+    uint32_t tok = 0;  // sampled, not yet emitted
+    float gap = 0.0f;
+    uint32_t rope = 0;
+    int mr0 = 0, mn = 1, mslot = 0;  // MTP input: (r0, tokens, positions, first cache slot)
+    uint32_t mtok[2] = {0, 0};
+    uint32_t mpos[6] = {0, 0, 0, 0, 0, 0};
+    snl_gen_stats st{};
+};
+
+extern "C" {
+
+int snl_decoder_create(snl_engine* e, const uint32_t* prompt, int n, int spec, snl_decoder** out) {
+    using clk = std::chrono::steady_clock;
+    if (!e || !prompt || !out) return SNL_EARG;
+    *out = nullptr;
+    if (n <= 0) return e->fail(SNL_EARG, "empty prompt");
+    if (n >= e->ctx) return e->fail(SNL_EARG, "prompt is %d tokens but the context size is %d", n, e->ctx);
+    int rc = snl_reset(e);
+    if (rc) return rc;
+    auto d = new snl_decoder();
+    d->e = e;
+    d->spec = spec && e->cfg.has_mtp;
+    auto t0 = clk::now();
+    std::vector<uint32_t> pos3((size_t)n * 3);
+    for (int i = 0; i < n; ++i) pos3[i * 3] = pos3[i * 3 + 1] = pos3[i * 3 + 2] = (uint32_t)i;
+    snl_pick picks[2];
+    const int chunk = snl_prefill_chunk(e);
+    // Worker::feed (src/worker.rs:291-323): forward a chunk, then catch the MTP cache up
+    for (int c0 = 0; c0 < n; c0 += chunk) {
+        const int c1 = std::min(c0 + chunk, n);
+        rc = snl_forward(e, prompt + c0, c1 - c0, pos3.data() + c0 * 3, c1 == n ? 1 : 0, 0, nullptr, picks);
+        const int r0 = c0 == 0;
+        if (!rc && d->spec && r0 < c1 - c0)
+            rc = snl_mtp(e, r0, prompt + c0 + r0, c1 - c0 - r0, pos3.data() + (c0 + r0 - 1) * 3, c0 + r0 - 1, 0,
+                         nullptr, nullptr, nullptr);
+        if (rc) {
+            delete d;
+            return rc;
+        }
+    }
+    d->st.prefill_s = std::chrono::duration<double>(clk::now() - t0).count();
+    d->rope = (uint32_t)n;
+    d->tok = picks[0].token;
+    d->gap = picks[0].top1 - picks[0].top2;
+    d->mr0 = e->hid_rows;
+    d->mn = 1;
+    d->mslot = n - 1;
+    d->mtok[0] = d->tok;
+    for (int k = 0; k < 3; ++k) d->mpos[k] = (uint32_t)(n - 1);
+    *out = d;
+    return SNL_OK;
+}
+
+void snl_decoder_destroy(snl_decoder* d) { delete d; }
+
+int snl_decoder_stats(const snl_decoder* d, snl_gen_stats* out) {
+    if (!d || !out) return SNL_EARG;
+    *out = d->st;
+    return SNL_OK;
+}
+
+int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out) {
+    using clk = std::chrono::steady_clock;
+    if (!d || !out || !n_out) return SNL_EARG;
+    snl_engine* e = d->e;
+    *n_out = 0;
+    auto ts = clk::now();
+    int rc;
+    // emit the pending token (Emit::push, src/worker.rs:346-381)
+    out[0] = d->tok;
+    if (gaps) gaps[0] = d->gap;
+    *n_out = 1;
+    d->st.generated++;
+    snl_pick picks[2];
+    if (!d->spec) {
+        uint32_t p1[3] = {d->rope, d->rope, d->rope};
+        if ((rc = snl_forward(e, &d->tok, 1, p1, 1, 0, nullptr, picks))) return rc;
+        d->rope += 1;
+        d->tok = picks[0].token;
+        d->gap = picks[0].top1 - picks[0].top2;
+        d->st.decode_s += std::chrono::duration<double>(clk::now() - ts).count();
+        return SNL_OK;
+    }
+    uint32_t draft = 0;
+    if ((rc = snl_mtp(e, d->mr0, d->mtok, d->mn, d->mpos, d->mslot, 1, &draft, nullptr, nullptr))) return rc;
+    auto tb = clk::now();
+    const int slot = e->pos;
+    const uint32_t rope = d->rope;
+    uint32_t pair[2] = {d->tok, draft};
+    uint32_t p2[6] = {rope, rope, rope, rope + 1, rope + 1, rope + 1};
+    if ((rc = snl_forward(e, pair, 2, p2, 2, 1, nullptr, picks))) return rc;
+    auto tc = clk::now();
+    d->st.draft_s += std::chrono::duration<double>(tb - ts).count();
+    d->st.verify_s += std::chrono::duration<double>(tc - tb).count();
+    d->st.drafted++;
+    // Sampler::verify, greedy (src/sampler.rs:63-66, :87-89)
+    const uint32_t next = picks[0].token;
+    if (next == draft) {
+        d->st.accepted++;
+        d->st.generated++;
+        out[1] = draft;
+        if (gaps) gaps[1] = picks[0].top1 - picks[0].top2;
+        *n_out = 2;
+        d->tok = picks[1].token;
+        d->gap = picks[1].top1 - picks[1].top2;
+        d->mr0 = 1;
+        d->mn = 2;
+        d->mtok[0] = draft;
+        d->mtok[1] = d->tok;
+        for (int k = 0; k < 3; ++k) {
+            d->mpos[k] = rope;
+            d->mpos[3 + k] = rope + 1;
+        }
+        d->rope = rope + 2;
+    } else {
+        if ((rc = snl_rollback(e))) return rc;
+        d->tok = next;
+        d->gap = picks[0].top1 - picks[0].top2;
+        d->mr0 = 1;
+        d->mn = 1;
+        d->mtok[0] = d->tok;
+        for (int k = 0; k < 3; ++k) d->mpos[k] = rope;
+        d->rope = rope + 1;
+    }
+    d->mslot = slot;
+    d->st.decode_s += std::chrono::duration<double>(clk::now() - ts).count();
+    return SNL_OK;
+}
+
+int snl_generate(snl_engine* e, const uint32_t* prompt, int n, int max_tokens, int spec, uint32_t* out, float* gaps,
+                 snl_gen_stats* stats) {
+    if (!e || !prompt || !out) return SNL_EARG;
+    if (n > 0 && max_tokens > e->ctx - n) max_tokens = e->ctx - n;
+    if (max_tokens <= 0) return e->fail(SNL_EARG, "max_tokens must be positive");
+    snl_decoder* d = nullptr;
+    int rc = snl_decoder_create(e, prompt, n, spec, &d);
+    if (rc) return rc;
+    auto is_eos = [&](uint32_t t) {
+        for (int k = 0; k < e->cfg.n_eos; ++k)
+            if (e->cfg.eos[k] == t) return true;
+        return false;
+    };
+    int generated = 0;
+    bool done = false;
+    while (!done) {
+        // A step emits the pending token and, after an accepted draft, the draft.  The
+        // reference stops before feeding a token that ends generation; so does this loop:
+        // the last step's extra work on a token past the limit is not observable.
+        if (generated + 1 >= max_tokens || is_eos(d->tok)) {
+            out[generated] = d->tok;
+            if (gaps) gaps[generated] = d->gap;
+            generated++;
+            d->st.generated++;
+            break;
+        }
+        uint32_t o[2];
+        float g[2];
+        int k = 0;
+        if ((rc = snl_decoder_step(d, o, g, &k))) break;
+        for (int i = 0; i < k && !done; ++i) {
+            out[generated] = o[i];
+            if (gaps) gaps[generated] = g[i];
+            generated++;
+            if (is_eos(o[i]) || generated >= max_tokens) done = true;
+        }
+    }
+    if (stats) {
+        *stats = d->st;
+        stats->generated = generated;
+    }
+    snl_decoder_destroy(d);
+    return rc;
+}
+
+// ---- inspection ----
+static const void* find_tensor(const snl_engine* e, int layer, int kind, int* type, int* rows, int* cols,
+                               const float** scales) {
+    const QW* w = nullptr;
+    const Vec* v = nullptr;
+    if (layer == -1) {
+        if (kind == K_EMBED) w = &e->embed;
+        if (kind == K_LM_HEAD) w = &e->lm_head;
+        if (kind == K_NORM) v = &e->final_norm;
+    } else if (layer == kMtpLayer) {
+        if (!e->cfg.has_mtp) return nullptr;
+        switch (kind) {
+            case K_FC_E: w = &e->fc_e; break;
+            case K_FC_H: w = &e->fc_h; break;
+            case K_QKV: w = &e->m_qkv; break;
+            case K_O_PROJ: w = &e->m_o; break;
+            case K_GATE_UP: w = &e->m_gate_up; break;
+            case K_DOWN: w = &e->m_down; break;
+            case K_NORM_E: v = &e->norm_e; break;
+            case K_NORM_H: v = &e->norm_h; break;
+            case K_MTP_NORM: v = &e->m_norm; break;
+            case K_IN_LN: v = &e->m_in_ln; break;
+            case K_POST_LN: v = &e->m_post_ln; break;
+            case K_QK_NORM: v = &e->m_qk_norm; break;
+        }
+    } else if (layer >= 0 && layer < e->cfg.n_layers) {
+        const Layer& L = e->layers[layer];
+        switch (kind) {
+            case K_IN_LN: v = &L.in_ln; break;
+            case K_POST_LN: v = &L.post_ln; break;
+            case K_QK_NORM: if (L.full) v = &L.small; break;
+            case K_LIN: if (!L.full) v = &L.small; break;
+            case K_QKV: if (L.full) w = &L.mix_in; break;
+            case K_O_PROJ: if (L.full) w = &L.mix_out; break;
+            case K_IN_PROJ: if (!L.full) w = &L.mix_in; break;
+            case K_OUT_PROJ: if (!L.full) w = &L.mix_out; break;
+            case K_GATE_UP: w = &L.gate_up; break;
+            case K_DOWN: w = &L.down; break;
+            case K_MHC_ATTN: if (L.mhc_attn.p) v = &L.mhc_attn; break;
+            case K_MHC_FFN: if (L.mhc_ffn.p) v = &L.mhc_ffn; break;
+        }
+    }
+    if (w) {
+        *type = w->quant;
+        *rows = w->rows;
+        *cols = w->cols;
+        *scales = w->s;
+        return w->q;
+    }
+    if (v) {
+        *type = 2;
+        *rows = 1;
+        *cols = v->n;
+        *scales = nullptr;
+        return v->p;
+    }
+    return nullptr;
+}
+
+int snl_tensor_info(const snl_engine* e, int layer, int kind, int* rows, int* cols) {
+    int type = -1;
+    const float* s;
+    if (!e || !find_tensor(e, layer, kind, &type, rows, cols, &s)) return -1;
+    return type;
+}
+
+int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s) {
+    int type, rows, cols;
+    const float* sp;
+    const void* qp = find_tensor(e, layer, kind, &type, &rows, &cols, &sp);
+    if (!qp || !q) return SNL_EARG;
+    const size_t n = (size_t)rows * cols;
+    const size_t qb = type == 0 ? n : (type == 1 ? n / 2 : n * 4);
+    if (hipMemcpy(q, qp, qb, hipMemcpyDeviceToHost) != hipSuccess) return SNL_EDEVICE;
+    if (type != 2 && s && hipMemcpy(s, sp, n / 32 * 4, hipMemcpyDeviceToHost) != hipSuccess) return SNL_EDEVICE;
+    return SNL_OK;
+}
+
+size_t snl_buffer_size(const snl_engine* e, int id) {
+    const size_t nl = std::max(e->n_lin, 1);
+    switch (id) {
+        case 0: return (size_t)kMaxM * 2 * e->h * 4;
+        case 1: return (size_t)(kMaxM + 1) * e->h * 4;
+        case 2: return (size_t)e->h * 4;
+        case 3: return nl * e->state_floats * 4;
+        case 4: return nl * e->conv_floats * 4;
+        case 5: return (size_t)kMaxM * 2 * e->h * 4;
+    }
+    return 0;
+}
+
+int snl_buffer_read(snl_engine* e, int id, void* out, size_t bytes) {
+    if (!e || !out || bytes > snl_buffer_size(e, id)) return SNL_EARG;
+    const size_t nl = std::max(e->n_lin, 1);
+    const void* src = nullptr;
+    switch (id) {
+        case 0: src = e->x; break;
+        case 1: src = e->hid; break;
+        case 2: src = e->hlast; break;
+        case 3: src = e->lin_state + (size_t)e->cur * nl * e->state_floats; break;
+        case 4: src = e->conv_state + (size_t)e->cur * nl * e->conv_floats; break;
+        case 5: src = e->mx; break;
+        default: return SNL_EARG;
+    }
+    if (hipStreamSynchronize(e->stream) != hipSuccess || hipMemcpy(out, src, bytes, hipMemcpyDeviceToHost) != hipSuccess)
+        return SNL_EDEVICE;
+    return SNL_OK;
+}
+
+// ---- kernel-level entry points ----
+static std::mutex g_kstep_mu;
+static StepDev* g_kstep = nullptr;
+
+static StepDev* kernel_step(const StepDev& h, hipStream_t s) {
+    if (!g_kstep && hipMalloc((void**)&g_kstep, sizeof(StepDev)) != hipSuccess) return nullptr;
+    if (hipMemcpyAsync(g_kstep, &h, sizeof(StepDev), hipMemcpyHostToDevice, s) != hipSuccess) return nullptr;
+    if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
+    return g_kstep;
+}
+
+int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K, int x_stride,
+             int y_stride, void* stream) {
+    if ((quant != 0 && quant != 1) || !wq || !ws || !x || !y || x_stride % 4 || x_stride < K || y_stride < N)
+        return SNL_EARG;
+    GemvArgs g{};
+    g.wq = wq;
+    g.ws = ws;
+    g.x = x;
+    g.x_stride = x_stride;
+    g.y = y;
+    g.y_stride = y_stride;
+    g.N = N;
+    g.K = K;
+    g.epi = GEMV_STORE;
+    int rc = launch_gemv(g, quant, M, (hipStream_t)stream);
+    return rc == -1 ? SNL_EARG : (rc ? SNL_EDEVICE : SNL_OK);
+}
+
+int snl_deltanet(const float* proj, int proj_stride, const float* lw, float* conv_state, float* state, float* out,
+                 int conv_dim, int n_k, int n_v, float eps, int M, int ckpt, int s_in, int s_out, int s_ck,
+                 void* stream) {
+    if (!proj || !lw || !conv_state || !state || !out || M < 1 || M > SNL_MAX_M || ckpt < 0 || ckpt > M)
+        return SNL_EARG;
+    if (s_in < 0 || s_in > 2 || s_out < 0 || s_out > 2 || s_ck < 0 || s_ck > 2 || s_out == s_in ||
+        (ckpt && (s_ck == s_in || s_ck == s_out)))
+        return SNL_EARG;
+    if (n_k < 1 || n_v % n_k || conv_dim != 2 * n_k * 128 + n_v * 128) return SNL_EARG;
+    std::lock_guard<std::mutex> lk(g_kstep_mu);
+    StepDev h{};
+    h.m = M;
+    h.ckpt = ckpt;
+    h.s_in = s_in;
+    h.s_out = s_out;
+    h.s_ck = s_ck;
+    hipStream_t s = (hipStream_t)stream;
+    StepDev* d = kernel_step(h, s);
+    if (!d) return SNL_EDEVICE;
+    DeltaArgs a{};
+    a.proj = proj;
+    a.proj_stride = proj_stride;
+    a.lw = lw;
+    a.conv_state = conv_state;
+    a.state = state;
+    a.conv_slot = (size_t)3 * conv_dim;
+    a.state_slot = (size_t)n_v * 128 * 128;
+    a.out = out;
+    a.conv_dim = conv_dim;
+    a.n_k = n_k;
+    a.n_v = n_v;
+    a.eps = eps;
+    a.step = d;
+    if (launch_deltanet(a, M, s)) return SNL_EDEVICE;
+    return hipStreamSynchronize(s) == hipSuccess ? SNL_OK : SNL_EDEVICE;
+}
+
+int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kcache, uint16_t* vcache,
+                  const float* norms, float* out, float* partial, int n_heads, int n_kv, int rot_dim, float rope_theta,
+                  float eps, const int32_t* mrope_section, int ctx, int M, int pos0, const uint32_t* rpos,
+                  void* stream) {
+    if (!proj || !qbuf || !kcache || !vcache || !norms || !out || !partial || !mrope_section || !rpos) return SNL_EARG;
+    if (M < 1 || M > SNL_MAX_M || M == 3 || pos0 < 0 || pos0 + M > ctx || n_heads != 4 * n_kv) return SNL_EARG;
+    std::lock_guard<std::mutex> lk(g_kstep_mu);
+    StepDev h{};
+    h.pos0 = pos0;
+    h.m = M;
+    for (int i = 0; i < M; ++i)
+        for (int k = 0; k < 3; ++k) h.rpos[i][k] = rpos[i * 3 + k];
+    hipStream_t s = (hipStream_t)stream;
+    StepDev* d = kernel_step(h, s);
+    if (!d) return SNL_EDEVICE;
+    AttnArgs a{};
+    a.proj = proj;
+    a.proj_stride = proj_stride;
+    a.qbuf = qbuf;
+    a.kcache = kcache;
+    a.vcache = vcache;
+    a.norms = norms;
+    a.out = out;
+    a.partial = partial;
+    a.n_heads = n_heads;
+    a.n_kv = n_kv;
+    a.rot_dim = rot_dim;
+    a.rope_theta = rope_theta;
+    a.eps = eps;
+    a.scale = 1.0f / 16.0f;
+    a.mrope = ((uint32_t)(3 * mrope_section[1]) << 16) | (uint32_t)(3 * mrope_section[2]);
+    a.ctx = ctx;
+    a.step = d;
+    int rc = launch_attention(a, M, s);
+    if (rc) return rc == -1 ? SNL_EARG : SNL_EDEVICE;
+    return hipStreamSynchronize(s) == hipSuccess ? SNL_OK : SNL_EDEVICE;
+}
+
+int snl_pick_rows(const float* logits, int V, int rows, snl_pick* picks_out, void* stream) {
+    if (!logits || !picks_out || V < 1 || rows < 1 || rows > 64) return SNL_EARG;
+    float* scratch = nullptr;
+    if (hipMalloc((void**)&scratch, pick_scratch_floats(V, rows) * 4) != hipSuccess) return SNL_ENOMEM;
+    hipStream_t s = (hipStream_t)stream;
+    int rc = launch_pick(logits, V, rows, scratch, reinterpret_cast<Pick*>(picks_out), s);
+    hipError_t se = hipStreamSynchronize(s);
+    hipFree(scratch);
+    return rc || se != hipSuccess ? SNL_EDEVICE : SNL_OK;
+}
+
+}  // extern "C"

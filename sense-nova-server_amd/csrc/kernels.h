@@ -1,0 +1,120 @@
+// Launch descriptors and host-side launchers of the decode-step kernels.
+// Every launcher returns 0 on success, < 0 on a bad argument or launch error.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace snl {
+
+// ---------------------------------------------------------------- GEMV (gemv.hip)
+enum GemvEpi { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_MHC = 2, GEMV_SWIGLU = 3 };
+
+struct GemvArgs {
+    const void* wq;      // quants [N, K] (Q8) or [N, K/2] (Q4)
+    const float* ws;     // scales [N, K/32]
+    const float* x;      // token rows, x_stride floats apart (16-byte aligned, stride % 4 == 0)
+    int x_stride;
+    float* y;            // STORE: y[m*y_stride + n_off + n]; ADD/MHC: residual rows (stream 0 at +0,
+    int y_stride;        //   stream 1 at +h); SWIGLU: act[m*y_stride + i]
+    int N, K;
+    int n_off;
+    int epi;
+    const float* coef;   // MHC: [M, 8] router coefficients
+    int merge_mode;      // MHC: 1 mix, 2 mix then collapse to the mean
+    int h;               // MHC: offset of stream 1
+    int inter;           // SWIGLU: intermediate size (N == 2*inter; gate rows then up rows)
+};
+int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s);
+
+// ---------------------------------------------------------------- layers (layers.hip)
+// x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790)
+int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
+                 hipStream_t s);
+
+// out[r] = rmsnorm(branch input of row first+r) * (one + w) for r < count (layers.wgsl:46-73).
+// mode 1 mixes the two streams with coef[row][0..1].  Row `row` of x starts at
+// x + (row + (row_base ? *row_base : 0)) * x_stride.
+struct NormArgs {
+    const float* x;
+    int x_stride;
+    const int32_t* row_base;
+    const float* coef;
+    const float* w;
+    float* out;
+    int out_stride;
+    int h;
+    int mode;
+    int first;
+    int count;
+    float eps;
+    float one;
+};
+int launch_branch_norm(const NormArgs& a, hipStream_t s);
+
+// mHC router: raw[m][0..8] then coef[m][0..7] (layers.wgsl:75-126)
+int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s);
+
+// x[m, h + i] = x[m, i] (merge mode 3, layers.wgsl:146-149)
+int launch_expand(float* x, int h, int M, hipStream_t s);
+
+// Plain merge (modes 0..2) and SwiGLU, for paths that do not fuse them into a GEMV.
+int launch_merge(float* x, const float* coef, const float* br, int h, int M, int mode, hipStream_t s);
+int launch_swiglu(const float* proj, float* act, int inter, int M, hipStream_t s);
+
+// Greedy pick per logits row: first index of the maximum, the maximum and the second largest value.
+struct Pick {
+    uint32_t token;
+    float top1;
+    float top2;
+    uint32_t _pad;
+};
+int launch_pick(const float* logits, int V, int rows, float* scratch, Pick* out, hipStream_t s);
+size_t pick_scratch_floats(int V, int rows);
+
+int launch_copy(float* dst, const float* src, size_t n, hipStream_t s);
+
+// ---------------------------------------------------------------- Gated DeltaNet (deltanet.hip)
+struct DeltaArgs {
+    const float* proj;   // [M, proj_stride]: qkv[conv_dim] | z[n_v*128] | b[n_v] | a[n_v]
+    int proj_stride;
+    const float* lw;     // conv w [conv_dim*4] | A_log[n_v] | dt_bias[n_v] | norm[128]
+    float* conv_state;   // 3 slots of [3, conv_dim]
+    float* state;        // 3 slots of [n_v, 128, 128]
+    size_t conv_slot;    // floats per conv slot
+    size_t state_slot;   // floats per state slot
+    float* out;          // [M, n_v*128]
+    int conv_dim, n_k, n_v;
+    float eps;
+    const StepDev* step;  // s_in / s_out / s_ck / ckpt
+};
+int launch_deltanet(const DeltaArgs& a, int M, hipStream_t s);
+
+// ---------------------------------------------------------------- gated attention (attention.hip)
+struct AttnArgs {
+    const float* proj;   // [M, proj_stride] q+gate | k | v
+    int proj_stride;
+    float* qbuf;         // [M, n_heads*256]
+    uint16_t* kcache;    // [ctx, kv_dim] f16
+    uint16_t* vcache;
+    const float* norms;  // q_norm[256] | k_norm[256]
+    float* out;          // [M, n_heads*256]
+    float* partial;      // [M, n_heads, kMaxParts, 258]
+    int n_heads, n_kv, rot_dim;
+    float rope_theta, eps, scale;
+    uint32_t mrope;
+    int ctx;
+    const StepDev* step;  // pos0, rpos
+};
+constexpr int kMaxParts = 64;
+int launch_attention(const AttnArgs& a, int M, hipStream_t s);
+
+// ---------------------------------------------------------------- seeded initialiser (init.hip)
+int launch_gen_matrix(uint64_t key, int64_t rows, int64_t cols, float stdv, int quant, void* q, float* sc,
+                      hipStream_t s);
+// kind: 0 = std*N, 1 = 1 + std*N, 2 = DeltaNet parameter vector (conv_dim given), 3 = mHC router (h given)
+int launch_gen_vector(uint64_t key, int64_t n, int kind, float stdv, int aux0, int aux1, float* out, hipStream_t s);
+
+}  // namespace snl

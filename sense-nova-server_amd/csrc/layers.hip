@@ -1,0 +1,304 @@
+// Norms, mHC routing, residual merges, SwiGLU, embedding gather and the greedy pick.
+// Semantics follow src/shaders/layers.wgsl, src/engine.rs:777-790 and src/sampler.rs:169-177.
+#include <float.h>
+
+#include "common.h"
+#include "kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace snl {
+
+namespace {
+
+__global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const int8_t* eq, const float* es, int vocab,
+                                                     int h, float* x) {
+    const int m = blockIdx.x;
+    uint32_t tok = step->tokens[m];
+    if (tok >= (uint32_t)vocab) tok = 0;  // the host rejects out-of-range ids before launching
+    const int8_t* q = eq + (size_t)tok * h;
+    const float* s = es + (size_t)tok * (h / 32);
+    float* xr = x + (size_t)m * 2 * h;
+    for (int i = threadIdx.x; i < h; i += 256) {
+        xr[i] = (float)q[i] * s[i >> 5];
+        xr[h + i] = 0.0f;
+    }
+}
+
+// layers.wgsl:46-73 branch_norm; one block per output row.
+__global__ __launch_bounds__(256) void branch_norm_kernel(NormArgs a) {
+    __shared__ float red[8];
+    const int r = blockIdx.x;
+    const int row = a.first + r + (a.row_base ? *a.row_base : 0);
+    const float* xb = a.x + (size_t)row * a.x_stride;
+    float pre0 = 1.0f, pre1 = 0.0f;
+    if (a.mode == 1) {
+        pre0 = a.coef[(a.first + r) * 8];
+        pre1 = a.coef[(a.first + r) * 8 + 1];
+    }
+    constexpr int kMaxPer = 32;  // h <= 8192
+    float v[kMaxPer];
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        float t = 0.0f;
+        if (i < a.h) {
+            t = pre0 * xb[i];
+            if (a.mode == 1) t = t + pre1 * xb[a.h + i];
+        }
+        v[j] = t;
+        ss = fmaf(t, t, ss);
+    }
+    const float total = block_sum<256>(ss, red);
+    const float rinv = 1.0f / sqrtf(total / (float)a.h + a.eps);
+    float* ob = a.out + (size_t)r * a.out_stride;
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < a.h) ob[i] = (v[j] * rinv) * (a.one + a.w[i]);
+    }
+}
+
+// layers.wgsl:75-92 mhc_dots: block (o, m).
+__global__ __launch_bounds__(256) void mhc_dots_kernel(const float* x, const float* w, float* raw, int h) {
+    __shared__ float red[8];
+    const int o = blockIdx.x, m = blockIdx.y, d = 2 * h;
+    const float* xr = x + (size_t)m * d;
+    float acc = 0.0f;
+    if (o < 8) {
+        const float* wr = w + (size_t)o * d;
+        for (int i = threadIdx.x; i < d; i += 256) acc = fmaf(wr[i], xr[i], acc);
+    } else {
+        for (int i = threadIdx.x; i < d; i += 256) acc = fmaf(xr[i], xr[i], acc);
+    }
+    const float t = block_sum<256>(acc, red);
+    if (threadIdx.x == 0) raw[m * 9 + o] = t;
+}
+
+__device__ __forceinline__ float lse2(float a, float b) {
+    const float mx = fmaxf(a, b);
+    return mx + logf(expf(a - mx) + expf(b - mx));
+}
+
+// layers.wgsl:94-126 mhc_finish: one thread per token.
+__global__ void mhc_finish_kernel(const float* raw, const float* w, float* coef, int h, int M, int iterations) {
+    const int m = threadIdx.x;
+    if (m >= M) return;
+    const int d = 2 * h;
+    const float rinv = 1.0f / sqrtf(raw[m * 9 + 8] / (float)d + 1e-6f);
+    float lg[8];
+    for (int o = 0; o < 8; ++o) lg[o] = raw[m * 9 + o] * rinv + w[(size_t)8 * d + o];
+    float a = lg[4], b = lg[5], c = lg[6], e = lg[7];
+    for (int it = 0; it < iterations; ++it) {
+        const float r0 = lse2(a, b), r1 = lse2(c, e);
+        a -= r0;
+        b -= r0;
+        c -= r1;
+        e -= r1;
+        const float c0 = lse2(a, c), c1 = lse2(b, e);
+        a -= c0;
+        c -= c0;
+        b -= c1;
+        e -= c1;
+    }
+    float* cb = coef + m * 8;
+    cb[0] = 1.0f / (1.0f + expf(-lg[0]));
+    cb[1] = 1.0f / (1.0f + expf(-lg[1]));
+    cb[2] = 2.0f / (1.0f + expf(-lg[2]));
+    cb[3] = 2.0f / (1.0f + expf(-lg[3]));
+    cb[4] = expf(a);
+    cb[5] = expf(b);
+    cb[6] = expf(c);
+    cb[7] = expf(e);
+}
+
+__global__ __launch_bounds__(256) void expand_kernel(float* x, int h, int M) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * h) return;
+    const int m = idx / h, i = idx % h;
+    x[(size_t)m * 2 * h + h + i] = x[(size_t)m * 2 * h + i];
+}
+
+// layers.wgsl:128-162 merge, modes 0..2
+__global__ __launch_bounds__(256) void merge_kernel(float* x, const float* coef, const float* br, int h, int M,
+                                                     int mode) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * h) return;
+    const int m = idx / h, i = idx % h;
+    float* x0 = x + (size_t)m * 2 * h + i;
+    float* x1 = x0 + h;
+    const float b = br[idx];
+    if (mode == 0) {
+        *x0 = *x0 + b;
+        return;
+    }
+    const float* c = coef + m * 8;
+    const float a0 = *x0, a1 = *x1;
+    const float n0 = (c[4] * a0 + c[5] * a1) + c[2] * b;
+    const float n1 = (c[6] * a0 + c[7] * a1) + c[3] * b;
+    if (mode == 2) {
+        *x0 = 0.5f * (n0 + n1);
+    } else {
+        *x0 = n0;
+        *x1 = n1;
+    }
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* proj, float* act, int inter, int M) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * inter) return;
+    const int m = idx / inter, i = idx % inter;
+    const float g = proj[(size_t)m * 2 * inter + i], u = proj[(size_t)m * 2 * inter + inter + i];
+    act[idx] = g / (1.0f + expf(-g)) * u;
+}
+
+// ---- greedy pick: (max, first index of max, second largest) ----
+struct Top2 {
+    float v1;
+    uint32_t i1;
+    float v2;
+};
+
+__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
+    Top2 r;
+    const bool take_b = b.v1 > a.v1 || (b.v1 == a.v1 && b.i1 < a.i1);
+    r.v1 = take_b ? b.v1 : a.v1;
+    r.i1 = take_b ? b.i1 : a.i1;
+    r.v2 = fmaxf(fminf(a.v1, b.v1), fmaxf(a.v2, b.v2));
+    return r;
+}
+
+__device__ __forceinline__ Top2 top2_wave(Top2 t) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        Top2 u;
+        u.v1 = __shfl_xor(t.v1, o, 64);
+        u.i1 = __shfl_xor(t.i1, o, 64);
+        u.v2 = __shfl_xor(t.v2, o, 64);
+        t = top2_merge(t, u);
+    }
+    return t;
+}
+
+__device__ __forceinline__ Top2 top2_block(Top2 t) {
+    __shared__ float s1[4], s2[4];
+    __shared__ uint32_t si[4];
+    t = top2_wave(t);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+        s1[w] = t.v1;
+        si[w] = t.i1;
+        s2[w] = t.v2;
+    }
+    __syncthreads();
+    Top2 r = {s1[0], si[0], s2[0]};
+    for (int i = 1; i < 4; ++i) r = top2_merge(r, Top2{s1[i], si[i], s2[i]});
+    return r;
+}
+
+constexpr int kPickChunk = 8192;
+
+__global__ __launch_bounds__(256) void pick_partial_kernel(const float* logits, int V, float* scratch, int nblk) {
+    const int row = blockIdx.y, b = blockIdx.x;
+    const float* lg = logits + (size_t)row * V;
+    Top2 t = {-FLT_MAX, 0xFFFFFFFFu, -FLT_MAX};
+    const int end = min(V, (b + 1) * kPickChunk);
+    for (int i = b * kPickChunk + threadIdx.x; i < end; i += 256) {
+        const float v = lg[i];
+        // strict > keeps the first index; elements arrive in ascending order per thread
+        if (v > t.v1) {
+            t.v2 = t.v1;
+            t.v1 = v;
+            t.i1 = (uint32_t)i;
+        } else if (v > t.v2) {
+            t.v2 = v;
+        }
+    }
+    t = top2_block(t);
+    if (threadIdx.x == 0) {
+        float* o = scratch + ((size_t)row * nblk + b) * 3;
+        o[0] = t.v1;
+        o[1] = __uint_as_float(t.i1);
+        o[2] = t.v2;
+    }
+}
+
+__global__ __launch_bounds__(256) void pick_final_kernel(const float* scratch, int nblk, Pick* out) {
+    const int row = blockIdx.x;
+    Top2 t = {-FLT_MAX, 0xFFFFFFFFu, -FLT_MAX};
+    for (int b = threadIdx.x; b < nblk; b += 256) {
+        const float* o = scratch + ((size_t)row * nblk + b) * 3;
+        t = top2_merge(t, Top2{o[0], __float_as_uint(o[1]), o[2]});
+    }
+    t = top2_block(t);
+    if (threadIdx.x == 0) {
+        out[row].token = t.i1 == 0xFFFFFFFFu ? 0u : t.i1;
+        out[row].top1 = t.v1;
+        out[row].top2 = t.v2;
+        out[row]._pad = 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void copy_kernel(float* dst, const float* src, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+inline int last_error() { return hipGetLastError() == hipSuccess ? 0 : -2; }
+
+}  // namespace
+
+int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
+                 hipStream_t s) {
+    if (M < 1 || M > SNL_MAX_M || h % 32) return -1;
+    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, step, eq, es, vocab, h, x);
+    return last_error();
+}
+
+int launch_branch_norm(const NormArgs& a, hipStream_t s) {
+    if (a.count < 1 || a.h > 8192 || a.h < 1) return -1;
+    hipLaunchKernelGGL(branch_norm_kernel, dim3(a.count), dim3(256), 0, s, a);
+    return last_error();
+}
+
+int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s) {
+    if (M < 1 || M > 64) return -1;
+    hipLaunchKernelGGL(mhc_dots_kernel, dim3(9, M), dim3(256), 0, s, x, w, raw, h);
+    hipLaunchKernelGGL(mhc_finish_kernel, dim3(1), dim3(64), 0, s, raw, w, coef, h, M, iterations);
+    return last_error();
+}
+
+int launch_expand(float* x, int h, int M, hipStream_t s) {
+    hipLaunchKernelGGL(expand_kernel, dim3((M * h + 255) / 256), dim3(256), 0, s, x, h, M);
+    return last_error();
+}
+
+int launch_merge(float* x, const float* coef, const float* br, int h, int M, int mode, hipStream_t s) {
+    if (mode < 0 || mode > 2) return -1;
+    hipLaunchKernelGGL(merge_kernel, dim3((M * h + 255) / 256), dim3(256), 0, s, x, coef, br, h, M, mode);
+    return last_error();
+}
+
+int launch_swiglu(const float* proj, float* act, int inter, int M, hipStream_t s) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3((M * inter + 255) / 256), dim3(256), 0, s, proj, act, inter, M);
+    return last_error();
+}
+
+size_t pick_scratch_floats(int V, int rows) { return (size_t)rows * ((V + kPickChunk - 1) / kPickChunk) * 3; }
+
+int launch_pick(const float* logits, int V, int rows, float* scratch, Pick* out, hipStream_t s) {
+    if (rows < 1 || V < 1) return -1;
+    const int nblk = (V + kPickChunk - 1) / kPickChunk;
+    hipLaunchKernelGGL(pick_partial_kernel, dim3(nblk, rows), dim3(256), 0, s, logits, V, scratch, nblk);
+    hipLaunchKernelGGL(pick_final_kernel, dim3(rows), dim3(256), 0, s, scratch, nblk, out);
+    return last_error();
+}
+
+int launch_copy(float* dst, const float* src, size_t n, hipStream_t s) {
+    hipLaunchKernelGGL(copy_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, dst, src, n);
+    return last_error();
+}
+
+}  // namespace snl

@@ -1,0 +1,220 @@
+"""End-to-end parity of the engine (C ABI) on the tiny SenseNova-Loop-style model.
+
+hidden 256, FFN 768, vocab 4096, 8 layers (DeltaNet : attention = 3 : 1), layers 2-5 looped
+twice, 2-stream mHC over the loop, 1-layer MTP head; seeded Q8_0 / Q4_0 weights drawn on the
+device and, independently, by the oracle on the CPU.
+
+Bars (north star): weights bit-exact; token ids and acceptance decisions bit-exact except at
+argmax near-ties (top-2 gap < 1e-3 in the oracle's logits); logits and DeltaNet state within
+1e-2 relative; greedy output byte-identical with and without MTP.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TIE = 1e-3
+
+
+@pytest.fixture(scope="module")
+def snl_mod():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import snl
+
+    snl.lib()
+    return snl
+
+
+def _prompt(n, vocab, seed=1):
+    return np.random.default_rng(seed).integers(0, vocab, n).tolist()
+
+
+@pytest.fixture(scope="module", params=[0, 1], ids=["q8", "q4"])
+def pair(request, snl_mod, oracle):
+    cfg = snl_mod.tiny_config()
+    quant = request.param
+    print(f"engine pair quant={quant}", flush=True)
+    g = snl_mod.Engine(cfg, seed=3, quant=quant, ctx=256)
+    o = oracle.Engine(cfg, seed=3, quant=quant, ctx=256, max_m=g.prefill_chunk)
+    yield cfg, g, o
+    g.close()
+    o.close()
+
+
+def test_weights_bit_exact(pair, oracle):
+    cfg, g, o = pair
+    import snl
+
+    kinds = [(-1, snl.engine.K_EMBED), (-1, snl.engine.K_LM_HEAD), (-1, snl.engine.K_NORM)]
+    for l in range(cfg.n_layers):
+        ks = [1, 2, 9, 10] + ([3, 5, 6] if cfg.full_attention[l] else [4, 7, 8])
+        if cfg.is_mhc(l):
+            ks += [11, 12]
+        kinds += [(l, k) for k in ks]
+    kinds += [(snl.engine.MTP_LAYER, k) for k in (20, 21, 22, 23, 24, 1, 2, 3, 5, 6, 9, 10)]
+    for layer, kind in kinds:
+        gt, gq, gs = g.tensor(layer, kind)
+        ot, oq, os_ = o.tensor(layer, kind)
+        assert gt == ot, (layer, kind)
+        if gt == 2:
+            assert np.array_equal(gq.view(np.uint32), oq.view(np.uint32)), (layer, kind)
+        else:
+            assert np.array_equal(gq, oq), (layer, kind)
+            assert np.array_equal(gs.view(np.uint32), os_.view(np.uint32)), (layer, kind)
+
+
+def test_forward_logits_match_oracle(pair):
+    cfg, g, o = pair
+    g.reset()
+    o.reset()
+    prompt = _prompt(9, cfg.vocab, seed=4)
+    pos = [[i] * 3 for i in range(len(prompt))]
+    lg_g, picks = g.forward(prompt, pos, logit_rows=1)
+    lg_o = o.forward(prompt, pos, logit_rows=1)
+    rel = np.abs(lg_g - lg_o).max() / np.abs(lg_o).max()
+    assert rel < 1e-3, rel
+    assert picks[0].token == int(np.argmax(lg_g[0]))
+    # a verify step: two rows, checkpointed
+    t = [int(np.argmax(lg_o[0])), 17]
+    p2 = [[9] * 3, [10] * 3]
+    lg_g2, picks2 = g.forward(t, p2, logit_rows=2, ckpt=True)
+    lg_o2 = o.forward(t, p2, logit_rows=2, ckpt=True)
+    rel = np.abs(lg_g2 - lg_o2).max() / np.abs(lg_o2).max()
+    assert rel < 1e-3, rel
+    for r in range(2):
+        srt = np.sort(lg_o2[r])
+        if srt[-1] - srt[-2] >= TIE:
+            assert picks2[r].token == int(np.argmax(lg_o2[r]))
+    # DeltaNet state after the verify step, current slot
+    st_g = g.buffer(3)
+    st_o = o.buf(3, st_g.size)
+    assert np.abs(st_g - st_o).max() / np.abs(st_o).max() < 1e-2
+    # rollback then compare again
+    g.rollback()
+    o.rollback()
+    assert g.pos == o.pos == 10 and g.hid_rows == o.hid_rows == 1
+    st_g = g.buffer(3)
+    st_o = o.buf(3, st_g.size)
+    assert np.abs(st_g - st_o).max() / np.abs(st_o).max() < 1e-2
+    hl_g, hl_o = g.buffer(2), o.buf(2, cfg.hidden)
+    assert np.abs(hl_g - hl_o).max() / np.abs(hl_o).max() < 1e-2
+
+
+def test_mtp_draft_matches_oracle(pair):
+    cfg, g, o = pair
+    for e in (g, o):
+        e.reset()
+    prompt = _prompt(12, cfg.vocab, seed=5)
+    pos = [[i] * 3 for i in range(12)]
+    g.forward(prompt, pos, logit_rows=1)
+    o.forward(prompt, pos, logit_rows=1)
+    d_g, pk, lg_g = g.mtp(1, [33], [[11] * 3], 11, True, want_logits=True)
+    d_o, lg_o = o.mtp(1, [33], [[11] * 3], 11, True)
+    rel = np.abs(lg_g - lg_o).max() / np.abs(lg_o).max()
+    assert rel < 1e-3, rel
+    srt = np.sort(lg_o)
+    if srt[-1] - srt[-2] >= TIE:
+        assert d_g == d_o
+
+
+def _compare_streams(a, ref_tokens, ref_gaps):
+    """Tokens equal up to the first divergence, which must sit at an oracle near-tie."""
+    n = min(len(a), len(ref_tokens))
+    for i in range(n):
+        if a[i] != ref_tokens[i]:
+            assert ref_gaps[i] < TIE, f"divergence at {i} with oracle gap {ref_gaps[i]}"
+            return i
+    assert len(a) == len(ref_tokens)
+    return n
+
+
+@pytest.mark.parametrize("spec", [False, True])
+def test_generate_matches_oracle(pair, spec):
+    cfg, g, o = pair
+    prompt = _prompt(32, cfg.vocab, seed=1)
+    rg = g.generate(prompt, 64, spec)
+    ro = o.generate(prompt, 64, spec)
+    matched = _compare_streams(rg["tokens"], ro["tokens"], ro["gaps"])
+    print(f"spec={spec} matched {matched}/64 drafted {rg['drafted']}/{ro['drafted']} "
+          f"accepted {rg['accepted']}/{ro['accepted']}", flush=True)
+    if matched == 64 and spec:
+        assert rg["drafted"] == ro["drafted"]
+
+
+def test_mtp_on_off_identical(pair):
+    cfg, g, o = pair
+    for seed in (1, 2, 3):
+        prompt = _prompt(32, cfg.vocab, seed=seed)
+        a = g.generate(prompt, 64, False)
+        b = g.generate(prompt, 64, True)
+        assert a["tokens"] == b["tokens"]
+        assert b["drafted"] > 0
+
+
+def test_rollback_equals_never_run(pair):
+    """verify([t, d]) + rollback leaves exactly the state of forward([t])."""
+    cfg, g, o = pair
+    prompt = _prompt(10, cfg.vocab, seed=8)
+    pos = [[i] * 3 for i in range(10)]
+    g.reset()
+    g.forward(prompt, pos, logit_rows=1)
+    g.forward([5, 6], [[10] * 3, [11] * 3], logit_rows=2, ckpt=True)
+    g.rollback()
+    s1, c1, h1 = g.buffer(3), g.buffer(4), g.buffer(2)
+    _, pk1 = g.forward([7], [[11] * 3], logit_rows=1)
+    g.reset()
+    g.forward(prompt, pos, logit_rows=1)
+    g.forward([5], [[10] * 3], logit_rows=1)
+    s2, c2, h2 = g.buffer(3), g.buffer(4), g.buffer(2)
+    _, pk2 = g.forward([7], [[11] * 3], logit_rows=1)
+    assert np.array_equal(s1, s2) and np.array_equal(c1, c2) and np.array_equal(h1, h2)
+    assert pk1[0].token == pk2[0].token and pk1[0].top1 == pk2[0].top1
+
+
+def test_snapshot_restore(pair):
+    cfg, g, o = pair
+    prompt = _prompt(20, cfg.vocab, seed=9)
+    pos = [[i] * 3 for i in range(20)]
+    g.reset()
+    g.forward(prompt[:12], pos[:12], logit_rows=0)
+    g.snapshot(2)
+    lg_a, _ = g.forward(prompt[12:], pos[12:], logit_rows=1)
+    g.forward([1, 2, 3], [[20] * 3, [21] * 3, [22] * 3], logit_rows=1)
+    g.restore(2, 12)
+    assert g.pos == 12
+    lg_b, _ = g.forward(prompt[12:], pos[12:], logit_rows=1)
+    assert np.array_equal(lg_a, lg_b)
+
+
+def test_error_paths(pair):
+    cfg, g, o = pair
+    import snl
+    from snl.engine import SnlError
+
+    g.reset()
+    with pytest.raises(SnlError) as ei:
+        g.forward([cfg.vocab], None, 1)
+    assert ei.value.code == snl.engine.SNL_ETOKEN
+    with pytest.raises(SnlError) as ei:
+        g.forward([1, 2, 3], None, 3)
+    assert ei.value.code == snl.engine.SNL_EARG
+    with pytest.raises(SnlError) as ei:
+        g.forward([1], None, 1, ckpt=True)
+    assert ei.value.code == snl.engine.SNL_EARG
+    with pytest.raises(SnlError) as ei:
+        g.forward([], None, 1)
+    assert ei.value.code == snl.engine.SNL_EARG
+    with pytest.raises(SnlError) as ei:
+        g.rollback()
+    assert ei.value.code == snl.engine.SNL_ESTATE
+    with pytest.raises(SnlError) as ei:
+        g.forward([1] * (g.ctx + 1), None, 1)
+    assert ei.value.code == snl.engine.SNL_ECTX
+    g.forward([1, 2], None, 1)
+    with pytest.raises(SnlError) as ei:
+        g.mtp(2, [1, 2], [[0] * 3, [1] * 3], 0, True)
+    assert ei.value.code == snl.engine.SNL_EARG
+    g.reset()
+    assert g.pos == 0
