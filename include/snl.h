@@ -167,9 +167,9 @@ int snl_deltanet(const float* proj, int proj_stride, const float* lw, float* con
                  int conv_dim, int n_k, int n_v, float eps, int M, int ckpt, int s_in, int s_out, int s_ck,
                  void* stream);
 
-/* Gated attention for M = 1, 2 or 4 tokens at cache positions pos0..pos0+M-1
+/* Gated attention for M = 1 or 2 tokens at cache positions pos0..pos0+M-1
  * (attention.wgsl prep + attend + combine).  rpos: host [M][3] rotary positions.
- * partial: device scratch of M * n_heads * ceil(ctx/128) * 258 floats. */
+ * partial: device scratch of M * n_heads * ceil(ctx/64) * 258 floats. */
 int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kcache, uint16_t* vcache,
                   const float* norms, float* out, float* partial, int n_heads, int n_kv, int rot_dim,
                   float rope_theta, float eps, const int32_t* mrope_section, int ctx, int M, int pos0,

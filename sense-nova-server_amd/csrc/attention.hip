@@ -1,8 +1,8 @@
 // Gated GQA decode attention with partial rotate-half RoPE over the f16 KV cache
 // (src/shaders/attention.wgsl: prep :59-127, attend :129-246, combine :248-269).
 //
-// Keys are split into fixed 128-key parts at absolute positions: part p covers keys
-// [128p, 128p+128).  A token with `total` keys uses parts 0..ceil(total/128)-1, so its
+// Keys are split into fixed 64-key parts at absolute positions: part p covers keys
+// [64p, 64p+64).  A token with `total` keys uses parts 0..ceil(total/64)-1, so its
 // partition depends only on its own position, never on how many tokens share the call
 // (the reference sizes its split from the whole step, src/engine.rs:827).  One block per
 // (kv head, part) serves all M tokens and all 4 query heads of the GQA group, so each K/V
@@ -20,7 +20,7 @@ namespace snl {
 
 namespace {
 
-constexpr int HD = 256, G = 4, kPart = 128;
+constexpr int HD = 256, G = 4, kPart = 64;
 
 // attention.wgsl:59-127: block (slot, token); slots [0, nh) queries, then keys, then values.
 __global__ __launch_bounds__(256) void prep_kernel(AttnArgs a) {
@@ -63,39 +63,24 @@ __global__ __launch_bounds__(256) void prep_kernel(AttnArgs a) {
     }
 }
 
-__device__ __forceinline__ float h2f(uint16_t b) { return __half2float(__ushort_as_half(b)); }
+__device__ __forceinline__ float h2f(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
 
-// Transposed butterfly: v[NV] per lane -> lane L returns the 64-lane sum of value L >> (6 - log2 NV).
-template <int NV>
-__device__ __forceinline__ float tsum(float (&v)[NV], int lane) {
-    int n = NV;
-#pragma unroll
-    for (int mask = 32; mask >= 64 / NV && n > 1; mask >>= 1) {
-        const bool up = lane & mask;
-        const int hn = n / 2;
-#pragma unroll
-        for (int i = 0; i < NV / 2; ++i) {
-            if (i < hn) {
-                const float send = up ? v[i] : v[hn + i], keep = up ? v[hn + i] : v[i];
-                v[i] = keep + __shfl_xor(send, mask, 64);
-            }
-        }
-        n = hn;
-    }
-    float r = v[0];
-#pragma unroll
-    for (int mask = 32 / NV; mask > 0; mask >>= 1) r = r + __shfl_xor(r, mask, 64);
-    return r;
-}
-
-// Block (kv head, part): scores for all M tokens x 4 heads over the part's keys, exact softmax
-// inside the part, then the value sum.  256 threads = 4 waves; wave w scores keys
-// [32w, 32w+32) of the part; lane l holds dims [4l, 4l+4).
+// Block (kv head, part of kPart keys) for all M tokens and the 4 query heads of the GQA group
+// (NC = 4M head-token combinations).  256 threads = 4 waves.
+//  scores: wave w takes keys [16w, 16w+16) of the part, 4 at a time: 16-lane row r of the wave
+//          holds key 4i+r, lane j of the row dims [16j, 16j+16); the 16 lanes of a row are reduced
+//          by a transposed butterfly (every combination takes the same shuffle sequence);
+//  softmax: exact within the part, 32 threads per combination;
+//  values: thread (dim pair, key half) accumulates its 32 keys with all loads in flight.
+// Each combination's arithmetic only depends on its own token's keys, so a token's result does
+// not depend on M or on its row index.
 template <int M>
 __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
-    constexpr int NC = G * M;  // (head, token) combinations
+    constexpr int NC = G * M;
+    static_assert(NC == 4 || NC == 8, "M = 1 or 2");
     __shared__ float sc[NC][kPart];
     __shared__ float smax[NC], ssum[NC];
+    __shared__ float2 vred[NC][128];
     const int kh = blockIdx.x, p = blockIdx.y;
     const StepDev* st = a.step;
     const int pos0 = st->pos0;
@@ -105,93 +90,137 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     const int nkeys = min(kPart, total_max - kstart);
     const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-
-    float q[NC][4];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const int g = c % G, m = c / G;
-        const float4 t = *reinterpret_cast<const float4*>(a.qbuf + (size_t)m * q_dim + (kh * G + g) * HD + 4 * lane);
-        q[c][0] = t.x, q[c][1] = t.y, q[c][2] = t.z, q[c][3] = t.w;
-    }
-    // 16 keys at a time; each (head, token) combination is reduced by its own 16-value
-    // butterfly, so a score's summation order never depends on M.
-    const uint16_t* kbase = a.kcache + (size_t)kh * HD + 4 * lane;
-#pragma unroll 1
-    for (int k0 = w * 32; k0 < w * 32 + 32; k0 += 16) {
-        if (k0 >= nkeys) break;
-        float v[NC][16];
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            float kf[4] = {0.f, 0.f, 0.f, 0.f};
-            if (k0 + t < nkeys) {
-                const uint2 raw = *reinterpret_cast<const uint2*>(kbase + (size_t)(kstart + k0 + t) * kv_dim);
-                kf[0] = h2f(raw.x & 0xFFFF), kf[1] = h2f(raw.x >> 16), kf[2] = h2f(raw.y & 0xFFFF),
-                kf[3] = h2f(raw.y >> 16);
-            }
-#pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                float d = q[c][0] * kf[0];
-                d = fmaf(q[c][1], kf[1], d);
-                d = fmaf(q[c][2], kf[2], d);
-                d = fmaf(q[c][3], kf[3], d);
-                v[c][t] = d;
-            }
-        }
-        const int t = lane >> 2;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const float r = tsum<16>(v[c], lane);  // lane L holds key L >> 2
-            if ((lane & 3) == 0 && k0 + t < nkeys) sc[c][k0 + t] = r * a.scale;
-        }
-    }
-    __syncthreads();
-    // exact softmax over the part, per (head, token); token m sees keys < pos0 + m + 1
-    if (w == 0) {
-        for (int c = 0; c < NC; ++c) {
-            const int m = c / G;
-            const int valid = min(nkeys, pos0 + m + 1 - kstart);
-            float mx = -FLT_MAX;
-            for (int t = lane; t < valid; t += 64) mx = fmaxf(mx, sc[c][t]);
-            mx = wave_max(mx);
-            float sum = 0.0f;
-            for (int t = lane; t < kPart; t += 64) {
-                float e = 0.0f;
-                if (t < valid) e = expf(sc[c][t] - mx);
-                sc[c][t] = e;
-                sum += e;
-            }
-            sum = wave_sum(sum);
-            if (lane == 0) {
-                smax[c] = valid > 0 ? mx : -1e30f;
-                ssum[c] = sum;
-            }
-        }
-    }
-    __syncthreads();
-    // value sum: thread d owns dim d
-    float acc[NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = 0.0f;
+    const int r = lane >> 4, j = lane & 15;
     int valid[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) valid[m] = min(nkeys, pos0 + m + 1 - kstart);
-    const uint16_t* vb = a.vcache + (size_t)kh * HD + tid;
-    for (int t = 0; t < nkeys; ++t) {
-        const float vv = h2f(vb[(size_t)(kstart + t) * kv_dim]);
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-            if (t < valid[c / G]) acc[c] = fmaf(sc[c][t], vv, acc[c]);
-    }
-    const int parts_max = (a.ctx + kPart - 1) / kPart;
+
+    // ---- scores ----
+    float q[NC][16];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        const int g = c % G, m = c / G;
-        const int hh = kh * G + g;
-        float* o = a.partial + (((size_t)m * a.n_heads + hh) * parts_max + p) * (HD + 2);
-        o[tid] = acc[c];
-        if (tid == 0) {
-            o[HD] = smax[c];
-            o[HD + 1] = ssum[c];
+        const float4* qp = reinterpret_cast<const float4*>(a.qbuf + (size_t)(c / G) * q_dim + (kh * G + c % G) * HD + 16 * j);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const float4 t = qp[v];
+            q[c][4 * v] = t.x, q[c][4 * v + 1] = t.y, q[c][4 * v + 2] = t.z, q[c][4 * v + 3] = t.w;
+        }
+    }
+    const uint16_t* kb = a.kcache + (size_t)kh * HD + 16 * j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * i + r;  // key of this 16-lane row
+        float kf[16];
+        if (t < nkeys) {
+            const uint4* kp = reinterpret_cast<const uint4*>(kb + (size_t)(kstart + t) * kv_dim);
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const uint4 raw = kp[v];
+                const uint32_t ws[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kf[8 * v + 2 * e] = h2f(ws[e] & 0xFFFF);
+                    kf[8 * v + 2 * e + 1] = h2f(ws[e] >> 16);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) kf[e] = 0.0f;
+        }
+        float d[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            float s = q[c][0] * kf[0];
+#pragma unroll
+            for (int e = 1; e < 16; ++e) s = fmaf(q[c][e], kf[e], s);
+            d[c] = s;
+        }
+        // transposed butterfly over the 16 lanes of the row
+        int n = NC;
+#pragma unroll
+        for (int mask = 8; mask >= 16 / NC && n > 1; mask >>= 1) {
+            const bool up = j & mask;
+            const int hn = n / 2;
+#pragma unroll
+            for (int e = 0; e < NC / 2; ++e) {
+                if (e < hn) {
+                    const float send = up ? d[e] : d[hn + e], keep = up ? d[hn + e] : d[e];
+                    d[e] = keep + __shfl_xor(send, mask, 64);
+                }
+            }
+            n = hn;
+        }
+        float tot = d[0];
+#pragma unroll
+        for (int mask = 8 / NC; mask > 0; mask >>= 1) tot = tot + __shfl_xor(tot, mask, 64);
+        // lane j of the row holds combination j / (16 / NC)
+        if ((j & (16 / NC - 1)) == 0 && t < nkeys) sc[j / (16 / NC)][t] = tot * a.scale;
+    }
+    __syncthreads();
+
+    // ---- exact softmax over the part, 32 threads per combination ----
+    if (tid < 32 * NC) {
+        const int c = tid >> 5, l = tid & 31;
+        const int vk = valid[c / G];
+        const float s0 = l < vk ? sc[c][l] : -FLT_MAX, s1 = l + 32 < vk ? sc[c][l + 32] : -FLT_MAX;
+        float mx = fmaxf(s0, s1);
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+        const float e0 = l < vk ? expf(s0 - mx) : 0.0f, e1 = l + 32 < vk ? expf(s1 - mx) : 0.0f;
+        sc[c][l] = e0;
+        sc[c][l + 32] = e1;
+        float sum = e0 + e1;
+#pragma unroll
+        for (int o = 16; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, 32);
+        if (l == 0) {
+            smax[c] = vk > 0 ? mx : -1e30f;
+            ssum[c] = sum;
+        }
+    }
+    __syncthreads();
+
+    // ---- values: thread (dim pair dp, key half kh2) ----
+    const int dp = tid & 127, kh2 = tid >> 7;
+    float2 acc[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = make_float2(0.0f, 0.0f);
+    const uint32_t* vb = reinterpret_cast<const uint32_t*>(a.vcache + (size_t)kh * HD) + dp;
+    constexpr int KH = kPart / 2;
+    uint32_t vw[KH];
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+        const int t = kh2 * KH + i;
+        vw[i] = t < nkeys ? vb[(size_t)(kstart + t) * (kv_dim / 2)] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+        const int t = kh2 * KH + i;
+        const float v0 = h2f(vw[i] & 0xFFFF), v1 = h2f(vw[i] >> 16);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            if (t < valid[c / G]) {
+                acc[c].x = fmaf(sc[c][t], v0, acc[c].x);
+                acc[c].y = fmaf(sc[c][t], v1, acc[c].y);
+            }
+        }
+    }
+    if (kh2 == 1)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) vred[c][dp] = acc[c];
+    __syncthreads();
+    if (kh2 == 0) {
+        const int parts_max = (a.ctx + kPart - 1) / kPart;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int m = c / G, hh = kh * G + c % G;
+            float* o = a.partial + (((size_t)m * a.n_heads + hh) * parts_max + p) * (HD + 2);
+            const float2 u = vred[c][dp];
+            o[2 * dp] = acc[c].x + u.x;
+            o[2 * dp + 1] = acc[c].y + u.y;
+            if (dp == 0) {
+                o[HD] = smax[c];
+                o[HD + 1] = ssum[c];
+            }
         }
     }
 }
@@ -219,14 +248,13 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
 }  // namespace
 
 int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
-    if (M < 1 || M > SNL_MAX_M || M == 3 || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2) return -1;
+    if (M < 1 || M > 2 || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2) return -1;
     hipLaunchKernelGGL(prep_kernel, dim3(a.n_heads + 2 * a.n_kv, M), dim3(256), 0, s, a);
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     dim3 grid(a.n_kv, parts_max);
     switch (M) {
         case 1: hipLaunchKernelGGL(attend_kernel<1>, grid, dim3(256), 0, s, a); break;
         case 2: hipLaunchKernelGGL(attend_kernel<2>, grid, dim3(256), 0, s, a); break;
-        case 4: hipLaunchKernelGGL(attend_kernel<4>, grid, dim3(256), 0, s, a); break;
         default: return -1;
     }
     hipLaunchKernelGGL(combine_kernel, dim3(a.n_heads, M), dim3(256), 0, s, a);

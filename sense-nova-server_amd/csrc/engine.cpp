@@ -195,14 +195,18 @@ struct snl_engine {
     int record_forward(int M, int rows, int ckpt);
     int record_mtp(int M, int draft);
     int run(int kind, int M, int a, int b);
+    // GEMV with an optional fused branch-input prologue (pro: GEMV_NORM with norm weights nw, or
+    // GEMV_NORM_MHC with router mw whose dots are in mhc_raw) and the epilogue `epi`.
     int gemv(const char* name, const QW& w, const float* xin, int x_stride, float* y, int y_stride, int M, int epi,
-             int merge_mode = 0) {
+             int merge_mode = 0, int pro = GEMV_PLAIN, const float* nw = nullptr, const float* mw = nullptr,
+             const int32_t* row_base = nullptr) {
         mark(name, gemv_bytes(w, M, epi, cfg.intermediate));
         GemvArgs g{};
         g.wq = w.q;
         g.ws = w.s;
         g.x = xin;
         g.x_stride = x_stride;
+        g.row_base = row_base;
         g.y = y;
         g.y_stride = y_stride;
         g.N = w.rows;
@@ -212,6 +216,13 @@ struct snl_engine {
         g.merge_mode = merge_mode;
         g.h = h;
         g.inter = cfg.intermediate;
+        g.pro = pro;
+        g.norm_w = nw;
+        g.eps = cfg.eps;
+        g.mhc_raw = mhc_raw;
+        g.mhc_w = mw;
+        g.coef_out = coef;
+        g.iterations = cfg.mhc_iterations;
         return launch_gemv(g, w.quant, M, stream);
     }
     int norm(const float* xin, int x_stride, const int32_t* row_base, int mode, const float* w, float* out,
@@ -299,6 +310,7 @@ int snl_engine::init() {
 
     if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess)
         return fail(SNL_EDEVICE, "hipStreamCreate failed");
+    if (gemv_init()) return fail(SNL_EDEVICE, "GEMV LDS configuration failed");
     int rc;
     // ---- weights (convert.rs:228-311 layout; seeded values) ----
     if ((rc = gen_q(embed, -1, K_EMBED, c.vocab, h, 0))) return rc;
@@ -348,7 +360,7 @@ int snl_engine::init() {
     const int act_w = std::max(c.intermediate, conv_dim);
     const int attn_w = std::max(q_dim, lin_value_dim);
     const int M = SNL_MAX_M;
-    const int parts_max = (ctx + 127) / 128;
+    const int parts_max = (ctx + kAttnPart - 1) / kAttnPart;
     if ((rc = dalloc(&x, (size_t)M * 2 * h)) || (rc = dalloc(&xn, (size_t)M * h)) ||
         (rc = dalloc(&proj, (size_t)M * proj_w)) || (rc = dalloc(&act, (size_t)M * act_w)) ||
         (rc = dalloc(&attn_out, (size_t)M * attn_w)) || (rc = dalloc(&qbuf, (size_t)M * q_dim)) ||
@@ -413,20 +425,23 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             mark("expand", 0.0);
             rc |= launch_expand(x, h, M, stream);
         }
+        // branch input: RMSNorm (1 + in_ln) of stream 0, or of the mHC pre-mix, fused into the GEMV
         if (mhc) {
-            mark("mhc", 0.0);
-            rc |= launch_mhc(x, L.mhc_attn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
+            mark("mhc_dots", 0.0);
+            rc |= launch_mhc_dots(x, L.mhc_attn.p, mhc_raw, h, M, stream);
         }
-        rc |= norm(x, 2 * h, nullptr, mhc ? 1 : 0, L.in_ln.p, xn, 0, M);
+        const int pro = mhc ? GEMV_NORM_MHC : GEMV_NORM;
         if (L.full) {
-            rc |= gemv("gemv_qkv", L.mix_in, xn, h, proj, attn_proj_rows, M, GEMV_STORE);
+            rc |= gemv("gemv_qkv", L.mix_in, x, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p,
+                       L.mhc_attn.p);
             AttnArgs a = attn_args(d_step, kcache + kvn * fslot, vcache + kvn * fslot, L.small.p);
             mark("attention", 0.0);
             rc |= launch_attention(a, M, stream);
             rc |= gemv("gemv_o", L.mix_out, attn_out, q_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, 1);
             ++fslot;
         } else {
-            rc |= gemv("gemv_in_proj", L.mix_in, xn, h, proj, lin_proj_rows, M, GEMV_STORE);
+            rc |= gemv("gemv_in_proj", L.mix_in, x, 2 * h, proj, lin_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p,
+                       L.mhc_attn.p);
             DeltaArgs d{};
             d.proj = proj;
             d.proj_stride = lin_proj_rows;
@@ -448,11 +463,11 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             ++lslot;
         }
         if (mhc) {
-            mark("mhc", 0.0);
-            rc |= launch_mhc(x, L.mhc_ffn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
+            mark("mhc_dots", 0.0);
+            rc |= launch_mhc_dots(x, L.mhc_ffn.p, mhc_raw, h, M, stream);
         }
-        rc |= norm(x, 2 * h, nullptr, mhc ? 1 : 0, L.post_ln.p, xn, 0, M);
-        rc |= gemv("gemv_gate_up", L.gate_up, xn, h, act, c.intermediate, M, GEMV_SWIGLU);
+        rc |= gemv("gemv_gate_up", L.gate_up, x, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, pro, L.post_ln.p,
+                   L.mhc_ffn.p);
         const int mode = !mhc ? 0 : (li + 1 == c.mhc_end ? 2 : 1);
         rc |= gemv("gemv_down", L.down, act, c.intermediate, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, mode);
     }
@@ -473,23 +488,26 @@ int snl_engine::record_mtp(int M, int draft) {
     const snl_config& c = cfg;
     int rc = 0;
     rc |= launch_embed(d_mstep, (const int8_t*)embed.q, embed.s, c.vocab, h, mx, M, stream);
+    // x = fc_e(norm_e(emb)) + fc_h(norm_h(hid[r0..])); fc_e reads xn, since it writes mx
     rc |= norm(mx, 2 * h, nullptr, 0, norm_e.p, xn, 0, M);
-    rc |= norm(hid, h, &d_mstep->r0, 0, norm_h.p, hn, 0, M);
     rc |= gemv("gemv_fc_e", fc_e, xn, h, mx, 2 * h, M, GEMV_STORE);
-    rc |= gemv("gemv_fc_h", fc_h, hn, h, mx, 2 * h, M, GEMV_ADD);
-    rc |= norm(mx, 2 * h, nullptr, 0, m_in_ln.p, xn, 0, M);
-    rc |= gemv("gemv_mtp_qkv", m_qkv, xn, h, proj, attn_proj_rows, M, GEMV_STORE);
+    rc |= gemv("gemv_fc_h", fc_h, hid, h, mx, 2 * h, M, GEMV_ADD, 0, GEMV_NORM, norm_h.p, nullptr, &d_mstep->r0);
+    rc |= gemv("gemv_mtp_qkv", m_qkv, mx, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, GEMV_NORM, m_in_ln.p);
     AttnArgs a = attn_args(d_mstep, m_kc, m_vc, m_qk_norm.p);
+    mark("attention", 0.0);
     rc |= launch_attention(a, M, stream);
     rc |= gemv("gemv_mtp_o", m_o, attn_out, q_dim, mx, 2 * h, M, GEMV_ADD);
-    rc |= norm(mx, 2 * h, nullptr, 0, m_post_ln.p, xn, 0, M);
-    rc |= gemv("gemv_mtp_gate_up", m_gate_up, xn, h, act, c.intermediate, M, GEMV_SWIGLU);
+    rc |= gemv("gemv_mtp_gate_up", m_gate_up, mx, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, GEMV_NORM,
+               m_post_ln.p);
     rc |= gemv("gemv_mtp_down", m_down, act, c.intermediate, mx, 2 * h, M, GEMV_ADD);
     if (draft) {
-        rc |= norm(mx, 2 * h, nullptr, 0, m_norm.p, xn, M - 1, 1);
-        rc |= gemv("gemv_lm_head", lm_head, xn, h, m_logits, c.vocab, 1, GEMV_STORE);
+        // final norm of the last pair fused into the LM head
+        rc |= gemv("gemv_lm_head", lm_head, mx + (size_t)(M - 1) * 2 * h, 2 * h, m_logits, c.vocab, 1, GEMV_STORE, 0,
+                   GEMV_NORM, m_norm.p);
+        mark("pick", 0.0);
         rc |= launch_pick(m_logits, c.vocab, 1, pick_scratch, d_mpick, stream);
     }
+    mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
 }
 
@@ -1085,6 +1103,8 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
              int y_stride, void* stream) {
     if ((quant != 0 && quant != 1) || !wq || !ws || !x || !y || x_stride % 4 || x_stride < K || y_stride < N)
         return SNL_EARG;
+    static const int init_rc = gemv_init();
+    if (init_rc) return SNL_EDEVICE;
     GemvArgs g{};
     g.wq = wq;
     g.ws = ws;
@@ -1141,7 +1161,7 @@ int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kca
                   float eps, const int32_t* mrope_section, int ctx, int M, int pos0, const uint32_t* rpos,
                   void* stream) {
     if (!proj || !qbuf || !kcache || !vcache || !norms || !out || !partial || !mrope_section || !rpos) return SNL_EARG;
-    if (M < 1 || M > SNL_MAX_M || M == 3 || pos0 < 0 || pos0 + M > ctx || n_heads != 4 * n_kv) return SNL_EARG;
+    if (M < 1 || M > 2 || pos0 < 0 || pos0 + M > ctx || n_heads != 4 * n_kv) return SNL_EARG;
     std::lock_guard<std::mutex> lk(g_kstep_mu);
     StepDev h{};
     h.pos0 = pos0;

@@ -1,34 +1,39 @@
-// Skinny block-quantised GEMV for decode (M = 1..4 token rows), gfx950.
+// Streaming skinny block-quantised GEMV for decode (M = 1..4 token rows), gfx950.
 //
 // y[m, n] = sum_b s[n, b] * sum_{i<32} q[n, 32b + i] * x[m, 32b + i]
 //
 // Weights stay in the reference's row-major layout (src/weights.rs:48-55,
-// src/engine.rs:84-108): quants [N, K] (Q8_0: int8; Q4_0: 16 bytes per 32-block,
-// nibble i of little-endian word w = element 8w + i), then f32 scales [N, K/32].
+// src/engine.rs:84-108): quants [N, K] (Q8_0: int8; Q4_0: 16 bytes per 32-block, nibble i of
+// little-endian word w = element 8w + i), then f32 scales [N, K/32].
 //
-// Mapping.  A block of 256 threads (4 wave64s) owns R = 16 output rows and the whole
-// K range.  K is cut into 1024-element chunks; wave w takes chunks w, w+4, ...  Lane l
-// of a wave covers elements [chunk*1024 + 16l, +16) of every row of the block, so one
-// wave-wide load reads 1 KiB (Q8, 16 B/lane) or 512 B (Q4, 8 B/lane) of one row
-// contiguously.  The lane keeps its 16 x values per token row in registers and applies
-// them to all 16 weight rows: the weights are read once for every token row (the M=2
-// verify pass costs the weight bytes of one pass).
+// Mapping.  A block of 256 threads (4 wave64s) first stages the M token rows in LDS, then each
+// wave streams its own groups of 4 weight rows over the whole K range: lane l covers elements
+// [1024c + 16l, +16) of chunk c, so one load instruction reads 1 KiB (Q8, 16 B/lane) or 512 B
+// (Q4, 8 B/lane) of one row contiguously.  The next (group, chunk) step's loads are issued before
+// the current step is computed, so every wave keeps weight bytes in flight while it computes.
+// One x slice read from LDS serves the 4 rows of the group and all M token rows are applied to
+// each weight byte once: the M=2 verify pass reads each weight once.
 //
-// Dequantisation in registers.  Q8: the word is xor-ed with 0x80808080, which turns
-// each int8 q into the unsigned byte q+128; v_cvt_f32_ubyte{0..3} converts one byte per
-// instruction and the bias is removed once per half-block, sum (q+128) x - 128 sum x.
-// Q4: the nibbles n are masked into bytes and converted the same way, minus 8 sum x.
+// Dequantisation in registers.  Q8: the word is xor-ed with 0x80808080, which turns each int8 q
+// into the unsigned byte q+128; v_cvt_f32_ubyte{0..3} converts one byte per instruction and the
+// bias is removed once per lane slice, sum (q+128) x - 128 sum x.  Q4: the nibbles are masked
+// into bytes and converted the same way, minus 8 sum x.  The 16-element sums of x are staged in
+// LDS with x.
 //
-// Reduction.  Each lane holds 16 row partials per token row; a transposed butterfly
-// (xor 32, 16, 8, 4 exchange half of the values, then xor 2, 1 add) leaves lane 4r with
-// row r, then the 4 waves are summed in fixed order through LDS.  Every token row takes
-// exactly the same instruction sequence whatever M is, so row m of an M=2 call is
-// bitwise equal to the same row in an M=1 call (greedy output is then byte-identical
-// with and without speculative drafting).
+// Prologue (fused branch input, layers.wgsl:46-73 and :94-126): the staged rows are either the
+// plain x rows, or RMSNorm(x0)*(1+w), or, inside the mHC range, RMSNorm(pre0*x0 + pre1*x1)*(1+w)
+// with pre from the router dots and a 2x2 log-space Sinkhorn computed by the block itself
+// (block 0 also stores the token coefficients for the merge epilogue).
 //
-// Epilogues: plain store; residual add into stream 0 (merge mode 0, layers.wgsl:142-145);
-// mHC merge (modes 1/2, layers.wgsl:150-161); SwiGLU pairs (layers.wgsl:164-175), where
-// a block owns gate rows [8b, 8b+8) and the matching up rows, and writes act directly.
+// Reduction.  Per group each lane holds 4 row partials per token row; a transposed butterfly
+// (xor 32, 16 exchange halves, then xor 8..1 add) leaves lane 16r with row r.  Every token row
+// takes the same instruction sequence whatever M and its index are, so a token's row of an M=2
+// call is bitwise the row of an M=1 call (greedy output is then byte-identical with and without
+// speculative drafting).
+//
+// Epilogues: plain store; residual add into stream 0 (merge mode 0, layers.wgsl:142-145); mHC
+// merge (modes 1/2, layers.wgsl:150-161); SwiGLU pairs (layers.wgsl:164-175): a group owns gate
+// rows c0, c0+1 and the matching up rows and writes act directly.
 #include "common.h"
 #include "kernels.h"
 
@@ -38,31 +43,55 @@ namespace snl {
 
 namespace {
 
-constexpr int kRows = 16;
-constexpr int kThreads = 256;
-constexpr int kChunk = 1024;
+constexpr int kThreads = 256, kWaves = 4, kChunk = 1024;
+constexpr int kLdsFloats = 32768;  // token rows staged in LDS: M * K (whole chunks) <= 32768 floats
 
 template <int EPI>
-__device__ __forceinline__ int row_of(int blk, int r, int inter) {
-    if constexpr (EPI == GEMV_SWIGLU) return r < 8 ? blk * 8 + r : inter + blk * 8 + (r - 8);
-    return blk * kRows + r;
+__device__ __forceinline__ int group_row(const GemvArgs& a, int blk, int G, int wg, int r) {
+    // wg = wave * G + g; returns the weight row of row r (0..3) of the group or -1
+    if constexpr (EPI == GEMV_SWIGLU) {
+        const int c0 = blk * 8 * G + wg * 2 + (r & 1);
+        if (c0 >= a.inter) return -1;
+        return r < 2 ? c0 : a.inter + c0;
+    } else {
+        const int row = blk * 16 * G + wg * 4 + r;
+        return row < a.N ? row : -1;
+    }
 }
 
-// sum over the lane's 16 products of (byte value) * x, for one token row
 template <int QT>
-__device__ __forceinline__ void dot16(const uint32_t (&w)[4], const float (&x)[16], float& p) {
+__device__ __forceinline__ void load_frag(const GemvArgs& a, int row, int k, uint32_t (&w)[4], float& sc) {
+    if (row >= 0 && k < a.K) {
+        if constexpr (QT == 0) {
+            const uint4 t = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.wq) + (size_t)row * a.K + k);
+            w[0] = t.x, w[1] = t.y, w[2] = t.z, w[3] = t.w;
+        } else {
+            const uint2 t =
+                *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.wq) + (size_t)row * (a.K >> 1) + (k >> 1));
+            w[0] = t.x, w[1] = t.y, w[2] = 0u, w[3] = 0u;
+        }
+        sc = a.ws[(size_t)row * (a.K >> 5) + (k >> 5)];
+    } else {
+        w[0] = w[1] = w[2] = w[3] = QT == 0 ? 0x80808080u : 0x88888888u;
+        sc = 0.0f;
+    }
+}
+
+// sum over the lane's 16 elements of (biased byte value) * x for one token row
+template <int QT>
+__device__ __forceinline__ float dot16(const uint32_t (&w)[4], const float (&x)[16]) {
+    float p = 0.0f;
     if constexpr (QT == 0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            uint32_t u = w[j] ^ 0x80808080u;
+            const uint32_t u = w[j] ^ 0x80808080u;
 #pragma unroll
             for (int b = 0; b < 4; ++b) p = fmaf((float)((u >> (8 * b)) & 0xFFu), x[4 * j + b], p);
         }
     } else {
-        // two words = 16 nibbles = elements 0..15 of the lane's half block
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            uint32_t lo = w[j] & 0x0F0F0F0Fu, hi = (w[j] >> 4) & 0x0F0F0F0Fu;
+            const uint32_t lo = w[j] & 0x0F0F0F0Fu, hi = (w[j] >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
                 p = fmaf((float)((lo >> (8 * b)) & 0xFFu), x[8 * j + 2 * b], p);
@@ -70,185 +99,342 @@ __device__ __forceinline__ void dot16(const uint32_t (&w)[4], const float (&x)[1
             }
         }
     }
+    return p;
 }
 
-template <int QT, int M, int EPI>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int blk = blockIdx.x;
-    const int K = a.K, nb = K >> 5;
-    const int nchunks = (K + kChunk - 1) / kChunk;
+// LDS layout of a staged token row: per 1024-element chunk, float4 v (0..3) of lane l sits at
+// float4 index chunk*256 + v*64 + l, so the 4 ds_read_b128 of a wave hit consecutive addresses.
+__device__ __forceinline__ int lds_f4(int k4) {  // k4 = k / 4
+    const int c = k4 >> 8, l = (k4 >> 2) & 63, v = k4 & 3;
+    return (c << 8) + (v << 6) + l;
+}
 
-    float acc[kRows][M];
+__device__ __forceinline__ float lse2(float a, float b) {
+    const float mx = fmaxf(a, b);
+    return mx + __logf(__expf(a - mx) + __expf(b - mx));
+}
+
+template <int QT, int M, int EPI, int PRO>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
+    extern __shared__ float4 lds4[];
+    __shared__ float coef_s[SNL_MAX_M][8];
+    __shared__ float red_s[kWaves][SNL_MAX_M];
+    const int K = a.K, K4 = K >> 2, K16 = K >> 4;
+    const int nchunks = (K + kChunk - 1) / kChunk;
+    const int K4p = nchunks * (kChunk / 4);                         // staged row length, whole chunks
+    float4* xs4 = lds4;                                             // [M][K4p] staged rows (permuted)
+    float* sxs = reinterpret_cast<float*>(lds4 + (size_t)M * K4p);  // [M][K/16] 16-element sums
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int blk = blockIdx.x;
+    const int steps = G * nchunks;
+
+    // issue the first weight fragments before the prologue so HBM latency overlaps it
+    uint32_t wc[4][4], wn[4][4];
+    float scc[4], scn[4];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < 4; ++r) load_frag<QT>(a, group_row<EPI>(a, blk, G, wave * G, r), lane * 16, wc[r], scc[r]);
+
+    // ---- prologue: stage the token rows (optionally normalised) in LDS ----
+    const int row0 = a.row_base ? *a.row_base : 0;
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        // router logits -> pre/post/mix coefficients (layers.wgsl:94-126), one thread per token
+        if (tid < M) {
+            const int m = tid, d = 2 * K;
+            const float* raw = a.mhc_raw + m * 9;
+            const float rinv = 1.0f / sqrtf(raw[8] / (float)d + 1e-6f);
+            float lg[8];
+#pragma unroll
+            for (int o = 0; o < 8; ++o) lg[o] = raw[o] * rinv + a.mhc_w[(size_t)8 * d + o];
+            float p = lg[4], q = lg[5], u = lg[6], v = lg[7];
+            for (int it = 0; it < a.iterations; ++it) {
+                const float r0 = lse2(p, q), r1 = lse2(u, v);
+                p -= r0;
+                q -= r0;
+                u -= r1;
+                v -= r1;
+                const float c0 = lse2(p, u), c1 = lse2(q, v);
+                p -= c0;
+                u -= c0;
+                q -= c1;
+                v -= c1;
+            }
+            float cf[8];
+            cf[0] = 1.0f / (1.0f + __expf(-lg[0]));
+            cf[1] = 1.0f / (1.0f + __expf(-lg[1]));
+            cf[2] = 2.0f / (1.0f + __expf(-lg[2]));
+            cf[3] = 2.0f / (1.0f + __expf(-lg[3]));
+            cf[4] = __expf(p);
+            cf[5] = __expf(q);
+            cf[6] = __expf(u);
+            cf[7] = __expf(v);
+#pragma unroll
+            for (int o = 0; o < 8; ++o) {
+                coef_s[m][o] = cf[o];
+                if (blk == 0) a.coef_out[m * 8 + o] = cf[o];
+            }
+        }
+        __syncthreads();
+    }
+    if constexpr (PRO == GEMV_PLAIN) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float4* xr = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + m) * a.x_stride);
+            for (int k4 = tid; k4 < K4; k4 += kThreads) xs4[m * K4p + lds_f4(k4)] = xr[k4];
+        }
+        __syncthreads();
+    } else {
+        float ss[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float4* x0 = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + m) * a.x_stride);
+            const float pre0 = PRO == GEMV_NORM_MHC ? coef_s[m][0] : 1.0f;
+            const float pre1 = PRO == GEMV_NORM_MHC ? coef_s[m][1] : 0.0f;
+            float acc = 0.0f;
+            for (int k4 = tid; k4 < K4; k4 += kThreads) {
+                float4 v = x0[k4];
+                if constexpr (PRO == GEMV_NORM_MHC) {
+                    const float4 w1 = x0[K4 + k4];
+                    v.x = pre0 * v.x + pre1 * w1.x;
+                    v.y = pre0 * v.y + pre1 * w1.y;
+                    v.z = pre0 * v.z + pre1 * w1.z;
+                    v.w = pre0 * v.w + pre1 * w1.w;
+                }
+                acc = fmaf(v.x, v.x, acc);
+                acc = fmaf(v.y, v.y, acc);
+                acc = fmaf(v.z, v.z, acc);
+                acc = fmaf(v.w, v.w, acc);
+                xs4[m * K4p + lds_f4(k4)] = v;
+            }
+            ss[m] = wave_sum(acc);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int m = 0; m < M; ++m) red_s[wave][m] = ss[m];
+        __syncthreads();
+        // scale by rinv * (1 + w) in place
+        float rinv[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float total = ((red_s[0][m] + red_s[1][m]) + red_s[2][m]) + red_s[3][m];
+            rinv[m] = 1.0f / sqrtf(total / (float)K + a.eps);
+        }
+        const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            for (int k4 = tid; k4 < K4; k4 += kThreads) {
+                float4 v = xs4[m * K4p + lds_f4(k4)];
+                const float4 w = w4[k4];
+                v.x = (v.x * rinv[m]) * (1.0f + w.x);
+                v.y = (v.y * rinv[m]) * (1.0f + w.y);
+                v.z = (v.z * rinv[m]) * (1.0f + w.z);
+                v.w = (v.w * rinv[m]) * (1.0f + w.w);
+                xs4[m * K4p + lds_f4(k4)] = v;
+            }
+        __syncthreads();
+    }
+    // 16-element sums for the dequantisation bias
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+        for (int j = tid; j < K16; j += kThreads) {
+            float s = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float4 t = xs4[m * K4p + lds_f4(4 * j + v)];
+                s = s + t.x;
+                s = s + t.y;
+                s = s + t.z;
+                s = s + t.w;
+            }
+            sxs[m * K16 + j] = s;
+        }
+    __syncthreads();
+
+    // ---- streaming main loop ----
+    const float bias = QT == 0 ? 128.0f : 8.0f;
+    float acc[4][M];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[r][m] = 0.0f;
 
-    for (int c = wave; c < nchunks; c += 4) {
+    for (int s = 0; s < steps; ++s) {
+        const int g = s / nchunks, c = s - g * nchunks;
+        if (s + 1 < steps) {
+            const int g1 = (s + 1) / nchunks, c1 = (s + 1) - g1 * nchunks;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                load_frag<QT>(a, group_row<EPI>(a, blk, G, wave * G + g1, r), c1 * kChunk + lane * 16, wn[r], scn[r]);
+        }
         const int k = c * kChunk + lane * 16;
         if (k < K) {
-            float xs[M][16], sx[M];
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const float4* xp = reinterpret_cast<const float4*>(a.x + (size_t)m * a.x_stride + k);
+                float xv[16];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    float4 t = xp[v];
-                    xs[m][4 * v] = t.x;
-                    xs[m][4 * v + 1] = t.y;
-                    xs[m][4 * v + 2] = t.z;
-                    xs[m][4 * v + 3] = t.w;
+                    const float4 t = xs4[m * K4p + (c << 8) + (v << 6) + lane];
+                    xv[4 * v] = t.x;
+                    xv[4 * v + 1] = t.y;
+                    xv[4 * v + 2] = t.z;
+                    xv[4 * v + 3] = t.w;
                 }
-                float s = xs[m][0];
+                const float sx = sxs[m * K16 + (k >> 4)];
 #pragma unroll
-                for (int i = 1; i < 16; ++i) s = s + xs[m][i];
-                sx[m] = s;
+                for (int r = 0; r < 4; ++r) {
+                    const float p = dot16<QT>(wc[r], xv);
+                    acc[r][m] = fmaf(scc[r], fmaf(-bias, sx, p), acc[r][m]);
+                }
             }
-            const float bias = QT == 0 ? 128.0f : 8.0f;
+        }
+        if (c == nchunks - 1) {
+            // transposed butterfly per token row: lane 16r ends with row r of the group
+            const bool b5 = lane & 32, b4 = lane & 16;
+            float out[M];
 #pragma unroll
-            for (int r0 = 0; r0 < kRows; r0 += 8) {
-                uint32_t wv[8][4];
-                float sc[8];
+            for (int m = 0; m < M; ++m) {
+                float k0 = b5 ? acc[2][m] : acc[0][m], k1 = b5 ? acc[3][m] : acc[1][m];
+                const float s0 = b5 ? acc[0][m] : acc[2][m], s1 = b5 ? acc[1][m] : acc[3][m];
+                k0 = k0 + __shfl_xor(s0, 32, 64);
+                k1 = k1 + __shfl_xor(s1, 32, 64);
+                float kk = b4 ? k1 : k0;
+                const float ss = b4 ? k0 : k1;
+                kk = kk + __shfl_xor(ss, 16, 64);
+                kk = kk + __shfl_xor(kk, 8, 64);
+                kk = kk + __shfl_xor(kk, 4, 64);
+                kk = kk + __shfl_xor(kk, 2, 64);
+                kk = kk + __shfl_xor(kk, 1, 64);
+                out[m] = kk;
 #pragma unroll
-                for (int r = 0; r < 8; ++r) {
-                    const int row = row_of<EPI>(blk, r0 + r, a.inter);
-                    const bool ok = EPI == GEMV_SWIGLU ? (blk * 8 + ((r0 + r) & 7) < a.inter) : (row < a.N);
-                    if (ok) {
-                        if constexpr (QT == 0) {
-                            uint4 t = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.wq) +
-                                                                      (size_t)row * K + k);
-                            wv[r][0] = t.x, wv[r][1] = t.y, wv[r][2] = t.z, wv[r][3] = t.w;
-                        } else {
-                            uint2 t = *reinterpret_cast<const uint2*>(static_cast<const uint8_t*>(a.wq) +
-                                                                      (size_t)row * (K >> 1) + (k >> 1));
-                            wv[r][0] = t.x, wv[r][1] = t.y, wv[r][2] = 0u, wv[r][3] = 0u;
+                for (int r = 0; r < 4; ++r) acc[r][m] = 0.0f;
+            }
+            const int r = lane >> 4;
+            const int wg = wave * G + g;
+            if constexpr (EPI == GEMV_SWIGLU) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float u = __shfl(out[m], (lane + 32) & 63, 64);
+                    if ((lane & 15) == 0 && r < 2) {
+                        const int row = group_row<EPI>(a, blk, G, wg, r);
+                        if (row >= 0) {
+                            const float gt = out[m];
+                            a.y[(size_t)m * a.y_stride + row] = gt / (1.0f + expf(-gt)) * u;
                         }
-                        sc[r] = a.ws[(size_t)row * nb + (k >> 5)];
-                    } else {
-                        wv[r][0] = wv[r][1] = wv[r][2] = wv[r][3] = QT == 0 ? 0x80808080u : 0x88888888u;
-                        sc[r] = 0.0f;
                     }
                 }
-#pragma unroll
-                for (int r = 0; r < 8; ++r)
+            } else {
+                const int row = group_row<EPI>(a, blk, G, wg, r);
+                if ((lane & 15) == 0 && row >= 0) {
 #pragma unroll
                     for (int m = 0; m < M; ++m) {
-                        float p = 0.0f;
-                        dot16<QT>(wv[r], xs[m], p);
-                        acc[r0 + r][m] = fmaf(sc[r], fmaf(-bias, sx[m], p), acc[r0 + r][m]);
-                    }
-            }
-        }
-    }
-
-    // transposed butterfly over the 64 lanes, per token row
-    __shared__ float red[4][M][kRows];
-    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        float v[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = acc[i][m];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            float send = b5 ? v[i] : v[8 + i], keep = b5 ? v[8 + i] : v[i];
-            v[i] = keep + __shfl_xor(send, 32, 64);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float send = b4 ? v[i] : v[4 + i], keep = b4 ? v[4 + i] : v[i];
-            v[i] = keep + __shfl_xor(send, 16, 64);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            float send = b3 ? v[i] : v[2 + i], keep = b3 ? v[2 + i] : v[i];
-            v[i] = keep + __shfl_xor(send, 8, 64);
-        }
-        {
-            float send = b2 ? v[0] : v[1], keep = b2 ? v[1] : v[0];
-            v[0] = keep + __shfl_xor(send, 4, 64);
-        }
-        v[0] = v[0] + __shfl_xor(v[0], 2, 64);
-        v[0] = v[0] + __shfl_xor(v[0], 1, 64);
-        if ((lane & 3) == 0) red[wave][m][lane >> 2] = v[0];
-    }
-    __syncthreads();
-
-    const int t = threadIdx.x;
-    if constexpr (EPI == GEMV_SWIGLU) {
-        if (t < 8 * M) {
-            const int i = t & 7, m = t >> 3;
-            const int col = blk * 8 + i;
-            if (col < a.inter) {
-                float g = ((red[0][m][i] + red[1][m][i]) + red[2][m][i]) + red[3][m][i];
-                float u = ((red[0][m][8 + i] + red[1][m][8 + i]) + red[2][m][8 + i]) + red[3][m][8 + i];
-                a.y[(size_t)m * a.y_stride + col] = g / (1.0f + expf(-g)) * u;
-            }
-        }
-    } else {
-        if (t < kRows * M) {
-            const int r = t & (kRows - 1), m = t / kRows;
-            const int row = blk * kRows + r;
-            if (row < a.N) {
-                float v = ((red[0][m][r] + red[1][m][r]) + red[2][m][r]) + red[3][m][r];
-                float* y = a.y + (size_t)m * a.y_stride;
-                if constexpr (EPI == GEMV_STORE) {
-                    y[a.n_off + row] = v;
-                } else if constexpr (EPI == GEMV_ADD) {
-                    y[row] = y[row] + v;
-                } else {  // GEMV_MHC: layers.wgsl:150-161
-                    const float* c = a.coef + m * 8;
-                    float x0 = y[row], x1 = y[a.h + row];
-                    float n0 = (c[4] * x0 + c[5] * x1) + c[2] * v;
-                    float n1 = (c[6] * x0 + c[7] * x1) + c[3] * v;
-                    if (a.merge_mode == 2) {
-                        y[row] = 0.5f * (n0 + n1);
-                    } else {
-                        y[row] = n0;
-                        y[a.h + row] = n1;
+                        float* y = a.y + (size_t)m * a.y_stride;
+                        const float v = out[m];
+                        if constexpr (EPI == GEMV_STORE) {
+                            y[a.n_off + row] = v;
+                        } else if constexpr (EPI == GEMV_ADD) {
+                            y[row] = y[row] + v;
+                        } else {  // GEMV_MHC, layers.wgsl:150-161
+                            const float* cf = a.coef + m * 8;
+                            const float x0 = y[row], x1 = y[a.h + row];
+                            const float n0 = (cf[4] * x0 + cf[5] * x1) + cf[2] * v;
+                            const float n1 = (cf[6] * x0 + cf[7] * x1) + cf[3] * v;
+                            if (a.merge_mode == 2) {
+                                y[row] = 0.5f * (n0 + n1);
+                            } else {
+                                y[row] = n0;
+                                y[a.h + row] = n1;
+                            }
+                        }
                     }
                 }
             }
         }
-    }
-}
-
-template <int QT, int M>
-int launch_q(const GemvArgs& a, hipStream_t s) {
-    if (a.epi == GEMV_SWIGLU) {
-        dim3 grid((a.inter + 7) / 8);
-        hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_SWIGLU>), grid, dim3(kThreads), 0, s, a);
-    } else {
-        dim3 grid((a.N + kRows - 1) / kRows);
-        switch (a.epi) {
-            case GEMV_STORE: hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_STORE>), grid, dim3(kThreads), 0, s, a); break;
-            case GEMV_ADD: hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_ADD>), grid, dim3(kThreads), 0, s, a); break;
-            case GEMV_MHC: hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_MHC>), grid, dim3(kThreads), 0, s, a); break;
-            default: return -1;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            scc[r] = scn[r];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wc[r][j] = wn[r][j];
         }
     }
-    return 0;
 }
 
-template <int QT>
-int launch_m(const GemvArgs& a, int M, hipStream_t s) {
-    switch (M) {
-        case 1: return launch_q<QT, 1>(a, s);
-        case 2: return launch_q<QT, 2>(a, s);
-        case 3: return launch_q<QT, 3>(a, s);
-        case 4: return launch_q<QT, 4>(a, s);
+template <int QT, int M, int EPI, int PRO>
+void* kernel_ptr() {
+    return reinterpret_cast<void*>(&gemv_kernel<QT, M, EPI, PRO>);
+}
+
+using KernelFn = void (*)(GemvArgs, int);
+
+template <int QT, int M>
+KernelFn pick_fn(int epi, int pro) {
+#define SNL_G(E, P) \
+    if (epi == E && pro == P) return &gemv_kernel<QT, M, E, P>;
+    SNL_G(GEMV_STORE, GEMV_PLAIN)
+    SNL_G(GEMV_STORE, GEMV_NORM)
+    SNL_G(GEMV_STORE, GEMV_NORM_MHC)
+    SNL_G(GEMV_ADD, GEMV_PLAIN)
+    SNL_G(GEMV_ADD, GEMV_NORM)
+    SNL_G(GEMV_MHC, GEMV_PLAIN)
+    SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
+    SNL_G(GEMV_SWIGLU, GEMV_NORM)
+    SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
+#undef SNL_G
+    return nullptr;
+}
+
+KernelFn pick(int quant, int M, int epi, int pro) {
+    switch (quant * 8 + M) {
+        case 1: return pick_fn<0, 1>(epi, pro);
+        case 2: return pick_fn<0, 2>(epi, pro);
+        case 3: return pick_fn<0, 3>(epi, pro);
+        case 4: return pick_fn<0, 4>(epi, pro);
+        case 9: return pick_fn<1, 1>(epi, pro);
+        case 10: return pick_fn<1, 2>(epi, pro);
+        case 11: return pick_fn<1, 3>(epi, pro);
+        case 12: return pick_fn<1, 4>(epi, pro);
     }
-    return -1;
+    return nullptr;
+}
+
+// Row groups (of 4 rows) per wave: more for tall matrices, so that fewer blocks restage x.
+int groups_for(int N) {
+    if (N >= 65536) return 4;
+    if (N >= 16384) return 2;
+    return 1;
 }
 
 }  // namespace
 
+int gemv_init() {
+    const int bytes = kLdsFloats * 4 + kLdsFloats / 16 * 4;
+    for (int q = 0; q < 2; ++q)
+        for (int M = 1; M <= SNL_MAX_M; ++M)
+            for (int e = 0; e < 4; ++e)
+                for (int p = 0; p < 3; ++p) {
+                    KernelFn f = pick(q, M, e, p);
+                    if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
+                        return -2;
+                }
+    return 0;
+}
+
 int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
-    if (M < 1 || M > SNL_MAX_M || a.K % 32 != 0 || a.K <= 0 || a.N <= 0) return -1;
+    if (M < 1 || M > SNL_MAX_M || a.K % 32 != 0 || a.K <= 0 || a.N <= 0 || (quant != 0 && quant != 1)) return -1;
     if (a.epi == GEMV_SWIGLU && a.N != 2 * a.inter) return -1;
-    int rc = quant == 0 ? launch_m<0>(a, M, s) : launch_m<1>(a, M, s);
-    if (rc) return rc;
+    if (a.pro != GEMV_PLAIN && a.K % 4) return -1;
+    const int K4p = (a.K + kChunk - 1) / kChunk * (kChunk / 4);
+    if ((size_t)M * K4p * 4 > (size_t)kLdsFloats) {
+        if (a.pro != GEMV_PLAIN || a.row_base) return -1;
+        return launch_gemv_ksplit(a, quant, M, s);
+    }
+    KernelFn f = pick(quant, M, a.epi, a.pro);
+    if (!f) return -1;
+    const int G = groups_for(a.N);
+    const int rows_per_block = a.epi == GEMV_SWIGLU ? 8 * G : 16 * G;
+    const int n_out = a.epi == GEMV_SWIGLU ? a.inter : a.N;
+    dim3 grid((n_out + rows_per_block - 1) / rows_per_block);
+    const size_t lds = (size_t)M * K4p * 16 + (size_t)M * (a.K / 16) * 4;
+    hipLaunchKernelGGL(f, grid, dim3(kThreads), lds, s, a, G);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -11,23 +11,37 @@ namespace snl {
 
 // ---------------------------------------------------------------- GEMV (gemv.hip)
 enum GemvEpi { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_MHC = 2, GEMV_SWIGLU = 3 };
+// Prologue applied to the token rows before the product: none, RMSNorm (1 + w) of stream 0, or
+// the mHC pre-mix of both streams (coefficients from the router dots + Sinkhorn) then RMSNorm.
+enum GemvPro { GEMV_PLAIN = 0, GEMV_NORM = 1, GEMV_NORM_MHC = 2 };
 
 struct GemvArgs {
     const void* wq;      // quants [N, K] (Q8) or [N, K/2] (Q4)
     const float* ws;     // scales [N, K/32]
-    const float* x;      // token rows, x_stride floats apart (16-byte aligned, stride % 4 == 0)
-    int x_stride;
+    const float* x;      // token row m at x + (row0 + m) * x_stride, row0 = row_base ? *row_base : 0
+    int x_stride;        //   (16-byte aligned, stride % 4 == 0; NORM_MHC: stream 1 at +K)
+    const int32_t* row_base;
     float* y;            // STORE: y[m*y_stride + n_off + n]; ADD/MHC: residual rows (stream 0 at +0,
     int y_stride;        //   stream 1 at +h); SWIGLU: act[m*y_stride + i]
     int N, K;
     int n_off;
     int epi;
-    const float* coef;   // MHC: [M, 8] router coefficients
+    const float* coef;   // MHC epilogue: [M, 8] router coefficients
     int merge_mode;      // MHC: 1 mix, 2 mix then collapse to the mean
     int h;               // MHC: offset of stream 1
     int inter;           // SWIGLU: intermediate size (N == 2*inter; gate rows then up rows)
+    int pro;             // GemvPro
+    const float* norm_w; // NORM*: weights w of the (1 + w) RMSNorm [K]
+    float eps;
+    const float* mhc_raw;  // NORM_MHC: router dots [M][9] (8 dots, sum of squares)
+    const float* mhc_w;    // NORM_MHC: router [8][2K] then bias[8]
+    float* coef_out;       // NORM_MHC: block 0 stores the token coefficients [M][8] here
+    int iterations;        // NORM_MHC: Sinkhorn iterations
 };
 int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s);
+int launch_gemv_ksplit(const GemvArgs& a, int quant, int M, hipStream_t s);
+// Set the LDS limit of every streaming-GEMV instantiation (call once, outside graph capture).
+int gemv_init();
 
 // ---------------------------------------------------------------- layers (layers.hip)
 // x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790)
@@ -54,8 +68,8 @@ struct NormArgs {
 };
 int launch_branch_norm(const NormArgs& a, hipStream_t s);
 
-// mHC router: raw[m][0..8] then coef[m][0..7] (layers.wgsl:75-126)
-int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s);
+// mHC router dots: raw[m][0..7] = router rows . [x0, x1], raw[m][8] = sum of squares (layers.wgsl:75-92)
+int launch_mhc_dots(const float* x, const float* w, float* raw, int h, int M, hipStream_t s);
 
 // x[m, h + i] = x[m, i] (merge mode 3, layers.wgsl:146-149)
 int launch_expand(float* x, int h, int M, hipStream_t s);
@@ -101,15 +115,16 @@ struct AttnArgs {
     uint16_t* vcache;
     const float* norms;  // q_norm[256] | k_norm[256]
     float* out;          // [M, n_heads*256]
-    float* partial;      // [M, n_heads, kMaxParts, 258]
+    float* partial;      // [M, n_heads, ceil(ctx / 64), 258] split-K partials
     int n_heads, n_kv, rot_dim;
     float rope_theta, eps, scale;
     uint32_t mrope;
     int ctx;
     const StepDev* step;  // pos0, rpos
 };
-constexpr int kMaxParts = 64;
+// prep + attend + combine for M = 1 or 2 tokens
 int launch_attention(const AttnArgs& a, int M, hipStream_t s);
+constexpr int kAttnPart = 64;  // keys per split-K part
 
 // ---------------------------------------------------------------- seeded initialiser (init.hip)
 int launch_gen_matrix(uint64_t key, int64_t rows, int64_t cols, float stdv, int quant, void* q, float* sc,

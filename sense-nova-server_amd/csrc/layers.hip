@@ -30,87 +30,73 @@ __global__ __launch_bounds__(256) void branch_norm_kernel(NormArgs a) {
     __shared__ float red[8];
     const int r = blockIdx.x;
     const int row = a.first + r + (a.row_base ? *a.row_base : 0);
-    const float* xb = a.x + (size_t)row * a.x_stride;
+    const float4* x0 = reinterpret_cast<const float4*>(a.x + (size_t)row * a.x_stride);
     float pre0 = 1.0f, pre1 = 0.0f;
     if (a.mode == 1) {
         pre0 = a.coef[(a.first + r) * 8];
         pre1 = a.coef[(a.first + r) * 8 + 1];
     }
-    constexpr int kMaxPer = 32;  // h <= 8192
-    float v[kMaxPer];
+    constexpr int kMaxPer = 8;  // h <= 8192: 2048 float4 over 256 threads
+    const int h4 = a.h >> 2;
+    float4 v[kMaxPer];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < kMaxPer; ++j) {
         const int i = threadIdx.x + 256 * j;
-        float t = 0.0f;
-        if (i < a.h) {
-            t = pre0 * xb[i];
-            if (a.mode == 1) t = t + pre1 * xb[a.h + i];
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i < h4) {
+            t = x0[i];
+            if (a.mode == 1) {
+                const float4 u = x0[h4 + i];
+                t.x = pre0 * t.x + pre1 * u.x;
+                t.y = pre0 * t.y + pre1 * u.y;
+                t.z = pre0 * t.z + pre1 * u.z;
+                t.w = pre0 * t.w + pre1 * u.w;
+            }
         }
         v[j] = t;
-        ss = fmaf(t, t, ss);
+        ss = fmaf(t.x, t.x, ss);
+        ss = fmaf(t.y, t.y, ss);
+        ss = fmaf(t.z, t.z, ss);
+        ss = fmaf(t.w, t.w, ss);
     }
     const float total = block_sum<256>(ss, red);
     const float rinv = 1.0f / sqrtf(total / (float)a.h + a.eps);
-    float* ob = a.out + (size_t)r * a.out_stride;
+    float4* ob = reinterpret_cast<float4*>(a.out + (size_t)r * a.out_stride);
+    const float4* w4 = reinterpret_cast<const float4*>(a.w);
 #pragma unroll
     for (int j = 0; j < kMaxPer; ++j) {
         const int i = threadIdx.x + 256 * j;
-        if (i < a.h) ob[i] = (v[j] * rinv) * (a.one + a.w[i]);
+        if (i < h4) {
+            const float4 w = w4[i];
+            float4 o;
+            o.x = (v[j].x * rinv) * (a.one + w.x);
+            o.y = (v[j].y * rinv) * (a.one + w.y);
+            o.z = (v[j].z * rinv) * (a.one + w.z);
+            o.w = (v[j].w * rinv) * (a.one + w.w);
+            ob[i] = o;
+        }
     }
 }
 
-// layers.wgsl:75-92 mhc_dots: block (o, m).
+// layers.wgsl:75-92 mhc_dots: block (o, m); o < 8 router row o . [x0, x1], o = 8 the sum of squares.
+// The coefficients (layers.wgsl:94-126) are computed by the next GEMV's prologue.
 __global__ __launch_bounds__(256) void mhc_dots_kernel(const float* x, const float* w, float* raw, int h) {
     __shared__ float red[8];
-    const int o = blockIdx.x, m = blockIdx.y, d = 2 * h;
-    const float* xr = x + (size_t)m * d;
+    const int o = blockIdx.x, m = blockIdx.y, d4 = h / 2;  // 2h floats = h/2 float4
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * 2 * h);
+    const float4* wr = reinterpret_cast<const float4*>(w + (size_t)(o < 8 ? o : 0) * 2 * h);
     float acc = 0.0f;
-    if (o < 8) {
-        const float* wr = w + (size_t)o * d;
-        for (int i = threadIdx.x; i < d; i += 256) acc = fmaf(wr[i], xr[i], acc);
-    } else {
-        for (int i = threadIdx.x; i < d; i += 256) acc = fmaf(xr[i], xr[i], acc);
+    for (int i = threadIdx.x; i < d4; i += 256) {
+        const float4 v = xr[i];
+        const float4 u = o < 8 ? wr[i] : v;
+        acc = fmaf(u.x, v.x, acc);
+        acc = fmaf(u.y, v.y, acc);
+        acc = fmaf(u.z, v.z, acc);
+        acc = fmaf(u.w, v.w, acc);
     }
     const float t = block_sum<256>(acc, red);
     if (threadIdx.x == 0) raw[m * 9 + o] = t;
-}
-
-__device__ __forceinline__ float lse2(float a, float b) {
-    const float mx = fmaxf(a, b);
-    return mx + logf(expf(a - mx) + expf(b - mx));
-}
-
-// layers.wgsl:94-126 mhc_finish: one thread per token.
-__global__ void mhc_finish_kernel(const float* raw, const float* w, float* coef, int h, int M, int iterations) {
-    const int m = threadIdx.x;
-    if (m >= M) return;
-    const int d = 2 * h;
-    const float rinv = 1.0f / sqrtf(raw[m * 9 + 8] / (float)d + 1e-6f);
-    float lg[8];
-    for (int o = 0; o < 8; ++o) lg[o] = raw[m * 9 + o] * rinv + w[(size_t)8 * d + o];
-    float a = lg[4], b = lg[5], c = lg[6], e = lg[7];
-    for (int it = 0; it < iterations; ++it) {
-        const float r0 = lse2(a, b), r1 = lse2(c, e);
-        a -= r0;
-        b -= r0;
-        c -= r1;
-        e -= r1;
-        const float c0 = lse2(a, c), c1 = lse2(b, e);
-        a -= c0;
-        c -= c0;
-        b -= c1;
-        e -= c1;
-    }
-    float* cb = coef + m * 8;
-    cb[0] = 1.0f / (1.0f + expf(-lg[0]));
-    cb[1] = 1.0f / (1.0f + expf(-lg[1]));
-    cb[2] = 2.0f / (1.0f + expf(-lg[2]));
-    cb[3] = 2.0f / (1.0f + expf(-lg[3]));
-    cb[4] = expf(a);
-    cb[5] = expf(b);
-    cb[6] = expf(c);
-    cb[7] = expf(e);
 }
 
 __global__ __launch_bounds__(256) void expand_kernel(float* x, int h, int M) {
@@ -258,15 +244,14 @@ int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int voc
 }
 
 int launch_branch_norm(const NormArgs& a, hipStream_t s) {
-    if (a.count < 1 || a.h > 8192 || a.h < 1) return -1;
+    if (a.count < 1 || a.h > 8192 || a.h < 4 || a.h % 4 || a.x_stride % 4 || a.out_stride % 4) return -1;
     hipLaunchKernelGGL(branch_norm_kernel, dim3(a.count), dim3(256), 0, s, a);
     return last_error();
 }
 
-int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s) {
-    if (M < 1 || M > 64) return -1;
+int launch_mhc_dots(const float* x, const float* w, float* raw, int h, int M, hipStream_t s) {
+    if (M < 1 || M > 64 || h % 2) return -1;
     hipLaunchKernelGGL(mhc_dots_kernel, dim3(9, M), dim3(256), 0, s, x, w, raw, h);
-    hipLaunchKernelGGL(mhc_finish_kernel, dim3(1), dim3(64), 0, s, raw, w, coef, h, M, iterations);
     return last_error();
 }
 

@@ -203,7 +203,7 @@ def test_attention_matches_oracle(torch_cuda, K, oracle, n_heads, n_kv, m, pos0)
     dk, dv = _dev(torch, kc.view(np.int16)), _dev(torch, vc.view(np.int16))
     qbuf = torch.zeros((m, n_heads * 256), dtype=torch.float32, device="cuda")
     out = torch.zeros((m, n_heads * 256), dtype=torch.float32, device="cuda")
-    partial = torch.zeros(m * n_heads * ((ctx + 127) // 128) * 258, dtype=torch.float32, device="cuda")
+    partial = torch.zeros(m * n_heads * ((ctx + 63) // 64) * 258, dtype=torch.float32, device="cuda")
     K.attention(_dev(torch, proj), stride, qbuf, dk, dv, _dev(torch, norms), out, partial, n_heads, n_kv, 64, 1e7,
                 1e-6, (11, 11, 10), ctx, m, pos0, rpos[:, :3])
     torch.cuda.synchronize()
@@ -232,7 +232,7 @@ def test_attention_rows_independent_of_m(torch_cuda, K):
         dk, dv = _dev(torch, kc.view(np.int16)), _dev(torch, vc.view(np.int16))
         qbuf = torch.zeros((m, n_heads * 256), dtype=torch.float32, device="cuda")
         out = torch.zeros((m, n_heads * 256), dtype=torch.float32, device="cuda")
-        partial = torch.zeros(m * n_heads * ((ctx + 127) // 128) * 258, dtype=torch.float32, device="cuda")
+        partial = torch.zeros(m * n_heads * ((ctx + 63) // 64) * 258, dtype=torch.float32, device="cuda")
         rpos = np.array([[pos0 + i] * 3 for i in range(m)], np.uint32)
         K.attention(_dev(torch, proj[:m]), stride, qbuf, dk, dv, _dev(torch, norms), out, partial, n_heads, n_kv, 64,
                     1e7, 1e-6, (11, 11, 10), ctx, m, pos0, rpos)
