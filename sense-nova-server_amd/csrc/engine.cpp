@@ -20,6 +20,7 @@
 
 #include "../../include/snl.h"
 #include "kernels.h"
+#include "packing.h"
 
 namespace snl {
 
@@ -61,6 +62,8 @@ struct QW {
     void* q = nullptr;
     float* s = nullptr;
     int rows = 0, cols = 0, quant = 0;
+    bool packed = false;  // tile order (packing.h); otherwise the reference's row-major layout
+    int inter = 0;        // packed with SwiGLU pairing of gate/up rows when > 0
 };
 
 struct Vec {
@@ -87,6 +90,10 @@ struct snl_engine {
     uint64_t seed = 0;
     hipStream_t stream = nullptr;
     std::vector<void*> allocs;
+    // reference-layout staging of one matrix while the weights are drawn and packed (init only)
+    uint8_t* gen_tmp_q = nullptr;
+    float* gen_tmp_s = nullptr;
+    size_t gen_tmp_n = 0;
 
     QW embed, lm_head;
     Vec final_norm;
@@ -165,19 +172,57 @@ struct snl_engine {
         return SNL_OK;
     }
 
-    int gen_q(QW& w, int layer, int kind, int rows, int cols, int qt) {
+    // Draw a rows x cols quantised matrix (reference layout, src/weights.rs:48-55).  GEMV matrices
+    // (pack_inter >= 0) are then stored in tile order; pack_inter > 0 pairs gate and up rows.
+    int gen_q(QW& w, int layer, int kind, int rows, int cols, int qt, int pack_inter = 0) {
         w.rows = rows;
         w.cols = cols;
         w.quant = qt;
         const size_t n = (size_t)rows * cols;
+        const uint64_t key = stream_key(seed, layer, kind);
+        int rc;
+        if (pack_inter < 0) {
+            uint8_t* q;
+            if ((rc = dalloc(&q, qt == 0 ? n : n / 2))) return rc;
+            w.q = q;
+            if ((rc = dalloc(&w.s, n / 32))) return rc;
+            if (launch_gen_matrix(key, rows, cols, 0.02f, qt, w.q, w.s, stream))
+                return fail(SNL_EDEVICE, "weight init launch failed");
+            return SNL_OK;
+        }
+        PackGeom g;
+        if (!pack_geom(qt, rows, cols, pack_inter, &g))
+            return fail(SNL_EARG, "a %d x %d GEMV matrix needs K %% 128 == 0", rows, cols);
+        if (n > gen_tmp_n) {
+            if (hipStreamSynchronize(stream) != hipSuccess) return fail(SNL_EDEVICE, "weight init failed");
+            hipFree(gen_tmp_q);
+            hipFree(gen_tmp_s);
+            gen_tmp_q = nullptr;
+            gen_tmp_s = nullptr;
+            gen_tmp_n = 0;
+            if (hipMalloc((void**)&gen_tmp_q, n) != hipSuccess || hipMalloc((void**)&gen_tmp_s, n / 32 * 4) != hipSuccess)
+                return fail(SNL_ENOMEM, "hipMalloc of the %zu-byte weight staging buffer failed", n);
+            gen_tmp_n = n;
+        }
         uint8_t* q;
-        int rc = dalloc(&q, qt == 0 ? n : n / 2);
-        if (rc) return rc;
+        if ((rc = dalloc(&q, g.q_bytes))) return rc;
         w.q = q;
-        if ((rc = dalloc(&w.s, n / 32))) return rc;
-        if (launch_gen_matrix(stream_key(seed, layer, kind), rows, cols, 0.02f, qt, w.q, w.s, stream))
+        if ((rc = dalloc(&w.s, g.s_floats))) return rc;
+        w.packed = true;
+        w.inter = pack_inter;
+        if (launch_gen_matrix(key, rows, cols, 0.02f, qt, gen_tmp_q, gen_tmp_s, stream) ||
+            launch_pack_matrix(g, gen_tmp_q, gen_tmp_s, w.q, w.s, stream))
             return fail(SNL_EDEVICE, "weight init launch failed");
         return SNL_OK;
+    }
+
+    void free_gen_tmp() {
+        if (gen_tmp_q || gen_tmp_s) hipStreamSynchronize(stream);
+        hipFree(gen_tmp_q);
+        hipFree(gen_tmp_s);
+        gen_tmp_q = nullptr;
+        gen_tmp_s = nullptr;
+        gen_tmp_n = 0;
     }
 
     int gen_v(Vec& v, int layer, int kind, int n, int vkind, float stdv, int aux0 = 0, int aux1 = 0) {
@@ -196,12 +241,12 @@ struct snl_engine {
     int record_mtp(int M, int draft);
     int run(int kind, int M, int a, int b);
     // GEMV with an optional fused branch-input prologue (pro: GEMV_NORM with norm weights nw, or
-    // GEMV_NORM_MHC with router mw whose dots are in mhc_raw) and the epilogue `epi`.
+    // GEMV_NORM_MHC, whose pre-mix coefficients launch_mhc left in coef) and the epilogue `epi`.
     int gemv(const char* name, const QW& w, const float* xin, int x_stride, float* y, int y_stride, int M, int epi,
-             int merge_mode = 0, int pro = GEMV_PLAIN, const float* nw = nullptr, const float* mw = nullptr,
-             const int32_t* row_base = nullptr) {
+             int merge_mode = 0, int pro = GEMV_PLAIN, const float* nw = nullptr, const int32_t* row_base = nullptr) {
         mark(name, gemv_bytes(w, M, epi, cfg.intermediate));
         GemvArgs g{};
+        g.packed = w.packed ? 1 : 0;
         g.wq = w.q;
         g.ws = w.s;
         g.x = xin;
@@ -219,10 +264,6 @@ struct snl_engine {
         g.pro = pro;
         g.norm_w = nw;
         g.eps = cfg.eps;
-        g.mhc_raw = mhc_raw;
-        g.mhc_w = mw;
-        g.coef_out = coef;
-        g.iterations = cfg.mhc_iterations;
         return launch_gemv(g, w.quant, M, stream);
     }
     int norm(const float* xin, int x_stride, const int32_t* row_base, int mode, const float* w, float* out,
@@ -313,8 +354,8 @@ int snl_engine::init() {
     if (gemv_init()) return fail(SNL_EDEVICE, "GEMV LDS configuration failed");
     int rc;
     // ---- weights (convert.rs:228-311 layout; seeded values) ----
-    if ((rc = gen_q(embed, -1, K_EMBED, c.vocab, h, 0))) return rc;
     if ((rc = gen_q(lm_head, -1, K_LM_HEAD, c.vocab, h, 0))) return rc;
+    if ((rc = gen_q(embed, -1, K_EMBED, c.vocab, h, 0, -1))) return rc;  // gathered by row
     if ((rc = gen_v(final_norm, -1, K_NORM, h, 0, 0.1f))) return rc;
     layers.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; ++l) {
@@ -332,7 +373,7 @@ int snl_engine::init() {
             if ((rc = gen_q(L.mix_in, l, K_IN_PROJ, lin_proj_rows, h, 0))) return rc;
             if ((rc = gen_q(L.mix_out, l, K_OUT_PROJ, h, lin_value_dim, quant))) return rc;
         }
-        if ((rc = gen_q(L.gate_up, l, K_GATE_UP, 2 * c.intermediate, h, quant))) return rc;
+        if ((rc = gen_q(L.gate_up, l, K_GATE_UP, 2 * c.intermediate, h, quant, c.intermediate))) return rc;
         if ((rc = gen_q(L.down, l, K_DOWN, h, c.intermediate, quant))) return rc;
         if (is_mhc(l)) {
             if ((rc = gen_v(L.mhc_attn, l, K_MHC_ATTN, 16 * h + 8, 3, 0.0f, h))) return rc;
@@ -345,7 +386,7 @@ int snl_engine::init() {
         if ((rc = gen_q(fc_h, L, K_FC_H, h, h, 0))) return rc;
         if ((rc = gen_q(m_qkv, L, K_QKV, attn_proj_rows, h, 0))) return rc;
         if ((rc = gen_q(m_o, L, K_O_PROJ, h, q_dim, 0))) return rc;
-        if ((rc = gen_q(m_gate_up, L, K_GATE_UP, 2 * c.intermediate, h, 0))) return rc;
+        if ((rc = gen_q(m_gate_up, L, K_GATE_UP, 2 * c.intermediate, h, 0, c.intermediate))) return rc;
         if ((rc = gen_q(m_down, L, K_DOWN, h, c.intermediate, 0))) return rc;
         if ((rc = gen_v(norm_e, L, K_NORM_E, h, 0, 0.1f))) return rc;
         if ((rc = gen_v(norm_h, L, K_NORM_H, h, 0, 0.1f))) return rc;
@@ -354,6 +395,7 @@ int snl_engine::init() {
         if ((rc = gen_v(m_post_ln, L, K_POST_LN, h, 0, 0.1f))) return rc;
         if ((rc = gen_v(m_qk_norm, L, K_QK_NORM, 2 * c.head_dim, 0, 0.1f))) return rc;
     }
+    free_gen_tmp();
 
     // ---- activations (src/engine.rs:244-256), sized for kMaxM rows ----
     const int proj_w = std::max(std::max(2 * c.intermediate, lin_proj_rows), attn_proj_rows);
@@ -427,21 +469,19 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
         }
         // branch input: RMSNorm (1 + in_ln) of stream 0, or of the mHC pre-mix, fused into the GEMV
         if (mhc) {
-            mark("mhc_dots", 0.0);
-            rc |= launch_mhc_dots(x, L.mhc_attn.p, mhc_raw, h, M, stream);
+            mark("mhc", 0.0);
+            rc |= launch_mhc(x, L.mhc_attn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
         }
         const int pro = mhc ? GEMV_NORM_MHC : GEMV_NORM;
         if (L.full) {
-            rc |= gemv("gemv_qkv", L.mix_in, x, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p,
-                       L.mhc_attn.p);
+            rc |= gemv("gemv_qkv", L.mix_in, x, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p);
             AttnArgs a = attn_args(d_step, kcache + kvn * fslot, vcache + kvn * fslot, L.small.p);
             mark("attention", 0.0);
             rc |= launch_attention(a, M, stream);
             rc |= gemv("gemv_o", L.mix_out, attn_out, q_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, 1);
             ++fslot;
         } else {
-            rc |= gemv("gemv_in_proj", L.mix_in, x, 2 * h, proj, lin_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p,
-                       L.mhc_attn.p);
+            rc |= gemv("gemv_in_proj", L.mix_in, x, 2 * h, proj, lin_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p);
             DeltaArgs d{};
             d.proj = proj;
             d.proj_stride = lin_proj_rows;
@@ -463,11 +503,10 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             ++lslot;
         }
         if (mhc) {
-            mark("mhc_dots", 0.0);
-            rc |= launch_mhc_dots(x, L.mhc_ffn.p, mhc_raw, h, M, stream);
+            mark("mhc", 0.0);
+            rc |= launch_mhc(x, L.mhc_ffn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
         }
-        rc |= gemv("gemv_gate_up", L.gate_up, x, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, pro, L.post_ln.p,
-                   L.mhc_ffn.p);
+        rc |= gemv("gemv_gate_up", L.gate_up, x, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, pro, L.post_ln.p);
         const int mode = !mhc ? 0 : (li + 1 == c.mhc_end ? 2 : 1);
         rc |= gemv("gemv_down", L.down, act, c.intermediate, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, mode);
     }
@@ -491,7 +530,7 @@ int snl_engine::record_mtp(int M, int draft) {
     // x = fc_e(norm_e(emb)) + fc_h(norm_h(hid[r0..])); fc_e reads xn, since it writes mx
     rc |= norm(mx, 2 * h, nullptr, 0, norm_e.p, xn, 0, M);
     rc |= gemv("gemv_fc_e", fc_e, xn, h, mx, 2 * h, M, GEMV_STORE);
-    rc |= gemv("gemv_fc_h", fc_h, hid, h, mx, 2 * h, M, GEMV_ADD, 0, GEMV_NORM, norm_h.p, nullptr, &d_mstep->r0);
+    rc |= gemv("gemv_fc_h", fc_h, hid, h, mx, 2 * h, M, GEMV_ADD, 0, GEMV_NORM, norm_h.p, &d_mstep->r0);
     rc |= gemv("gemv_mtp_qkv", m_qkv, mx, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, GEMV_NORM, m_in_ln.p);
     AttnArgs a = attn_args(d_mstep, m_kc, m_vc, m_qk_norm.p);
     mark("attention", 0.0);
@@ -578,6 +617,7 @@ void snl_engine_destroy(snl_engine* e) {
     if (!e) return;
     if (e->stream) hipStreamSynchronize(e->stream);
     for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
+    e->free_gen_tmp();
     for (void* p : e->allocs) hipFree(p);
     if (e->h_picks) hipHostFree(e->h_picks);
     if (e->h_step) hipHostFree(e->h_step);
@@ -981,7 +1021,7 @@ int snl_generate(snl_engine* e, const uint32_t* prompt, int n, int max_tokens, i
 
 // ---- inspection ----
 static const void* find_tensor(const snl_engine* e, int layer, int kind, int* type, int* rows, int* cols,
-                               const float** scales) {
+                               const float** scales, const QW** qw = nullptr) {
     const QW* w = nullptr;
     const Vec* v = nullptr;
     if (layer == -1) {
@@ -1026,6 +1066,7 @@ static const void* find_tensor(const snl_engine* e, int layer, int kind, int* ty
         *rows = w->rows;
         *cols = w->cols;
         *scales = w->s;
+        if (qw) *qw = w;
         return w->q;
     }
     if (v) {
@@ -1048,9 +1089,35 @@ int snl_tensor_info(const snl_engine* e, int layer, int kind, int* rows, int* co
 int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s) {
     int type, rows, cols;
     const float* sp;
-    const void* qp = find_tensor(e, layer, kind, &type, &rows, &cols, &sp);
+    const QW* w = nullptr;
+    const void* qp = find_tensor(e, layer, kind, &type, &rows, &cols, &sp, &w);
     if (!qp || !q) return SNL_EARG;
+    if (hipStreamSynchronize(e->stream) != hipSuccess) return SNL_EDEVICE;
     const size_t n = (size_t)rows * cols;
+    if (w && w->packed) {  // tile order -> the reference's row-major quants and scales
+        PackGeom g;
+        if (!pack_geom(w->quant, rows, cols, w->inter, &g)) return SNL_EDEVICE;
+        std::vector<uint8_t> hq(g.q_bytes);
+        std::vector<float> hs(g.s_floats);
+        if (hipMemcpy(hq.data(), qp, g.q_bytes, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(hs.data(), sp, g.s_floats * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return SNL_EDEVICE;
+        uint8_t* qo = static_cast<uint8_t*>(q);
+        for (int T = 0; T < g.tiles; ++T)
+            for (int S = 0; S < g.nss; ++S)
+                for (int lane = 0; lane < 64; ++lane) {
+                    const int row = pack_row(g, T, lane & 15);
+                    if (row < 0) continue;
+                    for (int v = 0; v < g.NI; ++v)
+                        std::memcpy(qo + (size_t)row * g.row_bytes + pack_row_offset(g, S, v, lane >> 4),
+                                    hq.data() + pack_piece(g, T, S, v, lane), 16);
+                    if (s)
+                        for (int u = 0; u < g.U; ++u)
+                            s[(size_t)row * (cols / 32) + 4 * g.U * S + g.U * (lane >> 4) + u] =
+                                hs[pack_scale(g, T, S, lane) + u];
+                }
+        return SNL_OK;
+    }
     const size_t qb = type == 0 ? n : (type == 1 ? n / 2 : n * 4);
     if (hipMemcpy(q, qp, qb, hipMemcpyDeviceToHost) != hipSuccess) return SNL_EDEVICE;
     if (type != 2 && s && hipMemcpy(s, sp, n / 32 * 4, hipMemcpyDeviceToHost) != hipSuccess) return SNL_EDEVICE;
@@ -1105,6 +1172,7 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
         return SNL_EARG;
     static const int init_rc = gemv_init();
     if (init_rc) return SNL_EDEVICE;
+    hipStream_t st = (hipStream_t)stream;
     GemvArgs g{};
     g.wq = wq;
     g.ws = ws;
@@ -1115,7 +1183,33 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
     g.N = N;
     g.K = K;
     g.epi = GEMV_STORE;
-    int rc = launch_gemv(g, quant, M, (hipStream_t)stream);
+    // The engine's kernel reads tile order: pack the caller's reference-layout matrix into a
+    // staging buffer first (held under the lock until the call has finished on the stream).
+    static uint8_t* pq = nullptr;
+    static float* ps = nullptr;
+    static size_t cap_q = 0, cap_s = 0;
+    std::lock_guard<std::mutex> lk(g_kstep_mu);
+    PackGeom pg;
+    if (pack_geom(quant, N, K, 0, &pg) && M >= 1 && M <= SNL_MAX_M && mgemv_fits(M, K)) {
+        if (pg.q_bytes > cap_q || pg.s_floats > cap_s) {
+            if (hipStreamSynchronize(st) != hipSuccess) return SNL_EDEVICE;
+            hipFree(pq);
+            hipFree(ps);
+            pq = nullptr;
+            ps = nullptr;
+            cap_q = cap_s = 0;
+            if (hipMalloc((void**)&pq, pg.q_bytes) != hipSuccess || hipMalloc((void**)&ps, pg.s_floats * 4) != hipSuccess)
+                return SNL_ENOMEM;
+            cap_q = pg.q_bytes;
+            cap_s = pg.s_floats;
+        }
+        if (launch_pack_matrix(pg, wq, ws, pq, ps, st)) return SNL_EDEVICE;
+        g.packed = 1;
+        g.wq = pq;
+        g.ws = ps;
+    }
+    int rc = launch_gemv(g, quant, M, st);
+    if (rc == 0 && g.packed && hipStreamSynchronize(st) != hipSuccess) rc = -2;
     return rc == -1 ? SNL_EARG : (rc ? SNL_EDEVICE : SNL_OK);
 }
 

@@ -109,15 +109,10 @@ __device__ __forceinline__ int lds_f4(int k4) {  // k4 = k / 4
     return (c << 8) + (v << 6) + l;
 }
 
-__device__ __forceinline__ float lse2(float a, float b) {
-    const float mx = fmaxf(a, b);
-    return mx + __logf(__expf(a - mx) + __expf(b - mx));
-}
-
 template <int QT, int M, int EPI, int PRO>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
     extern __shared__ float4 lds4[];
-    __shared__ float coef_s[SNL_MAX_M][8];
+    __shared__ float coef_s[SNL_MAX_M][2];
     __shared__ float red_s[kWaves][SNL_MAX_M];
     const int K = a.K, K4 = K >> 2, K16 = K >> 4;
     const int nchunks = (K + kChunk - 1) / kChunk;
@@ -137,41 +132,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
     // ---- prologue: stage the token rows (optionally normalised) in LDS ----
     const int row0 = a.row_base ? *a.row_base : 0;
     if constexpr (PRO == GEMV_NORM_MHC) {
-        // router logits -> pre/post/mix coefficients (layers.wgsl:94-126), one thread per token
-        if (tid < M) {
-            const int m = tid, d = 2 * K;
-            const float* raw = a.mhc_raw + m * 9;
-            const float rinv = 1.0f / sqrtf(raw[8] / (float)d + 1e-6f);
-            float lg[8];
-#pragma unroll
-            for (int o = 0; o < 8; ++o) lg[o] = raw[o] * rinv + a.mhc_w[(size_t)8 * d + o];
-            float p = lg[4], q = lg[5], u = lg[6], v = lg[7];
-            for (int it = 0; it < a.iterations; ++it) {
-                const float r0 = lse2(p, q), r1 = lse2(u, v);
-                p -= r0;
-                q -= r0;
-                u -= r1;
-                v -= r1;
-                const float c0 = lse2(p, u), c1 = lse2(q, v);
-                p -= c0;
-                u -= c0;
-                q -= c1;
-                v -= c1;
-            }
-            float cf[8];
-            cf[0] = 1.0f / (1.0f + __expf(-lg[0]));
-            cf[1] = 1.0f / (1.0f + __expf(-lg[1]));
-            cf[2] = 2.0f / (1.0f + __expf(-lg[2]));
-            cf[3] = 2.0f / (1.0f + __expf(-lg[3]));
-            cf[4] = __expf(p);
-            cf[5] = __expf(q);
-            cf[6] = __expf(u);
-            cf[7] = __expf(v);
-#pragma unroll
-            for (int o = 0; o < 8; ++o) {
-                coef_s[m][o] = cf[o];
-                if (blk == 0) a.coef_out[m * 8 + o] = cf[o];
-            }
+        if (tid < 2 * M) {
+            coef_s[tid][0] = tid < M ? a.coef[tid * 8] : 0.0f;
+            coef_s[tid][1] = tid < M ? a.coef[tid * 8 + 1] : 0.0f;
         }
         __syncthreads();
     }
@@ -415,13 +378,17 @@ int gemv_init() {
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
                         return -2;
                 }
-    return 0;
+    return mgemv_init();
 }
 
 int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if (M < 1 || M > SNL_MAX_M || a.K % 32 != 0 || a.K <= 0 || a.N <= 0 || (quant != 0 && quant != 1)) return -1;
     if (a.epi == GEMV_SWIGLU && a.N != 2 * a.inter) return -1;
     if (a.pro != GEMV_PLAIN && a.K % 4) return -1;
+    if (a.packed) {
+        const int rc = launch_mgemv(a, quant, M, s);
+        return rc == 1 ? -1 : rc;
+    }
     const int K4p = (a.K + kChunk - 1) / kChunk * (kChunk / 4);
     if ((size_t)M * K4p * 4 > (size_t)kLdsFloats) {
         if (a.pro != GEMV_PLAIN || a.row_base) return -1;

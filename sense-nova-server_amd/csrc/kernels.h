@@ -12,12 +12,14 @@ namespace snl {
 // ---------------------------------------------------------------- GEMV (gemv.hip)
 enum GemvEpi { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_MHC = 2, GEMV_SWIGLU = 3 };
 // Prologue applied to the token rows before the product: none, RMSNorm (1 + w) of stream 0, or
-// the mHC pre-mix of both streams (coefficients from the router dots + Sinkhorn) then RMSNorm.
+// the mHC pre-mix pre0*x0 + pre1*x1 of both streams (pre from coef, written by launch_mhc) then
+// RMSNorm.
 enum GemvPro { GEMV_PLAIN = 0, GEMV_NORM = 1, GEMV_NORM_MHC = 2 };
 
 struct GemvArgs {
-    const void* wq;      // quants [N, K] (Q8) or [N, K/2] (Q4)
-    const float* ws;     // scales [N, K/32]
+    const void* wq;      // quants [N, K] (Q8) or [N, K/2] (Q4), or tile order when packed
+    const float* ws;     // scales [N, K/32], or tile order when packed
+    int packed;          // 1: wq/ws in the tile order of packing.h (matrix-core kernel)
     const float* x;      // token row m at x + (row0 + m) * x_stride, row0 = row_base ? *row_base : 0
     int x_stride;        //   (16-byte aligned, stride % 4 == 0; NORM_MHC: stream 1 at +K)
     const int32_t* row_base;
@@ -26,20 +28,22 @@ struct GemvArgs {
     int N, K;
     int n_off;
     int epi;
-    const float* coef;   // MHC epilogue: [M, 8] router coefficients
+    const float* coef;   // [M, 8] mHC token coefficients (MHC epilogue; NORM_MHC prologue: pre0, pre1)
     int merge_mode;      // MHC: 1 mix, 2 mix then collapse to the mean
     int h;               // MHC: offset of stream 1
     int inter;           // SWIGLU: intermediate size (N == 2*inter; gate rows then up rows)
     int pro;             // GemvPro
     const float* norm_w; // NORM*: weights w of the (1 + w) RMSNorm [K]
     float eps;
-    const float* mhc_raw;  // NORM_MHC: router dots [M][9] (8 dots, sum of squares)
-    const float* mhc_w;    // NORM_MHC: router [8][2K] then bias[8]
-    float* coef_out;       // NORM_MHC: block 0 stores the token coefficients [M][8] here
-    int iterations;        // NORM_MHC: Sinkhorn iterations
 };
 int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s);
 int launch_gemv_ksplit(const GemvArgs& a, int quant, int M, hipStream_t s);
+// Matrix-core path (mgemv.hip) over tile-order weights: 0 launched, 1 not served (M too large for
+// LDS at this K), < 0 error.
+int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s);
+// whether launch_mgemv serves M token rows at this K (the staged rows fit in LDS)
+bool mgemv_fits(int M, int K);
+int mgemv_init();
 // Set the LDS limit of every streaming-GEMV instantiation (call once, outside graph capture).
 int gemv_init();
 
@@ -68,8 +72,10 @@ struct NormArgs {
 };
 int launch_branch_norm(const NormArgs& a, hipStream_t s);
 
-// mHC router dots: raw[m][0..7] = router rows . [x0, x1], raw[m][8] = sum of squares (layers.wgsl:75-92)
-int launch_mhc_dots(const float* x, const float* w, float* raw, int h, int M, hipStream_t s);
+// mHC router (layers.wgsl:75-126), one block per token: raw[m][0..7] = router rows . [x0, x1],
+// raw[m][8] = sum of squares; coef[m][0..7] = [pre0, pre1, post0, post1, mix00, mix01, mix10,
+// mix11] after `iterations` log-space Sinkhorn steps.
+int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s);
 
 // x[m, h + i] = x[m, i] (merge mode 3, layers.wgsl:146-149)
 int launch_expand(float* x, int h, int M, hipStream_t s);

@@ -79,24 +79,76 @@ __global__ __launch_bounds__(256) void branch_norm_kernel(NormArgs a) {
     }
 }
 
-// layers.wgsl:75-92 mhc_dots: block (o, m); o < 8 router row o . [x0, x1], o = 8 the sum of squares.
-// The coefficients (layers.wgsl:94-126) are computed by the next GEMV's prologue.
-__global__ __launch_bounds__(256) void mhc_dots_kernel(const float* x, const float* w, float* raw, int h) {
-    __shared__ float red[8];
-    const int o = blockIdx.x, m = blockIdx.y, d4 = h / 2;  // 2h floats = h/2 float4
-    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * 2 * h);
-    const float4* wr = reinterpret_cast<const float4*>(w + (size_t)(o < 8 ? o : 0) * 2 * h);
-    float acc = 0.0f;
-    for (int i = threadIdx.x; i < d4; i += 256) {
-        const float4 v = xr[i];
-        const float4 u = o < 8 ? wr[i] : v;
-        acc = fmaf(u.x, v.x, acc);
-        acc = fmaf(u.y, v.y, acc);
-        acc = fmaf(u.z, v.z, acc);
-        acc = fmaf(u.w, v.w, acc);
+// mHC router of one token per block (layers.wgsl:75-126): the 8 router-row dots with the 2-stream
+// row [x0, x1] and its sum of squares, then the token's coefficients [pre0, pre1, post0, post1,
+// mix00, mix01, mix10, mix11] (2x2 log-space Sinkhorn).  All loads of a batch are issued before
+// their first use.  raw keeps the 9 sums.
+constexpr int kMhcThreads = 1024;
+
+__global__ __launch_bounds__(kMhcThreads) void mhc_kernel(const float* x, const float* w, float* raw, float* coef,
+                                                          int h, int iterations) {
+    __shared__ float red[kMhcThreads / 64][9];
+    __shared__ float tot[9];
+    const int m = blockIdx.x, tid = threadIdx.x, d = 2 * h, d4 = d / 4;
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * d);
+    const float4* wr = reinterpret_cast<const float4*>(w);
+    float acc[9];
+#pragma unroll
+    for (int o = 0; o < 9; ++o) acc[o] = 0.0f;
+    for (int i0 = tid; i0 < d4; i0 += 2 * kMhcThreads) {
+        const int i1 = i0 + kMhcThreads;
+        const bool ok1 = i1 < d4;
+        const float4 v0 = xr[i0], v1 = xr[ok1 ? i1 : i0];
+        float4 u0[8], u1[8];
+#pragma unroll
+        for (int o = 0; o < 8; ++o) {
+            u0[o] = wr[(size_t)o * d4 + i0];
+            u1[o] = wr[(size_t)o * d4 + (ok1 ? i1 : i0)];
+        }
+#pragma unroll
+        for (int o = 0; o < 8; ++o) {
+            acc[o] = fmaf(u0[o].x, v0.x, acc[o]);
+            acc[o] = fmaf(u0[o].y, v0.y, acc[o]);
+            acc[o] = fmaf(u0[o].z, v0.z, acc[o]);
+            acc[o] = fmaf(u0[o].w, v0.w, acc[o]);
+        }
+        acc[8] = fmaf(v0.x, v0.x, acc[8]);
+        acc[8] = fmaf(v0.y, v0.y, acc[8]);
+        acc[8] = fmaf(v0.z, v0.z, acc[8]);
+        acc[8] = fmaf(v0.w, v0.w, acc[8]);
+        if (ok1) {
+#pragma unroll
+            for (int o = 0; o < 8; ++o) {
+                acc[o] = fmaf(u1[o].x, v1.x, acc[o]);
+                acc[o] = fmaf(u1[o].y, v1.y, acc[o]);
+                acc[o] = fmaf(u1[o].z, v1.z, acc[o]);
+                acc[o] = fmaf(u1[o].w, v1.w, acc[o]);
+            }
+            acc[8] = fmaf(v1.x, v1.x, acc[8]);
+            acc[8] = fmaf(v1.y, v1.y, acc[8]);
+            acc[8] = fmaf(v1.z, v1.z, acc[8]);
+            acc[8] = fmaf(v1.w, v1.w, acc[8]);
+        }
     }
-    const float t = block_sum<256>(acc, red);
-    if (threadIdx.x == 0) raw[m * 9 + o] = t;
+#pragma unroll
+    for (int o = 0; o < 9; ++o) acc[o] = wave_sum(acc[o]);
+    if ((tid & 63) == 0)
+#pragma unroll
+        for (int o = 0; o < 9; ++o) red[tid >> 6][o] = acc[o];
+    __syncthreads();
+    if (tid < 9) {
+        float t = 0.0f;
+        for (int wv = 0; wv < kMhcThreads / 64; ++wv) t = t + red[wv][tid];
+        tot[tid] = t;
+        raw[m * 9 + tid] = t;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float cf[8];
+        mhc_coefficients(tot, w, d, iterations, cf);
+#pragma unroll
+        for (int o = 0; o < 8; ++o) coef[m * 8 + o] = cf[o];
+    }
 }
 
 __global__ __launch_bounds__(256) void expand_kernel(float* x, int h, int M) {
@@ -249,9 +301,9 @@ int launch_branch_norm(const NormArgs& a, hipStream_t s) {
     return last_error();
 }
 
-int launch_mhc_dots(const float* x, const float* w, float* raw, int h, int M, hipStream_t s) {
+int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s) {
     if (M < 1 || M > 64 || h % 2) return -1;
-    hipLaunchKernelGGL(mhc_dots_kernel, dim3(9, M), dim3(256), 0, s, x, w, raw, h);
+    hipLaunchKernelGGL(mhc_kernel, dim3(M), dim3(kMhcThreads), 0, s, x, w, raw, coef, h, iterations);
     return last_error();
 }
 

@@ -1,0 +1,485 @@
+// Matrix-core skinny block-quantised GEMV for decode (M = 1..4 token rows), gfx950.
+//
+// y[m, n] = sum_b s[n, b] * sum_{i<32} q[n, 32b + i] * x[m, 32b + i]
+//
+// Weights are the reference's Q8_0 / Q4_0 blocks (src/weights.rs:48-55, src/engine.rs:84-108;
+// Q4_0 nibble i of little-endian word w = element 8w + i) with f32 scales, held in the tile
+// order of packing.h, so that every wave load is one contiguous KiB.
+//
+// The dot products run on v_mfma_f32_16x16x32_f16, which takes the place of the per-element
+// convert-and-FMA of a vector-ALU GEMV (that costs ~3.5 VALU lane-ops per weight byte at M=2,
+// close to the whole VALU budget at full HBM rate).  Both operands are exact:
+//   * quants become f16 exactly: Q8 bytes are xor-ed with 0x80, v_perm pairs each byte with 0x64
+//     (the f16 1024 + byte), and one packed f16 subtract of 1152 leaves q; Q4 nibbles are masked
+//     into the same f16 pattern and 1032 is subtracted;
+//   * each token row x (f32) is split into two f16 parts, hi = f16(x) and lo = f16(x - hi), whose
+//     sum carries 22 significant bits; a per-token power of two keeps hi inside the f16 range.
+// The accumulation is f32 throughout.
+//
+// MFMA orientation.  A (16 x 32) holds x, B (32 x 16) holds 16 weight rows.  The 4 lane groups of
+// B (k-groups) each cover one 16-element half-block, so each lane has one quant block per load.
+// A row i = 4*slot + combo (combo = token-in-pair x {hi, lo}) is non-zero only in the k-group of
+// its slot.  The 16x16 result then leaves lane (row j, group g) with the block dot products of
+// weight row j for the block of group g, one register per combo, and that lane scales them by
+// its own block scale s[j, block] and accumulates.  One MFMA group handles one pair of tokens;
+// M = 3, 4 runs a second A against the same converted B.
+//
+// Work split.  A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows).  A
+// superstep is 128*U elements of a row (U = 4 when K % 512 == 0, else 1), 8 KiB of a Q8 tile;
+// K is cut into KS equal slices of supersteps.  A block of NW = KS*TW waves owns TW tiles and every wave one
+// (tile, slice) item; KS and TW are chosen from the matrix shape alone, never from M.  Loads run
+// one superstep ahead of the MFMAs.  Slices are added in slice order through LDS, so a token's
+// result does not depend on M, on its index or on timing (greedy output is then byte-identical
+// with and without speculative drafting).
+//
+// Prologue (fused branch input, layers.wgsl:46-73 and :94-126): the staged rows are the plain x
+// rows, RMSNorm(x0)*(1+w), or, inside the mHC range, RMSNorm(pre0*x0 + pre1*x1)*(1+w) with the
+// token coefficients left by the router kernel.
+//
+// Epilogues: plain store; residual add into stream 0 (merge mode 0, layers.wgsl:142-145); mHC
+// merge (modes 1/2, layers.wgsl:150-161); SwiGLU (layers.wgsl:164-175).
+#include "common.h"
+#include "kernels.h"
+#include "packing.h"
+
+#pragma clang fp contract(off)
+
+namespace snl {
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxWaves = 8;
+constexpr int kTargetItems = 2048;        // wave items per launch worth splitting K for (8 per CU)
+constexpr int kLdsLimit = 150 * 1024;     // dynamic LDS per block
+constexpr int kZeroBytes = 64;            // zero A fragment read by the lanes outside their slot
+
+template <int EPI>
+__device__ __forceinline__ int tile_row(const GemvArgs& a, int T, int j) {
+    if constexpr (EPI == GEMV_SWIGLU) {
+        const int c = T * 8 + (j & 7);
+        if (c >= a.inter) return -1;
+        return j < 8 ? c : a.inter + c;
+    } else {
+        const int r = T * 16 + j;
+        return r < a.N ? r : -1;
+    }
+}
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+// 8 weights of one 16-byte load as exact f16: MFMA i (0..NM-1) of the load.
+// Q8 order: elements 8i..8i+7.  Q4 order (word i): elements 8i + {0, 4, 1, 5, 2, 6, 3, 7}.
+template <int QT>
+__device__ __forceinline__ half8_t dequant8(const uint4& w, int i) {
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+    if constexpr (QT == 0) {
+        const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+        const uint32_t u0 = wd[2 * i] ^ 0x80808080u, u1 = wd[2 * i + 1] ^ 0x80808080u;
+        const half2_t p0 = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) - bias;
+        const half2_t p1 = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) - bias;
+        const half2_t p2 = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) - bias;
+        const half2_t p3 = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) - bias;
+        return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+    } else {
+        const half2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+        const uint32_t v = wd[i];
+        const half2_t p0 = as_h2((v & 0x000F000Fu) | 0x64006400u) - bias;
+        const half2_t p1 = as_h2(((v >> 4) & 0x000F000Fu) | 0x64006400u) - bias;
+        const half2_t p2 = as_h2(((v >> 8) & 0x000F000Fu) | 0x64006400u) - bias;
+        const half2_t p3 = as_h2(((v >> 12) & 0x000F000Fu) | 0x64006400u) - bias;
+        return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+    }
+}
+
+// position of element e (0..31) of a block inside its staged A fragment
+template <int QT>
+__device__ __forceinline__ int a_pos(int e) {
+    if constexpr (QT == 0) return e;
+    else return (e & ~7) + 2 * (e & 3) + ((e >> 2) & 1);
+}
+
+// QT: 0 Q8_0, 1 Q4_0.  P: token pairs (M <= 2P).  U: quant blocks per lane group per superstep.
+template <int QT, int P, int EPI, int PRO, int U>
+__global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int TW, int nss_w,
+                                                               int tiles) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
+    __shared__ float wred_s[kMaxWaves][2 * P][2];
+    __shared__ float tok_s[2 * P][2];  // per token: input factor, output factor
+    __shared__ float coef_s[2 * P][2];
+    constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
+    constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
+    const int K = a.K, nb = K >> 5, K4 = K >> 2;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthr = KS * TW * 64;
+    const int tw = wave / KS, ks = wave - tw * KS;
+    const int T = blockIdx.x * TW + tw;
+    const int Tl = T < tiles ? T : tiles - 1;  // a block's spare waves read the last tile, unused
+    const int j = lane & 15, g = lane >> 4;
+    const int nss = nss_w * KS;
+    // tile order (packing.h): load v of superstep S of tile T is 1 KiB at ((T*nss + S)*NI + v) KiB
+    const uint8_t* wp = static_cast<const uint8_t*>(a.wq) + ((size_t)Tl * nss + ks * nss_w) * NI * 1024 + lane * 16;
+    const float* sp = a.ws + (((size_t)Tl * nss + ks * nss_w) * 64 + lane) * U;
+
+    uint4 w0[NI], w1[NI];
+    float s0[U], s1[U];
+    auto issue = [&](uint4 (&w)[NI], float (&s)[U], int si) {  // si: superstep within the slice
+        const uint8_t* p = wp + (size_t)si * NI * 1024;
+#pragma unroll
+        for (int v = 0; v < NI; ++v) w[v] = *reinterpret_cast<const uint4*>(p + 1024 * v);
+        if constexpr (U == 4) {
+            const float4 t = *reinterpret_cast<const float4*>(sp + (size_t)si * 64 * 4);
+            s[0] = t.x, s[1] = t.y, s[2] = t.z, s[3] = t.w;
+        } else {
+            s[0] = sp[(size_t)si * 64];
+        }
+    };
+    // weights of the first two supersteps are in flight during the prologue
+    if (nss_w > 0) issue(w0, s0, 0);
+    if (nss_w > 1) issue(w1, s1, 1);
+
+    // Thread tid owns output tid of the block (TW*16*M <= 64*TW outputs, fewer than the threads); the
+    // residual it will update is read now, off the critical path.
+    const int e_m = tid % M, e_r = tid / M;
+    const int e_T = blockIdx.x * TW + (e_r >> 4), e_j = e_r & 15;
+    const int e_row = tid < TW * 16 * M && !(EPI == GEMV_SWIGLU && e_j >= 8) ? tile_row<EPI>(a, e_T, e_j) : -1;
+    float e_y0 = 0.0f, e_y1 = 0.0f;
+    if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
+        if (e_row >= 0) {
+            const float* yr = a.y + (size_t)e_m * a.y_stride;
+            e_y0 = yr[e_row];
+            if constexpr (EPI == GEMV_MHC) e_y1 = yr[a.h + e_row];
+        }
+    }
+
+    // ---- prologue: token rows -> f32 in LDS, reduced per token ----
+    const int row0 = a.row_base ? *a.row_base : 0;
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        if (tid < 2 * P) {
+            coef_s[tid][0] = tid < M ? a.coef[tid * 8] : 0.0f;
+            coef_s[tid][1] = tid < M ? a.coef[tid * 8 + 1] : 0.0f;
+        }
+        __syncthreads();
+    }
+    // region of (token pair p, block bb, token-in-pair t): 128 bytes at ((p*nb + bb)*2 + t)*128.
+    // Each batch issues all of its loads before the first use, so staging costs few round trips.
+    constexpr int BATCH = PRO == GEMV_NORM_MHC ? 2 : 4;
+    float ssq[2 * P], amax[2 * P];
+    const float4* xrow[2 * P];
+#pragma unroll
+    for (int m = 0; m < 2 * P; ++m) {
+        ssq[m] = 0.0f;
+        amax[m] = 0.0f;
+        xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
+    }
+    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int k4b = tid; k4b < K4; k4b += BATCH * nthr) {
+        float4 v[2 * P][BATCH], v1[2 * P][BATCH], nw[BATCH];
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int k4 = k4b + b * nthr;
+            const int kk = k4 < K4 ? k4 : 0;
+            if constexpr (PRO != GEMV_PLAIN) nw[b] = reinterpret_cast<const float4*>(a.norm_w)[kk];
+#pragma unroll
+            for (int m = 0; m < 2 * P; ++m) {
+                v[m][b] = m < M ? xrow[m][kk] : zero4;
+                if constexpr (PRO == GEMV_NORM_MHC) v1[m][b] = m < M ? xrow[m][K4 + kk] : zero4;
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < BATCH; ++b) {
+            const int k4 = k4b + b * nthr;
+            if (k4 >= K4) continue;
+#pragma unroll
+            for (int m = 0; m < 2 * P; ++m) {
+                float4 t = v[m][b];
+                if (m < M) {
+                    if constexpr (PRO == GEMV_NORM_MHC) {
+                        const float pre0 = coef_s[m][0], pre1 = coef_s[m][1];
+                        const float4 u = v1[m][b];
+                        t.x = pre0 * t.x + pre1 * u.x;
+                        t.y = pre0 * t.y + pre1 * u.y;
+                        t.z = pre0 * t.z + pre1 * u.z;
+                        t.w = pre0 * t.w + pre1 * u.w;
+                    }
+                    if constexpr (PRO != GEMV_PLAIN) {
+                        ssq[m] = fmaf(t.x, t.x, ssq[m]);
+                        ssq[m] = fmaf(t.y, t.y, ssq[m]);
+                        ssq[m] = fmaf(t.z, t.z, ssq[m]);
+                        ssq[m] = fmaf(t.w, t.w, ssq[m]);
+                        t.x = t.x * (1.0f + nw[b].x);
+                        t.y = t.y * (1.0f + nw[b].y);
+                        t.z = t.z * (1.0f + nw[b].z);
+                        t.w = t.w * (1.0f + nw[b].w);
+                    }
+                    amax[m] = fmaxf(amax[m], fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+                }
+                unsigned char* base = lds + (size_t)(m >> 1) * nb * 256 + (m & 1) * 128;
+                *reinterpret_cast<float4*>(base + (size_t)(k4 >> 3) * 256 + (k4 & 7) * 16) = t;
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 2 * P; ++m) {
+        ssq[m] = wave_sum(ssq[m]);
+        amax[m] = wave_max(amax[m]);
+    }
+    if (tid < kZeroBytes / 16)
+        reinterpret_cast<float4*>(lds + (size_t)P * nb * 256)[tid] = make_float4(0, 0, 0, 0);
+    if (lane == 0)
+#pragma unroll
+        for (int m = 0; m < 2 * P; ++m) {
+            wred_s[wave][m][0] = ssq[m];
+            wred_s[wave][m][1] = amax[m];
+        }
+    __syncthreads();
+    if (tid < 2 * P) {
+        const int m = tid;
+        float ss = 0.0f, mx = 0.0f;
+        for (int w = 0; w < KS * TW; ++w) {
+            ss = ss + wred_s[w][m][0];
+            mx = fmaxf(mx, wred_s[w][m][1]);
+        }
+        const float rinv = PRO == GEMV_PLAIN ? 1.0f : 1.0f / sqrtf(ss / (float)K + a.eps);
+        const float top = mx * rinv;
+        // keep |x| * factor below 2^14 so the f16 high part cannot overflow
+        const int e = top >= 16384.0f ? ilogbf(top) - 13 : 0;
+        tok_s[m][0] = m < M ? ldexpf(rinv, -e) : 0.0f;
+        tok_s[m][1] = ldexpf(1.0f, e);
+    }
+    __syncthreads();
+    // f32 region -> f16 hi (first 64 bytes) and lo (last 64 bytes) in MFMA fragment order
+    for (int rg = tid; rg < P * nb * 2; rg += nthr) {
+        const int m = 2 * (rg / (2 * nb)) + (rg & 1);
+        const float f = tok_s[m][0];
+        unsigned char* base = lds + (size_t)rg * 128;
+        float v[32];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const float4 t = reinterpret_cast<const float4*>(base)[c];
+            v[4 * c] = t.x, v[4 * c + 1] = t.y, v[4 * c + 2] = t.z, v[4 * c + 3] = t.w;
+        }
+        half8_t hi[4], lo[4];
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float y = v[e] * f;
+            const _Float16 h = (_Float16)y;
+            const int pidx = a_pos<QT>(e);
+            hi[pidx >> 3][pidx & 7] = h;
+            lo[pidx >> 3][pidx & 7] = (_Float16)(y - (float)h);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            reinterpret_cast<half8_t*>(base)[c] = hi[c];
+            reinterpret_cast<half8_t*>(base + 64)[c] = lo[c];
+        }
+    }
+    __syncthreads();
+
+    // ---- main loop ----
+    // lane (j, g) feeds A row j = 4*slot + combo; it carries data only when slot == g
+    const int slot = j >> 2, combo = j & 3;
+    const bool a_on = slot == g;
+    f32x4_t acc[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) acc[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const int zero_off = P * nb * 256;
+
+    auto compute = [&](const uint4 (&w)[NI], const float (&s)[U], int si) {
+        const int S = ks * nss_w + si;  // superstep within the row
+#pragma unroll
+        for (int v = 0; v < NI; ++v) {
+            const int blk = S * 4 * U + U * g + (QT == 0 ? (v >> 1) : v);  // quant block of this load
+            const int eoff = QT == 0 ? (v & 1) * 16 : 0;                  // first element in the block
+            int abase[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+                abase[p] = a_on ? ((p * nb + blk) * 4 + combo) * 64 + eoff * 2 : zero_off;
+            f32x4_t d[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) d[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < NM; ++i) {
+                const half8_t b = dequant8<QT>(w[v], i);
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    const half8_t av = *reinterpret_cast<const half8_t*>(lds + abase[p] + (a_on ? 16 * i : 0));
+                    d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, d[p], 0, 0, 0);
+                }
+            }
+            const float sc = s[QT == 0 ? (v >> 1) : v];
+#pragma unroll
+            for (int p = 0; p < P; ++p)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[p][r] = fmaf(sc, d[p][r], acc[p][r]);
+        }
+    };
+
+    for (int s = 0; s < nss_w; s += 2) {
+        compute(w0, s0, s);
+        if (s + 2 < nss_w) issue(w0, s0, s + 2);
+        if (s + 1 < nss_w) {
+            compute(w1, s1, s + 1);
+            if (s + 3 < nss_w) issue(w1, s1, s + 3);
+        }
+    }
+
+    // ---- reduction: hi + lo, then the 4 lane groups, then the K slices in order ----
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        float t0 = acc[p][0] + acc[p][1], t1 = acc[p][2] + acc[p][3];
+        t0 = t0 + __shfl_xor(t0, 16, 64);
+        t1 = t1 + __shfl_xor(t1, 16, 64);
+        t0 = t0 + __shfl_xor(t0, 32, 64);
+        t1 = t1 + __shfl_xor(t1, 32, 64);
+        if (g == 0) {
+            red_s[(wave * 16 + j) * 2 * P + 2 * p] = t0;
+            red_s[(wave * 16 + j) * 2 * P + 2 * p + 1] = t1;
+        }
+    }
+    __syncthreads();
+    if (e_row >= 0) {
+        const int t2 = e_r >> 4;
+        float v = 0.0f;
+        for (int k = 0; k < KS; ++k) v = v + red_s[((t2 * KS + k) * 16 + e_j) * 2 * P + e_m];
+        v = v * tok_s[e_m][1];
+        float* y = a.y + (size_t)e_m * a.y_stride;
+        if constexpr (EPI == GEMV_SWIGLU) {
+            float u = 0.0f;
+            for (int k = 0; k < KS; ++k) u = u + red_s[((t2 * KS + k) * 16 + e_j + 8) * 2 * P + e_m];
+            u = u * tok_s[e_m][1];
+            y[e_T * 8 + e_j] = v / (1.0f + expf(-v)) * u;
+        } else if constexpr (EPI == GEMV_STORE) {
+            y[a.n_off + e_row] = v;
+        } else if constexpr (EPI == GEMV_ADD) {
+            y[e_row] = e_y0 + v;
+        } else {  // GEMV_MHC, layers.wgsl:150-161
+            const float* cf = a.coef + e_m * 8;
+            const float n0 = (cf[4] * e_y0 + cf[5] * e_y1) + cf[2] * v;
+            const float n1 = (cf[6] * e_y0 + cf[7] * e_y1) + cf[3] * v;
+            if (a.merge_mode == 2) {
+                y[e_row] = 0.5f * (n0 + n1);
+            } else {
+                y[e_row] = n0;
+                y[a.h + e_row] = n1;
+            }
+        }
+    }
+}
+
+using KernelFn = void (*)(GemvArgs, int, int, int, int, int);
+
+template <int QT, int U>
+KernelFn pick_fn(int P, int epi, int pro) {
+#define SNL_G(E, PR) \
+    if (epi == E && pro == PR) return &mgemv_kernel<QT, 1, E, PR, U>;
+    if (P == 1) {
+        SNL_G(GEMV_STORE, GEMV_PLAIN)
+        SNL_G(GEMV_STORE, GEMV_NORM)
+        SNL_G(GEMV_STORE, GEMV_NORM_MHC)
+        SNL_G(GEMV_ADD, GEMV_PLAIN)
+        SNL_G(GEMV_ADD, GEMV_NORM)
+        SNL_G(GEMV_MHC, GEMV_PLAIN)
+        SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
+        SNL_G(GEMV_SWIGLU, GEMV_NORM)
+        SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
+    }
+#undef SNL_G
+    // two token pairs: the plain product only (kernel-level calls with M = 3, 4)
+    if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U>;
+    return nullptr;
+}
+
+KernelFn pick(int quant, int U, int P, int epi, int pro) {
+    if (quant == 0) return U == 4 ? pick_fn<0, 4>(P, epi, pro) : pick_fn<0, 1>(P, epi, pro);
+    return U == 4 ? pick_fn<1, 4>(P, epi, pro) : pick_fn<1, 1>(P, epi, pro);
+}
+
+__global__ __launch_bounds__(256) void pack_q_kernel(PackGeom g, const uint8_t* q, uint8_t* qp) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece
+    if (i >= g.q_bytes / 16) return;
+    const int lane = (int)(i & 63);
+    size_t r = i >> 6;
+    const int v = (int)(r % g.NI);
+    r /= g.NI;
+    const int S = (int)(r % g.nss), T = (int)(r / g.nss);
+    const int row = pack_row(g, T, lane & 15);
+    uint4 val = make_uint4(0u, 0u, 0u, 0u);
+    if (row >= 0) val = *reinterpret_cast<const uint4*>(q + (size_t)row * g.row_bytes + pack_row_offset(g, S, v, lane >> 4));
+    *reinterpret_cast<uint4*>(qp + i * 16) = val;
+}
+
+__global__ __launch_bounds__(256) void pack_s_kernel(PackGeom g, const float* s, float* sp) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // (T, S, lane)
+    if (i >= g.s_floats / g.U) return;
+    const int lane = (int)(i & 63);
+    const size_t r = i >> 6;
+    const int S = (int)(r % g.nss), T = (int)(r / g.nss);
+    const int row = pack_row(g, T, lane & 15);
+    for (int u = 0; u < g.U; ++u)
+        sp[i * g.U + u] = row >= 0 ? s[(size_t)row * (g.K / 32) + 4 * g.U * S + g.U * (lane >> 4) + u] : 0.0f;
+}
+
+}  // namespace
+
+int launch_pack_matrix(const PackGeom& g, const void* q, const float* s, void* qp, float* sp, hipStream_t st) {
+    const size_t nq = g.q_bytes / 16, ns = g.s_floats / g.U;
+    hipLaunchKernelGGL(pack_q_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, st, g,
+                       static_cast<const uint8_t*>(q), static_cast<uint8_t*>(qp));
+    hipLaunchKernelGGL(pack_s_kernel, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0, st, g, s, sp);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int mgemv_init() {
+    for (int q = 0; q < 2; ++q)
+        for (int U = 1; U <= 4; U += 3)
+            for (int P = 1; P <= 2; ++P)
+                for (int e = 0; e < 4; ++e)
+                    for (int p = 0; p < 3; ++p) {
+                        KernelFn f = pick(q, U, P, e, p);
+                        if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     kLdsLimit) != hipSuccess)
+                            return -2;
+                    }
+    return 0;
+}
+
+// Launch shape from the matrix shape only: K slices KS, tiles per block TW, supersteps per wave.
+void mgemv_shape(const PackGeom& g, int* KS, int* TW, int* nss_w) {
+    *KS = 1;
+    while (*KS < kMaxWaves && (long)g.tiles * *KS < kTargetItems && g.nss % (2 * *KS) == 0) *KS *= 2;
+    const int NW = *KS < 4 ? 4 : *KS;
+    *TW = NW / *KS;
+    *nss_w = g.nss / *KS;
+}
+
+size_t mgemv_lds_bytes(int M, int K) { return (size_t)(M <= 2 ? 1 : 2) * (K / 32) * 256 + kZeroBytes; }
+
+bool mgemv_fits(int M, int K) { return mgemv_lds_bytes(M, K) <= (size_t)kLdsLimit; }
+
+// 0: launched; 1: this call is not served (M too large for LDS at this K); < 0 error.
+// The weights are in tile order (packing.h) for (N, K, inter when SwiGLU).
+int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
+    PackGeom g;
+    if (!pack_geom(quant, a.N, a.K, a.epi == GEMV_SWIGLU ? a.inter : 0, &g)) return -1;
+    int KS, TW, nss_w;
+    mgemv_shape(g, &KS, &TW, &nss_w);
+    const int P = M <= 2 ? 1 : 2;
+    const size_t lds = mgemv_lds_bytes(M, a.K);
+    if (!mgemv_fits(M, a.K)) return 1;
+    if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
+        (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_stride & 3))
+        return -1;
+    KernelFn f = pick(quant, g.U, P, a.epi, a.pro);
+    if (!f) return 1;
+    dim3 grid((g.tiles + TW - 1) / TW);
+    hipLaunchKernelGGL(f, grid, dim3(KS * TW * 64), lds, s, a, M, KS, TW, nss_w, g.tiles);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // namespace snl
