@@ -9,9 +9,11 @@ acceptance (rollback on reject).  W untimed warmup steps, then exactly K timed s
 device synchronisations; value = tokens emitted in those K steps / their wall time.
 
 roofline: the dominant kernel is the verify pass's gate_up GEMV (Q8_0, M=2, N=24576, K=4096 with
-the SwiGLU epilogue, 43% of the pass's weight bytes).  Its launch duration is measured live with
-HIP events on the engine's stream (a verify pass launched op by op after the timed region);
-achieved = algorithmic bytes per launch / mean duration.
+the fused mHC/RMSNorm prologue and SwiGLU epilogue, 43% of the pass's weight bytes).  After the
+timed region the engine launches only that op of a verify pass, `--roofline-reps` passes back to
+back (56 launches per pass, each layer's own 113 MB matrix, so nothing is served from the 256 MB
+Infinity Cache), between two HIP events on the engine's stream; achieved = algorithmic bytes per
+launch / mean time per launch.  A per-op table of an eagerly launched verify pass goes to stderr.
 
 cpu_baseline: the CPU oracle (oracle/, a C restatement of the reference's kernels, OpenMP) running
 the same 9B model on the host cores for a bounded sample (a 2-token prompt, then a few
@@ -31,10 +33,63 @@ sys.path.insert(0, os.path.join(REPO, "sense-nova-server_amd"))
 METRIC = "9B Q8_0 MTP greedy decode tok/s (1 GPU); Q8 GEMV GB/s vs HBM peak"
 HBM_PEAK_GBS = 8000.0
 PROMPT = 1024
+ROOFLINE_KERNEL = "mgemv_kernel<0, 1, 3, 2, 4>"  # Q8_0, one token pair, SwiGLU epilogue, mHC prologue, U=4
+# HBM traffic of the roofline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (see summarize_pmc);
+# reported only while the kernel sources hash to the value recorded with it.
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_gate_up_9b_q8_traffic.json")
+KERNEL_SOURCES = ["mgemv.hip", "packing.h", "kernels.h", "common.h"]
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def kernel_source_hash() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        with open(os.path.join(REPO, "sense-nova-server_amd", "csrc", f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
+
+
+def _pmc_mean(path: str, name_part: str) -> float:
+    import csv
+
+    vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path)) if name_part in r["Kernel_Name"]]
+    if not vals:
+        raise SystemExit(f"{path}: no dispatch of {name_part}")
+    return sum(vals) / len(vals)
+
+
+def summarize_pmc(d: str, copy_mb: int) -> dict:
+    """Turn four rocprofv3 --pmc runs into the roofline kernel's HBM bytes per launch.
+
+    pf/pw: FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the bench's roofline kernel; cf/cw: the
+    same counters for a device copy of copy_mb MiB (bench.py --copy-probe-mb), which read and write
+    exactly that many bytes: each counter is scaled by (true KiB / counted KiB) of the copy."""
+    true_kib = copy_mb * 1024.0
+    ff = true_kib / _pmc_mean(os.path.join(d, "cf_counter_collection.csv"), "copyBuffer")
+    wf = true_kib / _pmc_mean(os.path.join(d, "cw_counter_collection.csv"), "copyBuffer")
+    fetch = _pmc_mean(os.path.join(d, "pf_counter_collection.csv"), ROOFLINE_KERNEL)
+    write = _pmc_mean(os.path.join(d, "pw_counter_collection.csv"), ROOFLINE_KERNEL)
+    rec = {"kernel": ROOFLINE_KERNEL, "fetch_kib": fetch, "write_kib": write, "fetch_factor": ff,
+           "write_factor": wf, "traffic_bytes": (fetch * ff + write * wf) * 1024.0,
+           "kernel_sources_sha256": kernel_source_hash()}
+    with open(TRAFFIC_FILE, "w") as fh:
+        json.dump(rec, fh, indent=1)
+    return rec
+
+
+def measured_traffic():
+    try:
+        rec = json.load(open(TRAFFIC_FILE))
+    except (OSError, ValueError):
+        return None
+    if rec.get("kernel_sources_sha256") != kernel_source_hash():
+        return None
+    return round(rec["traffic_bytes"])
 
 
 def cpu_baseline(steps: int) -> dict:
@@ -90,9 +145,18 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--profile-passes", type=int, default=4)
+    ap.add_argument("--roofline-reps", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--summarize-pmc", metavar="DIR",
+                    help="write the roofline kernel's HBM traffic record from rocprofv3 --pmc CSVs in DIR and exit")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="only copy a buffer of this many MiB 4 times on the GPU and exit: the known-size "
+                         "kernel that HBM byte counters are calibrated against")
     args = ap.parse_args()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(args.summarize_pmc, args.copy_probe_mb or 256), indent=1))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs on a single MI355X (multi-GPU sharding is a "
               "design note only); run with --gpus 1", file=sys.stderr)
@@ -104,6 +168,14 @@ def main() -> int:
     import snl
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_probe_mb:
+        src = torch.ones(args.copy_probe_mb << 18, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 4, "copies": 4}), flush=True)
+        return 0
     cfg = snl.nine_b_config()
     ctx = PROMPT + 2 * (args.warmup + args.steps) + args.profile_passes + 64
     t0 = time.perf_counter()
@@ -146,8 +218,7 @@ def main() -> int:
             d[0] += 1
             d[1] += b
             d[2] += ms
-    gu = per_op["gemv_gate_up"]
-    gu_bytes, gu_ms = gu[1] / gu[0], gu[2] / gu[0]
+    gu_ms, gu_bytes, gu_n = eng.time_op("gemv_gate_up", args.roofline_reps)
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
     gemv_bytes = sum(v[1] for k, v in per_op.items() if k.startswith("gemv")) / args.profile_passes
     gemv_ms = sum(v[2] for k, v in per_op.items() if k.startswith("gemv")) / args.profile_passes
@@ -156,7 +227,8 @@ def main() -> int:
         gbs = b / (ms * 1e-3) / 1e9 if ms > 0 and b > 0 else 0.0
         log(f"  {name:<16} calls {n / args.profile_passes:6.1f}/pass  {ms / args.profile_passes:8.3f} ms/pass"
             f"  {gbs:8.1f} GB/s")
-    log(f"gate_up GEMV: {gu_bytes / 1e6:.2f} MB/launch, {gu_ms * 1e3:.2f} us -> {achieved:.0f} GB/s; all GEMVs "
+    log(f"gate_up GEMV alone ({gu_n} launches/pass x {args.roofline_reps}): {gu_bytes / 1e6:.2f} MB/launch, "
+        f"{gu_ms * 1e3:.2f} us -> {achieved:.0f} GB/s; all GEMVs "
         f"{gemv_bytes / 1e9:.3f} GB in {gemv_ms:.3f} ms/pass; eager pass {pass_ms:.3f} ms")
 
     weights_per_verify = 14765064192.0  # f32-scale layout, 56 layer visits + LM head
@@ -186,12 +258,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel<Q8_0, M=2, SwiGLU> (gate_up, N=24576, K=4096)",
+            "kernel": "mgemv_kernel<Q8_0, M=2, SwiGLU, mHC-RMSNorm prologue> (gate_up, N=24576, K=4096)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "cpu_baseline": None,
     }

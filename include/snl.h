@@ -94,6 +94,16 @@ typedef struct snl_op_time {
 int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows,
                          int ckpt, snl_op_time* recs, int max_recs, int* n_recs);
 
+/* Isolated-op timing (no reference counterpart; a measurement aid beside the profile mode
+ * above): launches only the ops called `name` (an snl_op_time name, e.g. "gemv_gate_up") of a
+ * 2-token verify pass at the current position, `reps` passes back to back between two device
+ * events on the engine stream, and reports the mean time per launch, the algorithmic HBM bytes
+ * per launch (0 where not counted) and the launches per pass.  Skipped ops leave the inputs as
+ * they are; nothing is committed (position, state slot and carried hidden row are unchanged).
+ * "copy" is refused. */
+int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch, double* bytes_per_launch,
+                int* launches_per_pass);
+
 /* Engine::mtp (src/engine.rs:713-774): run the MTP head on pairs (hidden row r0+i of the
  * last step, tokens[i]) into MTP cache slots slot0+i with rotary positions pos3[i].  With
  * draft != 0, *draft_out receives the draft token, pick_out (nullable) its pick and

@@ -138,6 +138,21 @@ struct snl_engine {
         hipEventRecord(ev, stream);
         marks->push_back({name, bytes, ev});
     }
+    // Isolated-op timing: when `only` is set, a pass launches only the ops of that name.
+    const char* only = nullptr;
+    int only_launches = 0;
+    double only_bytes = 0.0;
+    // Marks the start of op `name` and says whether to launch it.
+    bool op(const char* name, double bytes) {
+        if (only) {
+            if (strcmp(name, only) != 0) return false;
+            ++only_launches;
+            only_bytes += bytes;
+            return true;
+        }
+        mark(name, bytes);
+        return true;
+    }
     // Algorithmic HBM bytes of one GEMV launch: quants + f32 scales + the M input rows +
     // the output (read and written back for the residual epilogues).
     static double gemv_bytes(const QW& w, int M, int epi, int inter) {
@@ -244,7 +259,7 @@ struct snl_engine {
     // GEMV_NORM_MHC, whose pre-mix coefficients launch_mhc left in coef) and the epilogue `epi`.
     int gemv(const char* name, const QW& w, const float* xin, int x_stride, float* y, int y_stride, int M, int epi,
              int merge_mode = 0, int pro = GEMV_PLAIN, const float* nw = nullptr, const int32_t* row_base = nullptr) {
-        mark(name, gemv_bytes(w, M, epi, cfg.intermediate));
+        if (!op(name, gemv_bytes(w, M, epi, cfg.intermediate))) return 0;
         GemvArgs g{};
         g.packed = w.packed ? 1 : 0;
         g.wq = w.q;
@@ -282,7 +297,7 @@ struct snl_engine {
         a.count = count;
         a.eps = cfg.eps;
         a.one = 1.0f;
-        mark("norm", 0.0);
+        if (!op("norm", 0.0)) return 0;
         return launch_branch_norm(a, stream);
     }
     AttnArgs attn_args(const StepDev* st, uint16_t* kc, uint16_t* vc, const float* norms) const {
@@ -453,10 +468,8 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
     // the checkpoint request itself travels in the step record
     const snl_config& c = cfg;
     int rc = 0;
-    mark("embed", 0.0);
-    rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream);
-    mark("copy", 0.0);
-    rc |= launch_copy(hid, hlast, h, stream);  // row 0 = hidden of the token before this step
+    if (op("embed", 0.0)) rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream);
+    if (op("copy", 0.0)) rc |= launch_copy(hid, hlast, h, stream);  // row 0 = hidden of the token before this step
     int fslot = 0, lslot = 0;
     const size_t kvn = (size_t)ctx * kv_dim;
     const size_t nl = std::max(n_lin, 1);
@@ -464,20 +477,17 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
         const Layer& L = layers[li];
         const bool mhc = is_mhc(li);
         if (mhc && li == c.mhc_start) {
-            mark("expand", 0.0);
-            rc |= launch_expand(x, h, M, stream);
+            if (op("expand", 0.0)) rc |= launch_expand(x, h, M, stream);
         }
         // branch input: RMSNorm (1 + in_ln) of stream 0, or of the mHC pre-mix, fused into the GEMV
         if (mhc) {
-            mark("mhc", 0.0);
-            rc |= launch_mhc(x, L.mhc_attn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
+            if (op("mhc", 0.0)) rc |= launch_mhc(x, L.mhc_attn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
         }
         const int pro = mhc ? GEMV_NORM_MHC : GEMV_NORM;
         if (L.full) {
             rc |= gemv("gemv_qkv", L.mix_in, x, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p);
             AttnArgs a = attn_args(d_step, kcache + kvn * fslot, vcache + kvn * fslot, L.small.p);
-            mark("attention", 0.0);
-            rc |= launch_attention(a, M, stream);
+            if (op("attention", 0.0)) rc |= launch_attention(a, M, stream);
             rc |= gemv("gemv_o", L.mix_out, attn_out, q_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, 1);
             ++fslot;
         } else {
@@ -496,15 +506,14 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             d.n_v = c.lin_v_heads;
             d.eps = c.eps;
             d.step = d_step;
-            mark("deltanet", 2.0 * 4.0 * (double)state_floats + (ckpt ? 4.0 * (double)state_floats : 0.0));
-            rc |= launch_deltanet(d, M, stream);
+            const double dn_bytes = 2.0 * 4.0 * (double)state_floats + (ckpt ? 4.0 * (double)state_floats : 0.0);
+            if (op("deltanet", dn_bytes)) rc |= launch_deltanet(d, M, stream);
             rc |= gemv("gemv_out_proj", L.mix_out, attn_out, lin_value_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD,
                        1);
             ++lslot;
         }
         if (mhc) {
-            mark("mhc", 0.0);
-            rc |= launch_mhc(x, L.mhc_ffn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
+            if (op("mhc", 0.0)) rc |= launch_mhc(x, L.mhc_ffn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
         }
         rc |= gemv("gemv_gate_up", L.gate_up, x, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, pro, L.post_ln.p);
         const int mode = !mhc ? 0 : (li + 1 == c.mhc_end ? 2 : 1);
@@ -513,11 +522,9 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
     rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M);
     if (rows > 0) {
         rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
-        mark("pick", 0.0);
-        rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
+        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
     }
-    mark("copy", 0.0);
-    rc |= launch_copy(hlast, hid + (size_t)M * h, h, stream);
+    if (op("copy", 0.0)) rc |= launch_copy(hlast, hid + (size_t)M * h, h, stream);
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
 }
@@ -526,15 +533,14 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
 int snl_engine::record_mtp(int M, int draft) {
     const snl_config& c = cfg;
     int rc = 0;
-    rc |= launch_embed(d_mstep, (const int8_t*)embed.q, embed.s, c.vocab, h, mx, M, stream);
+    if (op("embed", 0.0)) rc |= launch_embed(d_mstep, (const int8_t*)embed.q, embed.s, c.vocab, h, mx, M, stream);
     // x = fc_e(norm_e(emb)) + fc_h(norm_h(hid[r0..])); fc_e reads xn, since it writes mx
     rc |= norm(mx, 2 * h, nullptr, 0, norm_e.p, xn, 0, M);
     rc |= gemv("gemv_fc_e", fc_e, xn, h, mx, 2 * h, M, GEMV_STORE);
     rc |= gemv("gemv_fc_h", fc_h, hid, h, mx, 2 * h, M, GEMV_ADD, 0, GEMV_NORM, norm_h.p, &d_mstep->r0);
     rc |= gemv("gemv_mtp_qkv", m_qkv, mx, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, GEMV_NORM, m_in_ln.p);
     AttnArgs a = attn_args(d_mstep, m_kc, m_vc, m_qk_norm.p);
-    mark("attention", 0.0);
-    rc |= launch_attention(a, M, stream);
+    if (op("attention", 0.0)) rc |= launch_attention(a, M, stream);
     rc |= gemv("gemv_mtp_o", m_o, attn_out, q_dim, mx, 2 * h, M, GEMV_ADD);
     rc |= gemv("gemv_mtp_gate_up", m_gate_up, mx, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, GEMV_NORM,
                m_post_ln.p);
@@ -543,8 +549,7 @@ int snl_engine::record_mtp(int M, int draft) {
         // final norm of the last pair fused into the LM head
         rc |= gemv("gemv_lm_head", lm_head, mx + (size_t)(M - 1) * 2 * h, 2 * h, m_logits, c.vocab, 1, GEMV_STORE, 0,
                    GEMV_NORM, m_norm.p);
-        mark("pick", 0.0);
-        rc |= launch_pick(m_logits, c.vocab, 1, pick_scratch, d_mpick, stream);
+        if (op("pick", 0.0)) rc |= launch_pick(m_logits, c.vocab, 1, pick_scratch, d_mpick, stream);
     }
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
@@ -738,6 +743,51 @@ int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uin
     e->cur = st.s_out;
     e->pos += n;
     e->hid_rows = n;
+    return SNL_OK;
+}
+
+int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch, double* bytes_per_launch,
+                int* launches_per_pass) {
+    if (!e || !name || reps < 1 || !ms_per_launch) return SNL_EARG;
+    e->err.clear();
+    if (!strcmp(name, "copy")) return e->fail(SNL_EARG, "time_op: 'copy' moves the carried hidden row");
+    if (e->pos + 2 > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + 2, e->ctx);
+    // a verify pass (2 rows, checkpoint) at the current position; nothing is committed
+    StepDev& st = e->h_step[0];
+    memset(&st, 0, sizeof st);
+    st.pos0 = e->pos;
+    st.m = 2;
+    st.ckpt = 1;
+    st.s_in = e->cur;
+    st.s_ck = (e->cur + 1) % 3;
+    st.s_out = (e->cur + 2) % 3;
+    for (int i = 0; i < 2; ++i)
+        for (int k = 0; k < 3; ++k) st.rpos[i][k] = (uint32_t)(e->pos + i);
+    if (hipMemcpyAsync(e->d_step, &st, sizeof(StepDev), hipMemcpyHostToDevice, e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "step upload failed");
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    if (hipEventCreate(&t0) != hipSuccess || hipEventCreate(&t1) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "event creation failed");
+    e->only = name;
+    e->only_launches = 0;
+    e->only_bytes = 0.0;
+    int rc = e->record_forward(2, 2, 1);  // warm-up pass
+    const int per_pass = e->only_launches;
+    const double bytes = per_pass ? e->only_bytes / per_pass : 0.0;
+    hipEventRecord(t0, e->stream);
+    for (int r = 0; r < reps && !rc; ++r) rc |= e->record_forward(2, 2, 1);
+    hipEventRecord(t1, e->stream);
+    e->only = nullptr;
+    float ms = 0.0f;
+    const hipError_t se = hipEventSynchronize(t1);
+    hipEventElapsedTime(&ms, t0, t1);
+    hipEventDestroy(t0);
+    hipEventDestroy(t1);
+    if (rc || se != hipSuccess) return e->fail(SNL_EDEVICE, "time_op pass failed");
+    if (!per_pass) return e->fail(SNL_EARG, "time_op: no op named '%s' in a verify pass", name);
+    *ms_per_launch = (double)ms / ((double)reps * per_pass);
+    if (bytes_per_launch) *bytes_per_launch = bytes;
+    if (launches_per_pass) *launches_per_pass = per_pass;
     return SNL_OK;
 }
 

@@ -176,7 +176,6 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         amax[m] = 0.0f;
         xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
     }
-    const float4 zero4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (int k4b = tid; k4b < K4; k4b += BATCH * nthr) {
         float4 v[2 * P][BATCH], v1[2 * P][BATCH], nw[BATCH];
 #pragma unroll
@@ -186,8 +185,15 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             if constexpr (PRO != GEMV_PLAIN) nw[b] = reinterpret_cast<const float4*>(a.norm_w)[kk];
 #pragma unroll
             for (int m = 0; m < 2 * P; ++m) {
-                v[m][b] = m < M ? xrow[m][kk] : zero4;
-                if constexpr (PRO == GEMV_NORM_MHC) v1[m][b] = m < M ? xrow[m][K4 + kk] : zero4;
+                // rows past M stage zeros (the loads are skipped, not selected, so that no
+                // zero vector has to live in memory)
+                if (m < M) {
+                    v[m][b] = xrow[m][kk];
+                    if constexpr (PRO == GEMV_NORM_MHC) v1[m][b] = xrow[m][K4 + kk];
+                } else {
+                    v[m][b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    v1[m][b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
             }
         }
 #pragma unroll

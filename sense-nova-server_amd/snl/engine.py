@@ -77,6 +77,8 @@ def lib() -> ctypes.CDLL:
                                    ctypes.POINTER(GenStats)]
         L.snl_forward_profiled.argtypes = [vp, u32p, ctypes.c_int, u32p, ctypes.c_int, ctypes.c_int,
                                            ctypes.POINTER(OpTime), ctypes.c_int, i32p]
+        L.snl_time_op.argtypes = [vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_double), i32p]
         L.snl_decoder_create.argtypes = [vp, u32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(vp)]
         L.snl_decoder_step.argtypes = [vp, u32p, f32p, i32p]
         L.snl_decoder_stats.argtypes = [vp, ctypes.POINTER(GenStats)]
@@ -177,6 +179,14 @@ class Engine:
                                         logit_rows, int(ckpt), recs, 4096, ctypes.byref(n))
         self._check(rc)
         return [(recs[i].name.decode(), recs[i].bytes, recs[i].ms) for i in range(n.value)]
+
+    def time_op(self, name: str, reps: int = 4):
+        """Launch only the `name` ops of a verify pass, `reps` passes back to back:
+        (ms per launch, algorithmic bytes per launch, launches per pass)."""
+        ms, b, n = ctypes.c_double(), ctypes.c_double(), ctypes.c_int32()
+        rc = lib().snl_time_op(self.h, name.encode(), reps, ctypes.byref(ms), ctypes.byref(b), ctypes.byref(n))
+        self._check(rc)
+        return ms.value, b.value, n.value
 
     def decoder(self, prompt: Sequence[int], spec: bool) -> "Decoder":
         return Decoder(self, prompt, spec)
