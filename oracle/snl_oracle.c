@@ -15,6 +15,27 @@
  * this file uses IEEE libm and round-to-nearest-even f16 packing.
  *
  * Citations are path:line into the reference repository.
+ *
+ * How each part is pinned (the reference cannot run here: Rust + wgpu, no
+ * toolchain or Vulkan; it ships no test vectors for this path):
+ *   f16 packing          numpy float16 (round to nearest even)
+ *   Q8_0/Q4_0 quantize   hand-derived known answers, half-away-from-zero ties,
+ *                        Q4 sign convention and nibble layout
+ *   gemv                 float64 dequant-matmul, one-hot columns, M=1 == rows of M=2
+ *   branch_norm          float64, transformers Qwen3_5RMSNorm
+ *   mhc_dots/mhc_finish  float64 router and Sinkhorn (doubly stochastic result)
+ *   merge, swiglu        closed forms
+ *   conv, delta          transformers causal_conv1d_update / recurrent gated delta
+ *                        rule and RMSNormGated; decay/beta/normalisation invariants
+ *   attn_prep, attend,   float64 RMSNorm + RoPE, transformers rotate-half, brute-force
+ *   combine              softmax attention over the f16 cache, split-K invariance
+ *   argmax               brute force, first index on ties
+ *   engine (forward,     self-consistency only: stepwise == batched, rollback ==
+ *   mtp, rollback,       never run, snapshot/restore, MTP on == off.  The op order
+ *   snapshot, generate)  itself (src/engine.rs:383-570) is a restatement with no
+ *                        independent check: parity unpinned.
+ *   twin RNG, weights    this build's own convention (no reference counterpart);
+ *                        moments and determinism only.
  */
 #include <math.h>
 #include <stdint.h>

@@ -454,3 +454,64 @@ def test_argmax_first_index_on_ties(oracle):
     for _ in range(20):
         v = r.integers(0, 5, 1000).astype(np.float32)
         assert oracle.argmax(v) == int(np.argmax(v))  # numpy also returns the first maximum
+
+
+# ---- engine composition (src/engine.rs:383-570, :653-697): self-consistency invariants ----
+def _tiny_engines(oracle, n=2):
+    import snl.config as C
+
+    cfg = C.tiny_config()
+    return cfg, [oracle.Engine(cfg, seed=5, quant=0, ctx=64, max_m=2) for _ in range(n)]
+
+
+def _state_sizes(cfg):
+    plan = cfg.execution_plan()
+    n_lin = sum(1 for l in plan if not cfg.full_attention[l])
+    conv_dim = 2 * cfg.lin_k_heads * cfg.lin_k_dim + cfg.lin_v_heads * cfg.lin_v_dim
+    return n_lin * cfg.lin_v_heads * cfg.lin_v_dim * cfg.lin_v_dim, n_lin * 3 * conv_dim
+
+
+def test_engine_stepwise_equals_batched(oracle):
+    """A 2-token pass gives each row the logits of two 1-token passes (positions, caches and the
+    recurrent state carried exactly between rows)."""
+    cfg, (a, b) = _tiny_engines(oracle)
+    p = np.random.default_rng(7).integers(0, cfg.vocab, 8).tolist()
+    a.forward(p[:6], logit_rows=0)
+    b.forward(p[:6], logit_rows=0)
+    two = a.forward(p[6:8], logit_rows=2)
+    one0 = b.forward(p[6:7], logit_rows=1)[0]
+    one1 = b.forward(p[7:8], logit_rows=1)[0]
+    assert np.array_equal(two[0], one0) and np.array_equal(two[1], one1)
+    a.close()
+    b.close()
+
+
+def test_engine_rollback_equals_never_run(oracle):
+    cfg, (a, b) = _tiny_engines(oracle)
+    n_state, n_conv = _state_sizes(cfg)
+    p = np.random.default_rng(8).integers(0, cfg.vocab, 9).tolist()
+    a.forward(p[:6], logit_rows=0)
+    b.forward(p[:6], logit_rows=0)
+    a.forward(p[6:8], logit_rows=2, ckpt=True)
+    a.rollback()
+    b.forward(p[6:7], logit_rows=1)
+    assert a.pos == b.pos == 7 and a.hid_rows == b.hid_rows == 1
+    for bid, n in ((3, n_state), (4, n_conv), (2, cfg.hidden)):
+        assert np.array_equal(a.buf(bid, n), b.buf(bid, n)), bid
+    assert np.array_equal(a.forward(p[8:9])[0], b.forward(p[8:9])[0])
+    a.close()
+    b.close()
+
+
+def test_engine_snapshot_restore(oracle):
+    cfg, (a, b) = _tiny_engines(oracle)
+    p = np.random.default_rng(9).integers(0, cfg.vocab, 12).tolist()
+    a.forward(p[:6], logit_rows=0)
+    a.snapshot(0)
+    a.forward(p[6:10], logit_rows=0)
+    a.restore(0, 6)
+    b.forward(p[:6], logit_rows=0)
+    assert a.pos == b.pos == 6
+    assert np.array_equal(a.forward(p[10:12], logit_rows=2), b.forward(p[10:12], logit_rows=2))
+    a.close()
+    b.close()
