@@ -166,7 +166,10 @@ size_t snl_buffer_size(const snl_engine* e, int id);
 /* ---- kernel-level entry points (device pointers; `stream` is a hipStream_t or NULL) ------ */
 
 /* y[m*y_stride + n] = sum_k x[m*x_stride + k] * W[n, k], M in 1..4 (matmul.wgsl matvec1/2).
- * wq/ws: reference layout quants [N, K] (Q8) or [N, K/2] (Q4), f32 scales [N, K/32]. */
+ * wq/ws: reference layout quants [N, K] (Q8) or [N, K/2] (Q4), f32 scales [N, K/32].  When
+ * K % 128 == 0 the call packs W into the engine's tile order in a staging buffer the library
+ * keeps, runs the matrix-core kernel and returns after it has finished on `stream`; other
+ * shapes run the vector-ALU kernel on W as given. */
 int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K,
              int x_stride, int y_stride, void* stream);
 
