@@ -148,6 +148,8 @@ def main() -> int:
     ap.add_argument("--roofline-reps", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--op-times", action="store_true",
+                    help="also print each op of a verify pass timed in isolation (stderr)")
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="write the roofline kernel's HBM traffic record from rocprofv3 --pmc CSVs in DIR and exit")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -218,6 +220,13 @@ def main() -> int:
             d[0] += 1
             d[1] += b
             d[2] += ms
+    if args.op_times:
+        for name in sorted(per_op):
+            if name in ("copy", "end"):
+                continue
+            ms, b, n = eng.time_op(name, args.roofline_reps)
+            gbs = b / (ms * 1e-3) / 1e9 if b > 0 else 0.0
+            log(f"  isolated {name:<16} {n:3d}/pass  {ms * 1e3:8.2f} us/launch  {b / 1e6:9.2f} MB  {gbs:8.1f} GB/s")
     gu_ms, gu_bytes, gu_n = eng.time_op("gemv_gate_up", args.roofline_reps)
     achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
     gemv_bytes = sum(v[1] for k, v in per_op.items() if k.startswith("gemv")) / args.profile_passes

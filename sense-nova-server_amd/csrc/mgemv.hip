@@ -26,9 +26,10 @@
 //
 // Work split.  A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows).  A
 // superstep is 128*U elements of a row (U = 4 when K % 512 == 0, else 1), 8 KiB of a Q8 tile;
-// K is cut into KS equal slices of supersteps.  A block of NW = KS*TW waves owns TW tiles and every wave one
-// (tile, slice) item; KS and TW are chosen from the matrix shape alone, never from M.  Loads run
-// one superstep ahead of the MFMAs.  Slices are added in slice order through LDS, so a token's
+// K is cut into KS equal slices of supersteps.  A block of 8 = KS*TW waves owns TW tiles and every
+// wave one (tile, slice) item; KS and TW are chosen from the matrix shape alone, never from M.
+// Weights stream through a three-chunk register ring (half supersteps), two chunks ahead of the
+// MFMAs, and the token rows are loaded before the first weight chunk.  Slices are added in slice order through LDS, so a token's
 // result does not depend on M, on its index or on timing (greedy output is then byte-identical
 // with and without speculative drafting).
 //
@@ -53,7 +54,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxWaves = 8;
-constexpr int kTargetItems = 2048;        // wave items per launch worth splitting K for (8 per CU)
+constexpr int kCUs = 256;                 // MI355X compute units
 constexpr int kLdsLimit = 150 * 1024;     // dynamic LDS per block
 constexpr int kZeroBytes = 64;            // zero A fragment read by the lanes outside their slot
 
@@ -103,14 +104,14 @@ __device__ __forceinline__ int a_pos(int e) {
 }
 
 // QT: 0 Q8_0, 1 Q4_0.  P: token pairs (M <= 2P).  U: quant blocks per lane group per superstep.
-template <int QT, int P, int EPI, int PRO, int U>
+// UPT: 8-element units of each token row per thread (K <= 8 * UPT * 512).
+template <int QT, int P, int EPI, int PRO, int U, int UPT>
 __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int TW, int nss_w,
                                                                int tiles) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
     __shared__ float wred_s[kMaxWaves][2 * P][2];
     __shared__ float tok_s[2 * P][2];  // per token: input factor, output factor
-    __shared__ float coef_s[2 * P][2];
     constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
     constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
     const int K = a.K, nb = K >> 5, K4 = K >> 2;
@@ -125,25 +126,74 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const uint8_t* wp = static_cast<const uint8_t*>(a.wq) + ((size_t)Tl * nss + ks * nss_w) * NI * 1024 + lane * 16;
     const float* sp = a.ws + (((size_t)Tl * nss + ks * nss_w) * 64 + lane) * U;
 
-    uint4 w0[NI], w1[NI];
-    float s0[U], s1[U];
-    auto issue = [&](uint4 (&w)[NI], float (&s)[U], int si) {  // si: superstep within the slice
-        const uint8_t* p = wp + (size_t)si * NI * 1024;
+    // Weights stream through a ring of three chunks of CL loads (half a superstep when U == 4):
+    // chunk q of the slice is loads [q*CL, q*CL + CL) counted from the slice start, with the
+    // CS = U*CL/NI scales of its quant blocks.
+    constexpr int CL = U == 4 ? NI / 2 : NI;  // loads per chunk
+    constexpr int CPS = NI / CL;              // chunks per superstep
+    constexpr int CS = U / CPS;               // scales per chunk
+    uint4 w0[CL], w1[CL], w2[CL];
+    float s0[CS], s1[CS], s2[CS];
+    const int nch = nss_w * CPS;
+    auto issue = [&](uint4 (&w)[CL], float (&sc)[CS], int q) {
+        const uint8_t* p = wp + (size_t)q * CL * 1024;
 #pragma unroll
-        for (int v = 0; v < NI; ++v) w[v] = *reinterpret_cast<const uint4*>(p + 1024 * v);
-        if constexpr (U == 4) {
-            const float4 t = *reinterpret_cast<const float4*>(sp + (size_t)si * 64 * 4);
-            s[0] = t.x, s[1] = t.y, s[2] = t.z, s[3] = t.w;
+        for (int v = 0; v < CL; ++v) w[v] = *reinterpret_cast<const uint4*>(p + 1024 * v);
+        const float* ps = sp + (size_t)(q / CPS) * 64 * U + (q % CPS) * CS;
+        if constexpr (CS == 2) {
+            const float2 t = *reinterpret_cast<const float2*>(ps);
+            sc[0] = t.x, sc[1] = t.y;
         } else {
-            s[0] = sp[(size_t)si * 64];
+            sc[0] = ps[0];
         }
     };
-    // weights of the first two supersteps are in flight during the prologue
-    if (nss_w > 0) issue(w0, s0, 0);
-    if (nss_w > 1) issue(w1, s1, 1);
+    // ---- prologue, part 1: every load of the token rows comes before the first weight load ----
+    // Vector loads complete in issue order, so a row load issued after the weights would wait for
+    // them; this way the rows are staged while the weights stream in.  Thread tid owns the
+    // 8-element units tid + u*nthr (u < UPT) of every token row.
+    const int row0 = a.row_base ? *a.row_base : 0;
+    const int K8 = K >> 3;
+    float pre0[2 * P], pre1[2 * P];
+    const float4* xrow[2 * P];
+#pragma unroll
+    for (int m = 0; m < 2 * P; ++m) {
+        pre0[m] = 1.0f;
+        pre1[m] = 0.0f;
+        if constexpr (PRO == GEMV_NORM_MHC) {
+            if (m < M) {
+                pre0[m] = a.coef[m * 8];
+                pre1[m] = a.coef[m * 8 + 1];
+            }
+        }
+        xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
+    }
+    float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2];
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+        const int k8 = tid + u * nthr;
+        const int kk = k8 < K8 ? k8 : 0;
+        if constexpr (PRO != GEMV_PLAIN) {
+            nw[u][0] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk];
+            nw[u][1] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk + 1];
+        }
+#pragma unroll
+        for (int m = 0; m < 2 * P; ++m) {
+            if (m < M) {
+                xa[m][u][0] = xrow[m][2 * kk];
+                xa[m][u][1] = xrow[m][2 * kk + 1];
+                if constexpr (PRO == GEMV_NORM_MHC) {
+                    xb[m][u][0] = xrow[m][K4 + 2 * kk];
+                    xb[m][u][1] = xrow[m][K4 + 2 * kk + 1];
+                }
+            } else {
+                xa[m][u][0] = xa[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                xb[m][u][0] = xb[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        }
+    }
 
-    // Thread tid owns output tid of the block (TW*16*M <= 64*TW outputs, fewer than the threads); the
-    // residual it will update is read now, off the critical path.
+    // Thread tid owns output tid of the block (TW*16*M <= 64*TW outputs, fewer than the threads);
+    // the residual it will update is read now, also ahead of the weights.
     const int e_m = tid % M, e_r = tid / M;
     const int e_T = blockIdx.x * TW + (e_r >> 4), e_j = e_r & 15;
     const int e_row = tid < TW * 16 * M && !(EPI == GEMV_SWIGLU && e_j >= 8) ? tile_row<EPI>(a, e_T, e_j) : -1;
@@ -156,76 +206,46 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         }
     }
 
-    // ---- prologue: token rows -> f32 in LDS, reduced per token ----
-    const int row0 = a.row_base ? *a.row_base : 0;
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        if (tid < 2 * P) {
-            coef_s[tid][0] = tid < M ? a.coef[tid * 8] : 0.0f;
-            coef_s[tid][1] = tid < M ? a.coef[tid * 8 + 1] : 0.0f;
-        }
-        __syncthreads();
-    }
-    // region of (token pair p, block bb, token-in-pair t): 128 bytes at ((p*nb + bb)*2 + t)*128.
-    // Each batch issues all of its loads before the first use, so staging costs few round trips.
-    constexpr int BATCH = PRO == GEMV_NORM_MHC ? 2 : 4;
+    // the first weight chunk (the next two follow the prologue, whose row registers they would
+    // otherwise share the register file with)
+    if (nch > 0) issue(w0, s0, 0);
+
+    // ---- prologue, part 2: branch input, per-token sums, f16 hi/lo in MFMA fragment order ----
     float ssq[2 * P], amax[2 * P];
-    const float4* xrow[2 * P];
 #pragma unroll
     for (int m = 0; m < 2 * P; ++m) {
         ssq[m] = 0.0f;
         amax[m] = 0.0f;
-        xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
     }
-    for (int k4b = tid; k4b < K4; k4b += BATCH * nthr) {
-        float4 v[2 * P][BATCH], v1[2 * P][BATCH], nw[BATCH];
 #pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int k4 = k4b + b * nthr;
-            const int kk = k4 < K4 ? k4 : 0;
-            if constexpr (PRO != GEMV_PLAIN) nw[b] = reinterpret_cast<const float4*>(a.norm_w)[kk];
+    for (int u = 0; u < UPT; ++u) {
+        if (tid + u * nthr >= K8) continue;
 #pragma unroll
-            for (int m = 0; m < 2 * P; ++m) {
-                // rows past M stage zeros (the loads are skipped, not selected, so that no
-                // zero vector has to live in memory)
-                if (m < M) {
-                    v[m][b] = xrow[m][kk];
-                    if constexpr (PRO == GEMV_NORM_MHC) v1[m][b] = xrow[m][K4 + kk];
-                } else {
-                    v[m][b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    v1[m][b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int m = 0; m < 2 * P; ++m) {
+            if (m >= M) continue;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float4 t = xa[m][u][hh];
+                if constexpr (PRO == GEMV_NORM_MHC) {
+                    const float4 v1 = xb[m][u][hh];
+                    t.x = pre0[m] * t.x + pre1[m] * v1.x;
+                    t.y = pre0[m] * t.y + pre1[m] * v1.y;
+                    t.z = pre0[m] * t.z + pre1[m] * v1.z;
+                    t.w = pre0[m] * t.w + pre1[m] * v1.w;
                 }
-            }
-        }
-#pragma unroll
-        for (int b = 0; b < BATCH; ++b) {
-            const int k4 = k4b + b * nthr;
-            if (k4 >= K4) continue;
-#pragma unroll
-            for (int m = 0; m < 2 * P; ++m) {
-                float4 t = v[m][b];
-                if (m < M) {
-                    if constexpr (PRO == GEMV_NORM_MHC) {
-                        const float pre0 = coef_s[m][0], pre1 = coef_s[m][1];
-                        const float4 u = v1[m][b];
-                        t.x = pre0 * t.x + pre1 * u.x;
-                        t.y = pre0 * t.y + pre1 * u.y;
-                        t.z = pre0 * t.z + pre1 * u.z;
-                        t.w = pre0 * t.w + pre1 * u.w;
-                    }
-                    if constexpr (PRO != GEMV_PLAIN) {
-                        ssq[m] = fmaf(t.x, t.x, ssq[m]);
-                        ssq[m] = fmaf(t.y, t.y, ssq[m]);
-                        ssq[m] = fmaf(t.z, t.z, ssq[m]);
-                        ssq[m] = fmaf(t.w, t.w, ssq[m]);
-                        t.x = t.x * (1.0f + nw[b].x);
-                        t.y = t.y * (1.0f + nw[b].y);
-                        t.z = t.z * (1.0f + nw[b].z);
-                        t.w = t.w * (1.0f + nw[b].w);
-                    }
-                    amax[m] = fmaxf(amax[m], fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+                if constexpr (PRO != GEMV_PLAIN) {
+                    ssq[m] = fmaf(t.x, t.x, ssq[m]);
+                    ssq[m] = fmaf(t.y, t.y, ssq[m]);
+                    ssq[m] = fmaf(t.z, t.z, ssq[m]);
+                    ssq[m] = fmaf(t.w, t.w, ssq[m]);
+                    const float4 w = nw[u][hh];
+                    t.x = t.x * (1.0f + w.x);
+                    t.y = t.y * (1.0f + w.y);
+                    t.z = t.z * (1.0f + w.z);
+                    t.w = t.w * (1.0f + w.w);
                 }
-                unsigned char* base = lds + (size_t)(m >> 1) * nb * 256 + (m & 1) * 128;
-                *reinterpret_cast<float4*>(base + (size_t)(k4 >> 3) * 256 + (k4 & 7) * 16) = t;
+                amax[m] = fmaxf(amax[m], fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+                xa[m][u][hh] = t;
             }
         }
     }
@@ -234,14 +254,14 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         ssq[m] = wave_sum(ssq[m]);
         amax[m] = wave_max(amax[m]);
     }
-    if (tid < kZeroBytes / 16)
-        reinterpret_cast<float4*>(lds + (size_t)P * nb * 256)[tid] = make_float4(0, 0, 0, 0);
     if (lane == 0)
 #pragma unroll
         for (int m = 0; m < 2 * P; ++m) {
             wred_s[wave][m][0] = ssq[m];
             wred_s[wave][m][1] = amax[m];
         }
+    if (tid < kZeroBytes / 16)
+        reinterpret_cast<float4*>(lds + (size_t)P * nb * 256)[tid] = make_float4(0, 0, 0, 0);
     __syncthreads();
     if (tid < 2 * P) {
         const int m = tid;
@@ -258,32 +278,33 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         tok_s[m][1] = ldexpf(1.0f, e);
     }
     __syncthreads();
-    // f32 region -> f16 hi (first 64 bytes) and lo (last 64 bytes) in MFMA fragment order
-    for (int rg = tid; rg < P * nb * 2; rg += nthr) {
-        const int m = 2 * (rg / (2 * nb)) + (rg & 1);
-        const float f = tok_s[m][0];
-        unsigned char* base = lds + (size_t)rg * 128;
-        float v[32];
+    // unit k8 of token m -> 8 hi then 8 lo f16 in fragment order inside region (pair, block, token)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const float4 t = reinterpret_cast<const float4*>(base)[c];
-            v[4 * c] = t.x, v[4 * c + 1] = t.y, v[4 * c + 2] = t.z, v[4 * c + 3] = t.w;
-        }
-        half8_t hi[4], lo[4];
+    for (int u = 0; u < UPT; ++u) {
+        const int k8 = tid + u * nthr;
+        if (k8 >= K8) continue;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float y = v[e] * f;
-            const _Float16 h = (_Float16)y;
-            const int pidx = a_pos<QT>(e);
-            hi[pidx >> 3][pidx & 7] = h;
-            lo[pidx >> 3][pidx & 7] = (_Float16)(y - (float)h);
-        }
+        for (int m = 0; m < 2 * P; ++m) {
+            const float f = tok_s[m][0];
+            const float v[8] = {xa[m][u][0].x, xa[m][u][0].y, xa[m][u][0].z, xa[m][u][0].w,
+                                xa[m][u][1].x, xa[m][u][1].y, xa[m][u][1].z, xa[m][u][1].w};
+            half8_t hi, lo;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            reinterpret_cast<half8_t*>(base)[c] = hi[c];
-            reinterpret_cast<half8_t*>(base + 64)[c] = lo[c];
+            for (int e = 0; e < 8; ++e) {
+                const float y = v[e] * f;
+                const _Float16 hv = (_Float16)y;
+                const int pidx = a_pos<QT>(e);
+                hi[pidx] = hv;
+                lo[pidx] = (_Float16)(y - (float)hv);
+            }
+            unsigned char* base =
+                lds + ((size_t)(m >> 1) * nb + (k8 >> 2)) * 256 + (m & 1) * 128 + (k8 & 3) * 16;
+            *reinterpret_cast<half8_t*>(base) = hi;
+            *reinterpret_cast<half8_t*>(base + 64) = lo;
         }
     }
+    if (nch > 1) issue(w1, s1, 1);
+    if (nch > 2) issue(w2, s2, 2);
     __syncthreads();
 
     // ---- main loop ----
@@ -295,10 +316,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     for (int p = 0; p < P; ++p) acc[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     const int zero_off = P * nb * 256;
 
-    auto compute = [&](const uint4 (&w)[NI], const float (&s)[U], int si) {
-        const int S = ks * nss_w + si;  // superstep within the row
+    auto compute = [&](const uint4 (&w)[CL], const float (&sc)[CS], int q) {
+        const int S = ks * nss_w + q / CPS;  // superstep within the row
 #pragma unroll
-        for (int v = 0; v < NI; ++v) {
+        for (int i0 = 0; i0 < CL; ++i0) {
+            const int v = (q % CPS) * CL + i0;                              // load within the superstep
             const int blk = S * 4 * U + U * g + (QT == 0 ? (v >> 1) : v);  // quant block of this load
             const int eoff = QT == 0 ? (v & 1) * 16 : 0;                  // first element in the block
             int abase[P];
@@ -310,27 +332,31 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             for (int p = 0; p < P; ++p) d[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int i = 0; i < NM; ++i) {
-                const half8_t b = dequant8<QT>(w[v], i);
+                const half8_t b = dequant8<QT>(w[i0], i);
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
                     const half8_t av = *reinterpret_cast<const half8_t*>(lds + abase[p] + (a_on ? 16 * i : 0));
                     d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, d[p], 0, 0, 0);
                 }
             }
-            const float sc = s[QT == 0 ? (v >> 1) : v];
+            const float scale = sc[QT == 0 ? (i0 >> 1) : i0];
 #pragma unroll
             for (int p = 0; p < P; ++p)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[p][r] = fmaf(sc, d[p][r], acc[p][r]);
+                for (int r = 0; r < 4; ++r) acc[p][r] = fmaf(scale, d[p][r], acc[p][r]);
         }
     };
 
-    for (int s = 0; s < nss_w; s += 2) {
-        compute(w0, s0, s);
-        if (s + 2 < nss_w) issue(w0, s0, s + 2);
-        if (s + 1 < nss_w) {
-            compute(w1, s1, s + 1);
-            if (s + 3 < nss_w) issue(w1, s1, s + 3);
+    for (int q = 0; q < nch; q += 3) {
+        compute(w0, s0, q);
+        if (q + 3 < nch) issue(w0, s0, q + 3);
+        if (q + 1 < nch) {
+            compute(w1, s1, q + 1);
+            if (q + 4 < nch) issue(w1, s1, q + 4);
+        }
+        if (q + 2 < nch) {
+            compute(w2, s2, q + 2);
+            if (q + 5 < nch) issue(w2, s2, q + 5);
         }
     }
 
@@ -379,10 +405,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
 
 using KernelFn = void (*)(GemvArgs, int, int, int, int, int);
 
-template <int QT, int U>
+template <int QT, int U, int UPT>
 KernelFn pick_fn(int P, int epi, int pro) {
 #define SNL_G(E, PR) \
-    if (epi == E && pro == PR) return &mgemv_kernel<QT, 1, E, PR, U>;
+    if (epi == E && pro == PR) return &mgemv_kernel<QT, 1, E, PR, U, UPT>;
     if (P == 1) {
         SNL_G(GEMV_STORE, GEMV_PLAIN)
         SNL_G(GEMV_STORE, GEMV_NORM)
@@ -395,15 +421,26 @@ KernelFn pick_fn(int P, int epi, int pro) {
         SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
     }
 #undef SNL_G
-    // two token pairs: the plain product only (kernel-level calls with M = 3, 4)
-    if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U>;
+    // two token pairs: the plain product at K <= 4096 only (kernel-level calls with M = 3, 4)
+    if constexpr (UPT == 1)
+        if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U, 1>;
     return nullptr;
 }
 
-KernelFn pick(int quant, int U, int P, int epi, int pro) {
-    if (quant == 0) return U == 4 ? pick_fn<0, 4>(P, epi, pro) : pick_fn<0, 1>(P, epi, pro);
-    return U == 4 ? pick_fn<1, 4>(P, epi, pro) : pick_fn<1, 1>(P, epi, pro);
+KernelFn pick(int quant, int U, int UPT, int P, int epi, int pro) {
+    if (UPT == 1) {
+        if (quant == 0) return U == 4 ? pick_fn<0, 4, 1>(P, epi, pro) : pick_fn<0, 1, 1>(P, epi, pro);
+        return U == 4 ? pick_fn<1, 4, 1>(P, epi, pro) : pick_fn<1, 1, 1>(P, epi, pro);
+    }
+    if (UPT == 3) {
+        if (quant == 0) return U == 4 ? pick_fn<0, 4, 3>(P, epi, pro) : pick_fn<0, 1, 3>(P, epi, pro);
+        return U == 4 ? pick_fn<1, 4, 3>(P, epi, pro) : pick_fn<1, 1, 3>(P, epi, pro);
+    }
+    return nullptr;
 }
+
+// token-row units per thread: one 8-element unit per 512 threads, 1 up to K = 4096, 3 up to 12288
+int upt_for(int K) { return K <= 8 * 512 ? 1 : (K <= 3 * 8 * 512 ? 3 : 0); }
 
 __global__ __launch_bounds__(256) void pack_q_kernel(PackGeom g, const uint8_t* q, uint8_t* qp) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece
@@ -443,30 +480,34 @@ int launch_pack_matrix(const PackGeom& g, const void* q, const float* s, void* q
 int mgemv_init() {
     for (int q = 0; q < 2; ++q)
         for (int U = 1; U <= 4; U += 3)
-            for (int P = 1; P <= 2; ++P)
-                for (int e = 0; e < 4; ++e)
-                    for (int p = 0; p < 3; ++p) {
-                        KernelFn f = pick(q, U, P, e, p);
-                        if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     kLdsLimit) != hipSuccess)
-                            return -2;
-                    }
+            for (int upt = 1; upt <= 3; upt += 2)
+                for (int P = 1; P <= 2; ++P)
+                    for (int e = 0; e < 4; ++e)
+                        for (int p = 0; p < 3; ++p) {
+                            KernelFn f = pick(q, U, upt, P, e, p);
+                            if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                         kLdsLimit) != hipSuccess)
+                                return -2;
+                        }
     return 0;
 }
 
-// Launch shape from the matrix shape only: K slices KS, tiles per block TW, supersteps per wave.
+// Launch shape from the matrix shape only: blocks of kMaxWaves waves; K slices KS (the fewest that
+// still give every CU a block), tiles per block TW = kMaxWaves / KS, supersteps per wave.
 void mgemv_shape(const PackGeom& g, int* KS, int* TW, int* nss_w) {
     *KS = 1;
-    while (*KS < kMaxWaves && (long)g.tiles * *KS < kTargetItems && g.nss % (2 * *KS) == 0) *KS *= 2;
-    const int NW = *KS < 4 ? 4 : *KS;
-    *TW = NW / *KS;
+    while (*KS < kMaxWaves && g.nss % (2 * *KS) == 0 && (long)g.tiles * *KS < (long)kCUs * kMaxWaves) *KS *= 2;
+    *TW = kMaxWaves / *KS;
     *nss_w = g.nss / *KS;
 }
 
 size_t mgemv_lds_bytes(int M, int K) { return (size_t)(M <= 2 ? 1 : 2) * (K / 32) * 256 + kZeroBytes; }
 
-bool mgemv_fits(int M, int K) { return mgemv_lds_bytes(M, K) <= (size_t)kLdsLimit; }
+bool mgemv_fits(int M, int K) {
+    const int upt = upt_for(K);
+    return upt && (M <= 2 || upt == 1) && mgemv_lds_bytes(M, K) <= (size_t)kLdsLimit;
+}
 
 // 0: launched; 1: this call is not served (M too large for LDS at this K); < 0 error.
 // The weights are in tile order (packing.h) for (N, K, inter when SwiGLU).
@@ -481,7 +522,7 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
         (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_stride & 3))
         return -1;
-    KernelFn f = pick(quant, g.U, P, a.epi, a.pro);
+    KernelFn f = pick(quant, g.U, upt_for(a.K), P, a.epi, a.pro);
     if (!f) return 1;
     dim3 grid((g.tiles + TW - 1) / TW);
     hipLaunchKernelGGL(f, grid, dim3(KS * TW * 64), lds, s, a, M, KS, TW, nss_w, g.tiles);
