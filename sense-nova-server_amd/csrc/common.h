@@ -40,6 +40,24 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// N independent wave sums, level by level so the N exchanges of a level overlap; each value gets
+// exactly the additions of wave_sum.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], o, SNL_WAVE);
+}
+
+template <int N>
+__device__ __forceinline__ void wave_max_n(float (&v)[N]) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __shfl_xor(v[i], o, SNL_WAVE));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SNL_WAVE));

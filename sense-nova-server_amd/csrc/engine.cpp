@@ -58,6 +58,16 @@ uint64_t stream_key(uint64_t seed, int layer, int kind) {
     return host_smix(seed ^ host_smix(stream * 0xD1B54A32D192ED03ull));
 }
 
+// mHC roles of a GEMV launch: `site` is the router of its own site (NORM_MHC prologue: sums from
+// the partials in mhc_part, coefficients left in coef for the site's MHC epilogue), `next` the
+// router of the next site whose partials its epilogue leaves in mhc_part (expand: stream 1 :=
+// stream 0 first).
+struct MhcRole {
+    const float* site = nullptr;
+    const float* next = nullptr;
+    int expand = 0;
+};
+
 struct QW {
     void* q = nullptr;
     float* s = nullptr;
@@ -106,7 +116,7 @@ struct snl_engine {
     int h = 0, q_dim = 0, kv_dim = 0, conv_dim = 0, lin_proj_rows = 0, attn_proj_rows = 0, lin_value_dim = 0;
 
     float *x = nullptr, *xn = nullptr, *proj = nullptr, *act = nullptr, *attn_out = nullptr, *qbuf = nullptr;
-    float *coef = nullptr, *mhc_raw = nullptr, *partial = nullptr, *logits = nullptr, *hid = nullptr,
+    float *coef = nullptr, *mhc_raw = nullptr, *mhc_part = nullptr, *partial = nullptr, *logits = nullptr, *hid = nullptr,
           *hlast = nullptr;
     float *mx = nullptr, *hn = nullptr, *m_logits = nullptr;
     uint16_t *kcache = nullptr, *vcache = nullptr, *m_kc = nullptr, *m_vc = nullptr;
@@ -255,10 +265,18 @@ struct snl_engine {
     int record_forward(int M, int rows, int ckpt);
     int record_mtp(int M, int draft);
     int run(int kind, int M, int a, int b);
+    static constexpr int kPartBlocks = 4096;  // partial-sum slots of mhc_part per token
+    int part_n = 0;                           // partials currently in mhc_part (0: none)
     // GEMV with an optional fused branch-input prologue (pro: GEMV_NORM with norm weights nw, or
-    // GEMV_NORM_MHC, whose pre-mix coefficients launch_mhc left in coef) and the epilogue `epi`.
+    // GEMV_NORM_MHC) and the epilogue `epi`.
     int gemv(const char* name, const QW& w, const float* xin, int x_stride, float* y, int y_stride, int M, int epi,
-             int merge_mode = 0, int pro = GEMV_PLAIN, const float* nw = nullptr, const int32_t* row_base = nullptr) {
+             int merge_mode = 0, int pro = GEMV_PLAIN, const float* nw = nullptr, const int32_t* row_base = nullptr,
+             MhcRole mr = {}) {
+        if (mr.next) {  // this launch leaves the next site's partials, launched or not (isolated timing)
+            const int n = mgemv_blocks(w.quant, w.rows, w.cols, epi == GEMV_SWIGLU ? cfg.intermediate : 0);
+            if (n < 1 || n > kPartBlocks) return SNL_EDEVICE;
+            part_n = n;
+        }
         if (!op(name, gemv_bytes(w, M, epi, cfg.intermediate))) return 0;
         GemvArgs g{};
         g.packed = w.packed ? 1 : 0;
@@ -272,15 +290,24 @@ struct snl_engine {
         g.N = w.rows;
         g.K = w.cols;
         g.epi = epi;
-        g.coef = coef;
         g.merge_mode = merge_mode;
         g.h = h;
         g.inter = cfg.intermediate;
         g.pro = pro;
         g.norm_w = nw;
         g.eps = cfg.eps;
+        g.site_w = mr.site;
+        g.raw = mhc_raw;
+        g.coef = coef;
+        g.rin = mhc_part;
+        g.rin_n = pro == GEMV_NORM_MHC ? consumed_n : 0;
+        g.iterations = cfg.mhc_iterations;
+        g.next_w = mr.next;
+        g.rpart = mr.next ? mhc_part : nullptr;
+        g.expand = mr.expand;
         return launch_gemv(g, w.quant, M, stream);
     }
+    int consumed_n = 0;  // partial count a NORM_MHC launch adds up
     int norm(const float* xin, int x_stride, const int32_t* row_base, int mode, const float* w, float* out,
              int first, int count) {
         NormArgs a{};
@@ -422,6 +449,7 @@ int snl_engine::init() {
         (rc = dalloc(&proj, (size_t)M * proj_w)) || (rc = dalloc(&act, (size_t)M * act_w)) ||
         (rc = dalloc(&attn_out, (size_t)M * attn_w)) || (rc = dalloc(&qbuf, (size_t)M * q_dim)) ||
         (rc = dalloc(&coef, (size_t)M * 8)) || (rc = dalloc(&mhc_raw, (size_t)M * 9)) ||
+        (rc = dalloc(&mhc_part, (size_t)kPartBlocks * M * 9)) ||
         (rc = dalloc(&partial, (size_t)M * c.n_heads * parts_max * (c.head_dim + 2))) ||
         (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)(M + 1) * h)) ||
         (rc = dalloc(&hlast, (size_t)h)) || (rc = dalloc(&mx, (size_t)M * 2 * h)) ||
@@ -473,25 +501,38 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
     int fslot = 0, lslot = 0;
     const size_t kvn = (size_t)ctx * kv_dim;
     const size_t nl = std::max(n_lin, 1);
-    for (int li : plan) {
+    part_n = 0;
+    for (size_t vi = 0; vi < plan.size(); ++vi) {
+        const int li = plan[vi];
         const Layer& L = layers[li];
         const bool mhc = is_mhc(li);
-        if (mhc && li == c.mhc_start) {
-            if (op("expand", 0.0)) rc |= launch_expand(x, h, M, stream);
+        const int ln = vi + 1 < plan.size() ? plan[vi + 1] : -1;  // layer of the next visit
+        // An mHC site's router sums arrive as partials from the GEMV that produced the row (the
+        // previous visit's down projection, or this visit's output projection); a site that no
+        // GEMV precedes runs the stream copy (mode 3) and the router kernel instead.
+        if (mhc && !part_n) {
+            if (li == c.mhc_start && op("expand", 0.0)) rc |= launch_expand(x, h, M, stream);
+            if (op("mhc", 0.0)) rc |= launch_mhc(x, L.mhc_attn.p, mhc_part, h, M, stream);
+            part_n = 1;
         }
         // branch input: RMSNorm (1 + in_ln) of stream 0, or of the mHC pre-mix, fused into the GEMV
-        if (mhc) {
-            if (op("mhc", 0.0)) rc |= launch_mhc(x, L.mhc_attn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
-        }
         const int pro = mhc ? GEMV_NORM_MHC : GEMV_NORM;
+        consumed_n = mhc ? part_n : 0;
+        const MhcRole site_attn{mhc ? L.mhc_attn.p : nullptr};
+        // the output projection merges the attention site and leaves the FFN site's partials
+        const MhcRole merge_attn{mhc ? L.mhc_attn.p : nullptr, mhc ? L.mhc_ffn.p : nullptr, 0};
+        part_n = 0;
         if (L.full) {
-            rc |= gemv("gemv_qkv", L.mix_in, x, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p);
+            rc |= gemv("gemv_qkv", L.mix_in, x, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p,
+                       nullptr, site_attn);
             AttnArgs a = attn_args(d_step, kcache + kvn * fslot, vcache + kvn * fslot, L.small.p);
             if (op("attention", 0.0)) rc |= launch_attention(a, M, stream);
-            rc |= gemv("gemv_o", L.mix_out, attn_out, q_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, 1);
+            rc |= gemv("gemv_o", L.mix_out, attn_out, q_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, 1, GEMV_PLAIN,
+                       nullptr, nullptr, merge_attn);
             ++fslot;
         } else {
-            rc |= gemv("gemv_in_proj", L.mix_in, x, 2 * h, proj, lin_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p);
+            rc |= gemv("gemv_in_proj", L.mix_in, x, 2 * h, proj, lin_proj_rows, M, GEMV_STORE, 0, pro, L.in_ln.p,
+                       nullptr, site_attn);
             DeltaArgs d{};
             d.proj = proj;
             d.proj_stride = lin_proj_rows;
@@ -509,15 +550,23 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             const double dn_bytes = 2.0 * 4.0 * (double)state_floats + (ckpt ? 4.0 * (double)state_floats : 0.0);
             if (op("deltanet", dn_bytes)) rc |= launch_deltanet(d, M, stream);
             rc |= gemv("gemv_out_proj", L.mix_out, attn_out, lin_value_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD,
-                       1);
+                       1, GEMV_PLAIN, nullptr, nullptr, merge_attn);
             ++lslot;
         }
-        if (mhc) {
-            if (op("mhc", 0.0)) rc |= launch_mhc(x, L.mhc_ffn.p, mhc_raw, coef, h, M, c.mhc_iterations, stream);
-        }
-        rc |= gemv("gemv_gate_up", L.gate_up, x, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, pro, L.post_ln.p);
+        consumed_n = mhc ? part_n : 0;
+        rc |= gemv("gemv_gate_up", L.gate_up, x, 2 * h, act, c.intermediate, M, GEMV_SWIGLU, 0, pro, L.post_ln.p,
+                   nullptr, MhcRole{mhc ? L.mhc_ffn.p : nullptr});
+        // the down projection merges the FFN site and leaves the next visit's attention-site
+        // partials: after a mode 1 merge into the mHC range, or with the stream copy (mode 3) when
+        // the next visit starts the range
         const int mode = !mhc ? 0 : (li + 1 == c.mhc_end ? 2 : 1);
-        rc |= gemv("gemv_down", L.down, act, c.intermediate, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, mode);
+        const bool next_mhc = ln >= 0 && is_mhc(ln);
+        const bool next_start = next_mhc && ln == c.mhc_start;
+        const bool leave = next_start || (next_mhc && mhc && mode == 1);
+        part_n = 0;
+        rc |= gemv("gemv_down", L.down, act, c.intermediate, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD, mode,
+                   GEMV_PLAIN, nullptr, nullptr,
+                   MhcRole{mhc ? L.mhc_ffn.p : nullptr, leave ? layers[ln].mhc_attn.p : nullptr, next_start ? 1 : 0});
     }
     rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M);
     if (rows > 0) {

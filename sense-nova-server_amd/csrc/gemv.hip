@@ -20,20 +20,13 @@
 // into bytes and converted the same way, minus 8 sum x.  The 16-element sums of x are staged in
 // LDS with x.
 //
-// Prologue (fused branch input, layers.wgsl:46-73 and :94-126): the staged rows are either the
-// plain x rows, or RMSNorm(x0)*(1+w), or, inside the mHC range, RMSNorm(pre0*x0 + pre1*x1)*(1+w)
-// with pre from the router dots and a 2x2 log-space Sinkhorn computed by the block itself
-// (block 0 also stores the token coefficients for the merge epilogue).
-//
 // Reduction.  Per group each lane holds 4 row partials per token row; a transposed butterfly
 // (xor 32, 16 exchange halves, then xor 8..1 add) leaves lane 16r with row r.  Every token row
-// takes the same instruction sequence whatever M and its index are, so a token's row of an M=2
-// call is bitwise the row of an M=1 call (greedy output is then byte-identical with and without
-// speculative drafting).
+// takes the same instruction sequence whatever M and its index are.
 //
-// Epilogues: plain store; residual add into stream 0 (merge mode 0, layers.wgsl:142-145); mHC
-// merge (modes 1/2, layers.wgsl:150-161); SwiGLU pairs (layers.wgsl:164-175): a group owns gate
-// rows c0, c0+1 and the matching up rows and writes act directly.
+// This vector-ALU kernel serves kernel-level calls on row-major weights that the matrix-core
+// kernel (mgemv.hip, tile-order weights) does not take: K % 128 != 0, or M = 3..4 at K > 4096.
+// It computes the plain product y = W x.
 #include "common.h"
 #include "kernels.h"
 
@@ -46,17 +39,10 @@ namespace {
 constexpr int kThreads = 256, kWaves = 4, kChunk = 1024;
 constexpr int kLdsFloats = 32768;  // token rows staged in LDS: M * K (whole chunks) <= 32768 floats
 
-template <int EPI>
 __device__ __forceinline__ int group_row(const GemvArgs& a, int blk, int G, int wg, int r) {
     // wg = wave * G + g; returns the weight row of row r (0..3) of the group or -1
-    if constexpr (EPI == GEMV_SWIGLU) {
-        const int c0 = blk * 8 * G + wg * 2 + (r & 1);
-        if (c0 >= a.inter) return -1;
-        return r < 2 ? c0 : a.inter + c0;
-    } else {
-        const int row = blk * 16 * G + wg * 4 + r;
-        return row < a.N ? row : -1;
-    }
+    const int row = blk * 16 * G + wg * 4 + r;
+    return row < a.N ? row : -1;
 }
 
 template <int QT>
@@ -109,11 +95,9 @@ __device__ __forceinline__ int lds_f4(int k4) {  // k4 = k / 4
     return (c << 8) + (v << 6) + l;
 }
 
-template <int QT, int M, int EPI, int PRO>
+template <int QT, int M>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
     extern __shared__ float4 lds4[];
-    __shared__ float coef_s[SNL_MAX_M][2];
-    __shared__ float red_s[kWaves][SNL_MAX_M];
     const int K = a.K, K4 = K >> 2, K16 = K >> 4;
     const int nchunks = (K + kChunk - 1) / kChunk;
     const int K4p = nchunks * (kChunk / 4);                         // staged row length, whole chunks
@@ -127,74 +111,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
     uint32_t wc[4][4], wn[4][4];
     float scc[4], scn[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) load_frag<QT>(a, group_row<EPI>(a, blk, G, wave * G, r), lane * 16, wc[r], scc[r]);
+    for (int r = 0; r < 4; ++r) load_frag<QT>(a, group_row(a, blk, G, wave * G, r), lane * 16, wc[r], scc[r]);
 
-    // ---- prologue: stage the token rows (optionally normalised) in LDS ----
+    // ---- prologue: stage the token rows in LDS ----
     const int row0 = a.row_base ? *a.row_base : 0;
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        if (tid < 2 * M) {
-            coef_s[tid][0] = tid < M ? a.coef[tid * 8] : 0.0f;
-            coef_s[tid][1] = tid < M ? a.coef[tid * 8 + 1] : 0.0f;
-        }
-        __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float4* xr = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + m) * a.x_stride);
+        for (int k4 = tid; k4 < K4; k4 += kThreads) xs4[m * K4p + lds_f4(k4)] = xr[k4];
     }
-    if constexpr (PRO == GEMV_PLAIN) {
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float4* xr = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + m) * a.x_stride);
-            for (int k4 = tid; k4 < K4; k4 += kThreads) xs4[m * K4p + lds_f4(k4)] = xr[k4];
-        }
-        __syncthreads();
-    } else {
-        float ss[M];
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float4* x0 = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + m) * a.x_stride);
-            const float pre0 = PRO == GEMV_NORM_MHC ? coef_s[m][0] : 1.0f;
-            const float pre1 = PRO == GEMV_NORM_MHC ? coef_s[m][1] : 0.0f;
-            float acc = 0.0f;
-            for (int k4 = tid; k4 < K4; k4 += kThreads) {
-                float4 v = x0[k4];
-                if constexpr (PRO == GEMV_NORM_MHC) {
-                    const float4 w1 = x0[K4 + k4];
-                    v.x = pre0 * v.x + pre1 * w1.x;
-                    v.y = pre0 * v.y + pre1 * w1.y;
-                    v.z = pre0 * v.z + pre1 * w1.z;
-                    v.w = pre0 * v.w + pre1 * w1.w;
-                }
-                acc = fmaf(v.x, v.x, acc);
-                acc = fmaf(v.y, v.y, acc);
-                acc = fmaf(v.z, v.z, acc);
-                acc = fmaf(v.w, v.w, acc);
-                xs4[m * K4p + lds_f4(k4)] = v;
-            }
-            ss[m] = wave_sum(acc);
-        }
-        if (lane == 0)
-#pragma unroll
-            for (int m = 0; m < M; ++m) red_s[wave][m] = ss[m];
-        __syncthreads();
-        // scale by rinv * (1 + w) in place
-        float rinv[M];
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float total = ((red_s[0][m] + red_s[1][m]) + red_s[2][m]) + red_s[3][m];
-            rinv[m] = 1.0f / sqrtf(total / (float)K + a.eps);
-        }
-        const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
-#pragma unroll
-        for (int m = 0; m < M; ++m)
-            for (int k4 = tid; k4 < K4; k4 += kThreads) {
-                float4 v = xs4[m * K4p + lds_f4(k4)];
-                const float4 w = w4[k4];
-                v.x = (v.x * rinv[m]) * (1.0f + w.x);
-                v.y = (v.y * rinv[m]) * (1.0f + w.y);
-                v.z = (v.z * rinv[m]) * (1.0f + w.z);
-                v.w = (v.w * rinv[m]) * (1.0f + w.w);
-                xs4[m * K4p + lds_f4(k4)] = v;
-            }
-        __syncthreads();
-    }
+    __syncthreads();
     // 16-element sums for the dequantisation bias
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -226,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
             const int g1 = (s + 1) / nchunks, c1 = (s + 1) - g1 * nchunks;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                load_frag<QT>(a, group_row<EPI>(a, blk, G, wave * G + g1, r), c1 * kChunk + lane * 16, wn[r], scn[r]);
+                load_frag<QT>(a, group_row(a, blk, G, wave * G + g1, r), c1 * kChunk + lane * 16, wn[r], scn[r]);
         }
         const int k = c * kChunk + lane * 16;
         if (k < K) {
@@ -271,45 +197,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
                 for (int r = 0; r < 4; ++r) acc[r][m] = 0.0f;
             }
             const int r = lane >> 4;
-            const int wg = wave * G + g;
-            if constexpr (EPI == GEMV_SWIGLU) {
+            const int row = group_row(a, blk, G, wave * G + g, r);
+            if ((lane & 15) == 0 && row >= 0)
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    const float u = __shfl(out[m], (lane + 32) & 63, 64);
-                    if ((lane & 15) == 0 && r < 2) {
-                        const int row = group_row<EPI>(a, blk, G, wg, r);
-                        if (row >= 0) {
-                            const float gt = out[m];
-                            a.y[(size_t)m * a.y_stride + row] = gt / (1.0f + expf(-gt)) * u;
-                        }
-                    }
-                }
-            } else {
-                const int row = group_row<EPI>(a, blk, G, wg, r);
-                if ((lane & 15) == 0 && row >= 0) {
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        float* y = a.y + (size_t)m * a.y_stride;
-                        const float v = out[m];
-                        if constexpr (EPI == GEMV_STORE) {
-                            y[a.n_off + row] = v;
-                        } else if constexpr (EPI == GEMV_ADD) {
-                            y[row] = y[row] + v;
-                        } else {  // GEMV_MHC, layers.wgsl:150-161
-                            const float* cf = a.coef + m * 8;
-                            const float x0 = y[row], x1 = y[a.h + row];
-                            const float n0 = (cf[4] * x0 + cf[5] * x1) + cf[2] * v;
-                            const float n1 = (cf[6] * x0 + cf[7] * x1) + cf[3] * v;
-                            if (a.merge_mode == 2) {
-                                y[row] = 0.5f * (n0 + n1);
-                            } else {
-                                y[row] = n0;
-                                y[a.h + row] = n1;
-                            }
-                        }
-                    }
-                }
-            }
+                for (int m = 0; m < M; ++m) a.y[(size_t)m * a.y_stride + a.n_off + row] = out[m];
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -320,40 +211,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
     }
 }
 
-template <int QT, int M, int EPI, int PRO>
-void* kernel_ptr() {
-    return reinterpret_cast<void*>(&gemv_kernel<QT, M, EPI, PRO>);
-}
-
 using KernelFn = void (*)(GemvArgs, int);
 
-template <int QT, int M>
-KernelFn pick_fn(int epi, int pro) {
-#define SNL_G(E, P) \
-    if (epi == E && pro == P) return &gemv_kernel<QT, M, E, P>;
-    SNL_G(GEMV_STORE, GEMV_PLAIN)
-    SNL_G(GEMV_STORE, GEMV_NORM)
-    SNL_G(GEMV_STORE, GEMV_NORM_MHC)
-    SNL_G(GEMV_ADD, GEMV_PLAIN)
-    SNL_G(GEMV_ADD, GEMV_NORM)
-    SNL_G(GEMV_MHC, GEMV_PLAIN)
-    SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
-    SNL_G(GEMV_SWIGLU, GEMV_NORM)
-    SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
-#undef SNL_G
-    return nullptr;
-}
-
-KernelFn pick(int quant, int M, int epi, int pro) {
+KernelFn pick(int quant, int M) {
     switch (quant * 8 + M) {
-        case 1: return pick_fn<0, 1>(epi, pro);
-        case 2: return pick_fn<0, 2>(epi, pro);
-        case 3: return pick_fn<0, 3>(epi, pro);
-        case 4: return pick_fn<0, 4>(epi, pro);
-        case 9: return pick_fn<1, 1>(epi, pro);
-        case 10: return pick_fn<1, 2>(epi, pro);
-        case 11: return pick_fn<1, 3>(epi, pro);
-        case 12: return pick_fn<1, 4>(epi, pro);
+        case 1: return &gemv_kernel<0, 1>;
+        case 2: return &gemv_kernel<0, 2>;
+        case 3: return &gemv_kernel<0, 3>;
+        case 4: return &gemv_kernel<0, 4>;
+        case 9: return &gemv_kernel<1, 1>;
+        case 10: return &gemv_kernel<1, 2>;
+        case 11: return &gemv_kernel<1, 3>;
+        case 12: return &gemv_kernel<1, 4>;
     }
     return nullptr;
 }
@@ -370,14 +239,12 @@ int groups_for(int N) {
 int gemv_init() {
     const int bytes = kLdsFloats * 4 + kLdsFloats / 16 * 4;
     for (int q = 0; q < 2; ++q)
-        for (int M = 1; M <= SNL_MAX_M; ++M)
-            for (int e = 0; e < 4; ++e)
-                for (int p = 0; p < 3; ++p) {
-                    KernelFn f = pick(q, M, e, p);
-                    if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess)
-                        return -2;
-                }
+        for (int M = 1; M <= SNL_MAX_M; ++M) {
+            KernelFn f = pick(q, M);
+            if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         bytes) != hipSuccess)
+                return -2;
+        }
     return mgemv_init();
 }
 
@@ -389,17 +256,17 @@ int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
         const int rc = launch_mgemv(a, quant, M, s);
         return rc == 1 ? -1 : rc;
     }
+    // row-major weights: the plain product only
+    if (a.epi != GEMV_STORE || a.pro != GEMV_PLAIN) return -1;
     const int K4p = (a.K + kChunk - 1) / kChunk * (kChunk / 4);
     if ((size_t)M * K4p * 4 > (size_t)kLdsFloats) {
-        if (a.pro != GEMV_PLAIN || a.row_base) return -1;
+        if (a.row_base) return -1;
         return launch_gemv_ksplit(a, quant, M, s);
     }
-    KernelFn f = pick(quant, M, a.epi, a.pro);
+    KernelFn f = pick(quant, M);
     if (!f) return -1;
     const int G = groups_for(a.N);
-    const int rows_per_block = a.epi == GEMV_SWIGLU ? 8 * G : 16 * G;
-    const int n_out = a.epi == GEMV_SWIGLU ? a.inter : a.N;
-    dim3 grid((n_out + rows_per_block - 1) / rows_per_block);
+    dim3 grid((a.N + 16 * G - 1) / (16 * G));
     const size_t lds = (size_t)M * K4p * 16 + (size_t)M * (a.K / 16) * 4;
     hipLaunchKernelGGL(f, grid, dim3(kThreads), lds, s, a, G);
     return hipGetLastError() == hipSuccess ? 0 : -2;

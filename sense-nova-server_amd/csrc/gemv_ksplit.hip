@@ -27,9 +27,7 @@
 // bitwise equal to the same row in an M=1 call (greedy output is then byte-identical
 // with and without speculative drafting).
 //
-// Epilogues: plain store; residual add into stream 0 (merge mode 0, layers.wgsl:142-145);
-// mHC merge (modes 1/2, layers.wgsl:150-161); SwiGLU pairs (layers.wgsl:164-175), where
-// a block owns gate rows [8b, 8b+8) and the matching up rows, and writes act directly.
+// It computes the plain product y = W x for kernel-level calls on row-major weights.
 #include "common.h"
 #include "kernels.h"
 
@@ -43,11 +41,7 @@ constexpr int kRows = 16;
 constexpr int kThreads = 256;
 constexpr int kChunk = 1024;
 
-template <int EPI>
-__device__ __forceinline__ int row_of(int blk, int r, int inter) {
-    if constexpr (EPI == GEMV_SWIGLU) return r < 8 ? blk * 8 + r : inter + blk * 8 + (r - 8);
-    return blk * kRows + r;
-}
+__device__ __forceinline__ int row_of(int blk, int r) { return blk * kRows + r; }
 
 // sum over the lane's 16 products of (byte value) * x, for one token row
 template <int QT>
@@ -73,7 +67,7 @@ __device__ __forceinline__ void dot16(const uint32_t (&w)[4], const float (&x)[1
     }
 }
 
-template <int QT, int M, int EPI>
+template <int QT, int M>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int blk = blockIdx.x;
@@ -113,8 +107,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 float sc[8];
 #pragma unroll
                 for (int r = 0; r < 8; ++r) {
-                    const int row = row_of<EPI>(blk, r0 + r, a.inter);
-                    const bool ok = EPI == GEMV_SWIGLU ? (blk * 8 + ((r0 + r) & 7) < a.inter) : (row < a.N);
+                    const int row = row_of(blk, r0 + r);
+                    const bool ok = row < a.N;
                     if (ok) {
                         if constexpr (QT == 0) {
                             uint4 t = *reinterpret_cast<const uint4*>(static_cast<const int8_t*>(a.wq) +
@@ -177,58 +171,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __syncthreads();
 
     const int t = threadIdx.x;
-    if constexpr (EPI == GEMV_SWIGLU) {
-        if (t < 8 * M) {
-            const int i = t & 7, m = t >> 3;
-            const int col = blk * 8 + i;
-            if (col < a.inter) {
-                float g = ((red[0][m][i] + red[1][m][i]) + red[2][m][i]) + red[3][m][i];
-                float u = ((red[0][m][8 + i] + red[1][m][8 + i]) + red[2][m][8 + i]) + red[3][m][8 + i];
-                a.y[(size_t)m * a.y_stride + col] = g / (1.0f + expf(-g)) * u;
-            }
-        }
-    } else {
-        if (t < kRows * M) {
-            const int r = t & (kRows - 1), m = t / kRows;
-            const int row = blk * kRows + r;
-            if (row < a.N) {
-                float v = ((red[0][m][r] + red[1][m][r]) + red[2][m][r]) + red[3][m][r];
-                float* y = a.y + (size_t)m * a.y_stride;
-                if constexpr (EPI == GEMV_STORE) {
-                    y[a.n_off + row] = v;
-                } else if constexpr (EPI == GEMV_ADD) {
-                    y[row] = y[row] + v;
-                } else {  // GEMV_MHC: layers.wgsl:150-161
-                    const float* c = a.coef + m * 8;
-                    float x0 = y[row], x1 = y[a.h + row];
-                    float n0 = (c[4] * x0 + c[5] * x1) + c[2] * v;
-                    float n1 = (c[6] * x0 + c[7] * x1) + c[3] * v;
-                    if (a.merge_mode == 2) {
-                        y[row] = 0.5f * (n0 + n1);
-                    } else {
-                        y[row] = n0;
-                        y[a.h + row] = n1;
-                    }
-                }
-            }
+    if (t < kRows * M) {
+        const int r = t & (kRows - 1), m = t / kRows;
+        const int row = blk * kRows + r;
+        if (row < a.N) {
+            const float v = ((red[0][m][r] + red[1][m][r]) + red[2][m][r]) + red[3][m][r];
+            a.y[(size_t)m * a.y_stride + a.n_off + row] = v;
         }
     }
 }
 
 template <int QT, int M>
 int launch_q(const GemvArgs& a, hipStream_t s) {
-    if (a.epi == GEMV_SWIGLU) {
-        dim3 grid((a.inter + 7) / 8);
-        hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_SWIGLU>), grid, dim3(kThreads), 0, s, a);
-    } else {
-        dim3 grid((a.N + kRows - 1) / kRows);
-        switch (a.epi) {
-            case GEMV_STORE: hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_STORE>), grid, dim3(kThreads), 0, s, a); break;
-            case GEMV_ADD: hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_ADD>), grid, dim3(kThreads), 0, s, a); break;
-            case GEMV_MHC: hipLaunchKernelGGL((gemv_kernel<QT, M, GEMV_MHC>), grid, dim3(kThreads), 0, s, a); break;
-            default: return -1;
-        }
-    }
+    dim3 grid((a.N + kRows - 1) / kRows);
+    hipLaunchKernelGGL((gemv_kernel<QT, M>), grid, dim3(kThreads), 0, s, a);
     return 0;
 }
 
@@ -246,8 +202,8 @@ int launch_m(const GemvArgs& a, int M, hipStream_t s) {
 }  // namespace
 
 int launch_gemv_ksplit(const GemvArgs& a, int quant, int M, hipStream_t s) {
-    if (M < 1 || M > SNL_MAX_M || a.K % 32 != 0 || a.K <= 0 || a.N <= 0 || a.pro != GEMV_PLAIN) return -1;
-    if (a.epi == GEMV_SWIGLU && a.N != 2 * a.inter) return -1;
+    if (M < 1 || M > SNL_MAX_M || a.K % 32 != 0 || a.K <= 0 || a.N <= 0) return -1;
+    if (a.pro != GEMV_PLAIN || a.epi != GEMV_STORE) return -1;
     int rc = quant == 0 ? launch_m<0>(a, M, s) : launch_m<1>(a, M, s);
     if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -2;

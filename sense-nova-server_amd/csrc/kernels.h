@@ -28,14 +28,29 @@ struct GemvArgs {
     int N, K;
     int n_off;
     int epi;
-    const float* coef;   // [M, 8] mHC token coefficients (MHC epilogue; NORM_MHC prologue: pre0, pre1)
     int merge_mode;      // MHC: 1 mix, 2 mix then collapse to the mean
     int h;               // MHC: offset of stream 1
     int inter;           // SWIGLU: intermediate size (N == 2*inter; gate rows then up rows)
     int pro;             // GemvPro
     const float* norm_w; // NORM*: weights w of the (1 + w) RMSNorm [K]
     float eps;
+    // mHC router (layers.wgsl:75-126).  A site's router sums (the 8 router-row dots with the
+    // 2-stream row and its sum of squares) arrive as per-block partials [M][9][blocks] from the
+    // GEMV that produced the row.  The NORM_MHC launch of the site adds them in block order and
+    // takes pre0/pre1; its block 0 stores the sums in raw and the token coefficients (post and
+    // the Sinkhorn mix) in coef, which the MHC epilogue of the same site reads.
+    const float* site_w; // NORM_MHC: router of this GEMV's site, [8][2h] then bias[8]
+    float* raw;          // NORM_MHC: [M][9] site sums (block 0)
+    float* coef;         // [M][8] token coefficients: written by NORM_MHC (block 0), read by MHC
+    const float* rin;    // NORM_MHC: partials [M][9][rin_n]
+    int rin_n;
+    int iterations;      // NORM_MHC: Sinkhorn iterations
+    const float* next_w; // ADD / MHC epilogue: router of the next site, whose partials this launch
+    float* rpart;        //   writes to rpart[M][9][gridDim.x] (null: none)
+    int expand;          //   and, at the start of the mHC range, stream 1 := stream 0 first
 };
+// grid size of launch_gemv over tile-order weights (the partial count a producer leaves)
+int mgemv_blocks(int quant, int N, int K, int inter);
 int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s);
 int launch_gemv_ksplit(const GemvArgs& a, int quant, int M, hipStream_t s);
 // Matrix-core path (mgemv.hip) over tile-order weights: 0 launched, 1 not served (M too large for
@@ -72,10 +87,9 @@ struct NormArgs {
 };
 int launch_branch_norm(const NormArgs& a, hipStream_t s);
 
-// mHC router (layers.wgsl:75-126), one block per token: raw[m][0..7] = router rows . [x0, x1],
-// raw[m][8] = sum of squares; coef[m][0..7] = [pre0, pre1, post0, post1, mix00, mix01, mix10,
-// mix11] after `iterations` log-space Sinkhorn steps.
-int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s);
+// mHC router sums (layers.wgsl:75-92) for a site that no GEMV precedes, one block per token:
+// part[m][0..7] = router rows . [x0, x1], part[m][8] = sum of squares (one partial per token).
+int launch_mhc(const float* x, const float* w, float* part, int h, int M, hipStream_t s);
 
 // x[m, h + i] = x[m, i] (merge mode 3, layers.wgsl:146-149)
 int launch_expand(float* x, int h, int M, hipStream_t s);

@@ -79,16 +79,13 @@ __global__ __launch_bounds__(256) void branch_norm_kernel(NormArgs a) {
     }
 }
 
-// mHC router of one token per block (layers.wgsl:75-126): the 8 router-row dots with the 2-stream
-// row [x0, x1] and its sum of squares, then the token's coefficients [pre0, pre1, post0, post1,
-// mix00, mix01, mix10, mix11] (2x2 log-space Sinkhorn).  All loads of a batch are issued before
-// their first use.  raw keeps the 9 sums.
+// mHC router sums of one token per block (layers.wgsl:75-92): the 8 router-row dots with the
+// 2-stream row [x0, x1] and its sum of squares, written as the token's single partial.  All loads
+// of a batch are issued before their first use.
 constexpr int kMhcThreads = 1024;
 
-__global__ __launch_bounds__(kMhcThreads) void mhc_kernel(const float* x, const float* w, float* raw, float* coef,
-                                                          int h, int iterations) {
+__global__ __launch_bounds__(kMhcThreads) void mhc_kernel(const float* x, const float* w, float* part, int h) {
     __shared__ float red[kMhcThreads / 64][9];
-    __shared__ float tot[9];
     const int m = blockIdx.x, tid = threadIdx.x, d = 2 * h, d4 = d / 4;
     const float4* xr = reinterpret_cast<const float4*>(x + (size_t)m * d);
     const float4* wr = reinterpret_cast<const float4*>(w);
@@ -130,8 +127,7 @@ __global__ __launch_bounds__(kMhcThreads) void mhc_kernel(const float* x, const 
             acc[8] = fmaf(v1.w, v1.w, acc[8]);
         }
     }
-#pragma unroll
-    for (int o = 0; o < 9; ++o) acc[o] = wave_sum(acc[o]);
+    wave_sum_n(acc);
     if ((tid & 63) == 0)
 #pragma unroll
         for (int o = 0; o < 9; ++o) red[tid >> 6][o] = acc[o];
@@ -139,15 +135,7 @@ __global__ __launch_bounds__(kMhcThreads) void mhc_kernel(const float* x, const 
     if (tid < 9) {
         float t = 0.0f;
         for (int wv = 0; wv < kMhcThreads / 64; ++wv) t = t + red[wv][tid];
-        tot[tid] = t;
-        raw[m * 9 + tid] = t;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float cf[8];
-        mhc_coefficients(tot, w, d, iterations, cf);
-#pragma unroll
-        for (int o = 0; o < 8; ++o) coef[m * 8 + o] = cf[o];
+        part[m * 9 + tid] = t;
     }
 }
 
@@ -301,9 +289,9 @@ int launch_branch_norm(const NormArgs& a, hipStream_t s) {
     return last_error();
 }
 
-int launch_mhc(const float* x, const float* w, float* raw, float* coef, int h, int M, int iterations, hipStream_t s) {
+int launch_mhc(const float* x, const float* w, float* part, int h, int M, hipStream_t s) {
     if (M < 1 || M > 64 || h % 2) return -1;
-    hipLaunchKernelGGL(mhc_kernel, dim3(M), dim3(kMhcThreads), 0, s, x, w, raw, coef, h, iterations);
+    hipLaunchKernelGGL(mhc_kernel, dim3(M), dim3(kMhcThreads), 0, s, x, w, part, h);
     return last_error();
 }
 

@@ -112,6 +112,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
     __shared__ float wred_s[kMaxWaves][2 * P][2];
     __shared__ float tok_s[2 * P][2];  // per token: input factor, output factor
+    __shared__ float raw_s[2 * P][9];  // mHC site sums (NORM_MHC)
+    __shared__ float cf_s[2 * P][8];   // mHC token coefficients (MHC epilogue)
+    __shared__ float pr_s[kMaxWaves * 16 / 32][2 * P][9];  // next-site router sums per 32-row group
     constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
     constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
     const int K = a.K, nb = K >> 5, K4 = K >> 2;
@@ -153,19 +156,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     // 8-element units tid + u*nthr (u < UPT) of every token row.
     const int row0 = a.row_base ? *a.row_base : 0;
     const int K8 = K >> 3;
-    float pre0[2 * P], pre1[2 * P];
     const float4* xrow[2 * P];
 #pragma unroll
-    for (int m = 0; m < 2 * P; ++m) {
-        pre0[m] = 1.0f;
-        pre1[m] = 0.0f;
-        if constexpr (PRO == GEMV_NORM_MHC) {
-            if (m < M) {
-                pre0[m] = a.coef[m * 8];
-                pre1[m] = a.coef[m * 8 + 1];
+    for (int m = 0; m < 2 * P; ++m)
+        xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
+    // mHC site sums: wave w adds sums w, w + 8, w + 16 (sum n = 9m + o) over the producer's blocks,
+    // lane l taking blocks l, l + 64, ... (partials are laid out [m][o][block])
+    float rsum[3] = {0.0f, 0.0f, 0.0f};
+    if constexpr (PRO == GEMV_NORM_MHC) {
+#pragma unroll
+        for (int pi = 0; pi < 3; ++pi) {
+            const int n = wave + kMaxWaves * pi;
+            if (n < 9 * M) {
+                const int m = n / 9, o = n - 9 * (n / 9);
+#pragma unroll 4
+                for (int b = lane; b < a.rin_n; b += 64) rsum[pi] = rsum[pi] + a.rin[(size_t)(m * 9 + o) * a.rin_n + b];
             }
         }
-        xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
     }
     float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2];
 #pragma unroll
@@ -205,10 +212,52 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             if constexpr (EPI == GEMV_MHC) e_y1 = yr[a.h + e_row];
         }
     }
+    // the site's token coefficients (MHC epilogue), left by the NORM_MHC launch of the same site
+    float cfv = 0.0f;
+    if constexpr (EPI == GEMV_MHC) {
+        if (tid < 8 * M) cfv = a.coef[tid];
+    }
+    // router rows of the next mHC site at this output's row, when this launch leaves its partials
+    float nr0[8], nr1[8];
+#pragma unroll
+    for (int o = 0; o < 8; ++o) nr0[o] = nr1[o] = 0.0f;
+    if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
+        if (a.rpart && e_row >= 0)
+#pragma unroll
+            for (int o = 0; o < 8; ++o) {
+                nr0[o] = a.next_w[(size_t)o * 2 * a.h + e_row];
+                nr1[o] = a.next_w[(size_t)o * 2 * a.h + a.h + e_row];
+            }
+    }
 
     // the first weight chunk (the next two follow the prologue, whose row registers they would
     // otherwise share the register file with)
     if (nch > 0) issue(w0, s0, 0);
+
+    float pre0[2 * P], pre1[2 * P];
+#pragma unroll
+    for (int m = 0; m < 2 * P; ++m) {
+        pre0[m] = 1.0f;
+        pre1[m] = 0.0f;
+    }
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        wave_sum_n(rsum);
+#pragma unroll
+        for (int pi = 0; pi < 3; ++pi) {
+            const int n = wave + kMaxWaves * pi;
+            if (lane == 0 && n < 9 * M) raw_s[n / 9][n - 9 * (n / 9)] = rsum[pi];
+        }
+        __syncthreads();
+        const int d = 2 * K;
+#pragma unroll
+        for (int m = 0; m < 2 * P; ++m) {
+            if (m >= M) continue;
+            const float rinv = 1.0f / sqrtf(raw_s[m][8] / (float)d + 1e-6f);
+            pre0[m] = 1.0f / (1.0f + __expf(-(raw_s[m][0] * rinv + a.site_w[(size_t)8 * d])));
+            pre1[m] = 1.0f / (1.0f + __expf(-(raw_s[m][1] * rinv + a.site_w[(size_t)8 * d + 1])));
+        }
+        if (blockIdx.x == 0 && tid < 9 * M) a.raw[tid] = raw_s[tid / 9][tid - 9 * (tid / 9)];
+    }
 
     // ---- prologue, part 2: branch input, per-token sums, f16 hi/lo in MFMA fragment order ----
     float ssq[2 * P], amax[2 * P];
@@ -249,11 +298,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             }
         }
     }
-#pragma unroll
-    for (int m = 0; m < 2 * P; ++m) {
-        ssq[m] = wave_sum(ssq[m]);
-        amax[m] = wave_max(amax[m]);
-    }
+    wave_sum_n(ssq);
+    wave_max_n(amax);
     if (lane == 0)
 #pragma unroll
         for (int m = 0; m < 2 * P; ++m) {
@@ -306,6 +352,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     if (nch > 1) issue(w1, s1, 1);
     if (nch > 2) issue(w2, s2, 2);
     __syncthreads();
+    if constexpr (EPI == GEMV_MHC) {
+        if (tid < 8 * M) cf_s[tid >> 3][tid & 7] = cfv;
+    }
 
     // ---- main loop ----
     // lane (j, g) feeds A row j = 4*slot + combo; it carries data only when slot == g
@@ -374,6 +423,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         }
     }
     __syncthreads();
+    float x0n = 0.0f, x1n = 0.0f;  // the new residual of this output's row (ADD / MHC)
     if (e_row >= 0) {
         const int t2 = e_r >> 4;
         float v = 0.0f;
@@ -387,18 +437,55 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             y[e_T * 8 + e_j] = v / (1.0f + expf(-v)) * u;
         } else if constexpr (EPI == GEMV_STORE) {
             y[a.n_off + e_row] = v;
-        } else if constexpr (EPI == GEMV_ADD) {
-            y[e_row] = e_y0 + v;
-        } else {  // GEMV_MHC, layers.wgsl:150-161
-            const float* cf = a.coef + e_m * 8;
+        } else if constexpr (EPI == GEMV_ADD) {  // merge mode 0, layers.wgsl:142-145
+            x0n = e_y0 + v;
+            x1n = x0n;
+            y[e_row] = x0n;
+            if (a.expand) y[a.h + e_row] = x0n;  // mode 3 of the next visit, layers.wgsl:146-149
+        } else {  // GEMV_MHC, modes 1 and 2, layers.wgsl:150-161
+            const float* cf = cf_s[e_m];
             const float n0 = (cf[4] * e_y0 + cf[5] * e_y1) + cf[2] * v;
             const float n1 = (cf[6] * e_y0 + cf[7] * e_y1) + cf[3] * v;
-            if (a.merge_mode == 2) {
-                y[e_row] = 0.5f * (n0 + n1);
-            } else {
-                y[e_row] = n0;
-                y[a.h + e_row] = n1;
+            x0n = a.merge_mode == 2 ? 0.5f * (n0 + n1) : n0;
+            x1n = a.merge_mode == 2 ? e_y1 : n1;  // mode 2 leaves stream 1 as it was
+            if (a.expand) x1n = x0n;
+            y[e_row] = x0n;
+            if (a.merge_mode != 2 || a.expand) y[a.h + e_row] = x1n;
+        }
+    }
+    if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
+        if (a.rpart) {
+            // partial router sums of the next site over this block's rows: the lanes of one token
+            // add 32-row groups in a butterfly (stride M), then the groups are added in order, so
+            // the association is the same for every M
+            float c[9];
+#pragma unroll
+            for (int o = 0; o < 8; ++o) c[o] = nr0[o] * x0n + nr1[o] * x1n;
+            c[8] = x0n * x0n + x1n * x1n;
+            for (int off = M; off < 32 * M; off <<= 1)
+#pragma unroll
+                for (int o = 0; o < 9; ++o) c[o] = c[o] + __shfl_xor(c[o], off, 64);
+            if (((tid / M) & 31) == 0 && tid < TW * 16 * M)
+#pragma unroll
+                for (int o = 0; o < 9; ++o) pr_s[(tid / M) >> 5][tid % M][o] = c[o];
+            __syncthreads();
+            if (tid < 9 * M) {
+                const int m = tid / 9, o = tid - 9 * (tid / 9);
+                const int groups = (TW * 16 + 31) / 32;
+                float t = 0.0f;
+                for (int gi = 0; gi < groups; ++gi) t = t + pr_s[gi][m][o];
+                a.rpart[(size_t)(m * 9 + o) * gridDim.x + blockIdx.x] = t;
             }
+        }
+    }
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        // block 0 turns the site sums into the token coefficients (2x2 Sinkhorn) for the MHC
+        // epilogue of the same site, after its own work
+        if (blockIdx.x == 0 && tid < M) {
+            float cf[8];
+            mhc_coefficients(raw_s[tid], a.site_w, 2 * K, a.iterations, cf);
+#pragma unroll
+            for (int o = 0; o < 8; ++o) a.coef[tid * 8 + o] = cf[o];
         }
     }
 }
@@ -502,6 +589,14 @@ void mgemv_shape(const PackGeom& g, int* KS, int* TW, int* nss_w) {
     *nss_w = g.nss / *KS;
 }
 
+int mgemv_blocks(int quant, int N, int K, int inter) {
+    PackGeom g;
+    if (!pack_geom(quant, N, K, inter, &g)) return 0;
+    int KS, TW, nss_w;
+    mgemv_shape(g, &KS, &TW, &nss_w);
+    return (g.tiles + TW - 1) / TW;
+}
+
 size_t mgemv_lds_bytes(int M, int K) { return (size_t)(M <= 2 ? 1 : 2) * (K / 32) * 256 + kZeroBytes; }
 
 bool mgemv_fits(int M, int K) {
@@ -522,6 +617,10 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
         (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_stride & 3))
         return -1;
+    if (a.pro == GEMV_NORM_MHC && (!a.site_w || !a.raw || !a.coef || !a.rin || a.rin_n < 1 || M > 2)) return -1;
+    if (a.epi == GEMV_MHC && !a.coef) return -1;
+    if (a.rpart && (!a.next_w || (a.epi != GEMV_ADD && a.epi != GEMV_MHC) || (M & (M - 1)))) return -1;
+    if (a.epi == GEMV_ADD && a.rpart && !a.expand) return -1;  // an ADD producer starts the mHC range
     KernelFn f = pick(quant, g.U, upt_for(a.K), P, a.epi, a.pro);
     if (!f) return 1;
     dim3 grid((g.tiles + TW - 1) / TW);
