@@ -95,6 +95,19 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) valid[m] = min(nkeys, pos0 + m + 1 - kstart);
 
+    // the part's values do not depend on the scores: their loads go out first
+    const int dp = tid & 127, kh2 = tid >> 7;
+    constexpr int KH = kPart / 2;
+    uint32_t vw[KH];
+    {
+        const uint32_t* vb = reinterpret_cast<const uint32_t*>(a.vcache + (size_t)kh * HD) + dp;
+#pragma unroll
+        for (int i = 0; i < KH; ++i) {
+            const int t = kh2 * KH + i;
+            vw[i] = t < nkeys ? vb[(size_t)(kstart + t) * (kv_dim / 2)] : 0u;
+        }
+    }
+
     // ---- scores ----
     float q[NC][16];
 #pragma unroll
@@ -179,19 +192,10 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- values: thread (dim pair dp, key half kh2) ----
-    const int dp = tid & 127, kh2 = tid >> 7;
+    // ---- values: thread (dim pair dp, key half kh2), loaded with the keys above ----
     float2 acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = make_float2(0.0f, 0.0f);
-    const uint32_t* vb = reinterpret_cast<const uint32_t*>(a.vcache + (size_t)kh * HD) + dp;
-    constexpr int KH = kPart / 2;
-    uint32_t vw[KH];
-#pragma unroll
-    for (int i = 0; i < KH; ++i) {
-        const int t = kh2 * KH + i;
-        vw[i] = t < nkeys ? vb[(size_t)(kstart + t) * (kv_dim / 2)] : 0u;
-    }
 #pragma unroll
     for (int i = 0; i < KH; ++i) {
         const int t = kh2 * KH + i;
@@ -225,30 +229,54 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     }
 }
 
-// attention.wgsl:248-269: merge the token's parts in order, then the sigmoid gate.
-__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
-    const int h = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+// attention.wgsl:248-269: merge the token's parts, then the sigmoid gate.  Block (head, token) of
+// 1024 threads: every part's scale e^(max_p - max) goes to LDS once, then thread (d, q) adds the
+// parts q, q+4, ... of dim d and the four groups are added in order.
+constexpr int kCombThreads = 1024, kMaxParts = 1024;
+
+__global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
+    __shared__ float fs[kMaxParts];
+    __shared__ float red[kCombThreads / 64];
+    __shared__ float accq[4][HD];
+    const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+    const int d = tid & (HD - 1), q = tid >> 8;
     const int total = a.step->pos0 + m + 1;
     const int np = (total + kPart - 1) / kPart;
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     const float* base = a.partial + ((size_t)m * a.n_heads + h) * parts_max * (HD + 2);
-    float mx = -1e30f;
-    for (int p = 0; p < np; ++p) mx = fmaxf(mx, base[(size_t)p * (HD + 2) + HD]);
-    float l = 0.0f, acc = 0.0f;
-    for (int p = 0; p < np; ++p) {
-        const float* o = base + (size_t)p * (HD + 2);
-        const float f = expf(o[HD] - mx);
-        l = l + o[HD + 1] * f;
-        acc = acc + o[d] * f;
-    }
     const float gate = a.proj[(size_t)m * a.proj_stride + h * 2 * HD + HD + d];
-    a.out[(size_t)m * a.n_heads * HD + h * HD + d] = acc / l / (1.0f + expf(-gate));
+    // global max of the part maxima
+    float mp = -1e30f, lp = 0.0f;
+    if (tid < np) {
+        mp = base[(size_t)tid * (HD + 2) + HD];
+        lp = base[(size_t)tid * (HD + 2) + HD + 1];
+    }
+    float mx = wave_max(mp);
+    if ((tid & 63) == 0) red[tid >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < kCombThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+    __syncthreads();
+    const float f = tid < np ? expf(mp - mx) : 0.0f;
+    if (tid < np) fs[tid] = f;
+    const float l = block_sum<kCombThreads>(lp * f, red);  // the sum of the parts' weights
+    float acc = 0.0f;
+#pragma unroll 8
+    for (int p = q; p < np; p += 4) acc = acc + base[(size_t)p * (HD + 2) + d] * fs[p];
+    accq[q][d] = acc;
+    __syncthreads();
+    if (q == 0) {
+        const float v = ((accq[0][d] + accq[1][d]) + accq[2][d]) + accq[3][d];
+        a.out[(size_t)m * a.n_heads * HD + h * HD + d] = v / l / (1.0f + expf(-gate));
+    }
 }
 
 }  // namespace
 
 int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
     if (M < 1 || M > 2 || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2) return -1;
+    if ((a.ctx + kPart - 1) / kPart > kMaxParts) return -1;
     hipLaunchKernelGGL(prep_kernel, dim3(a.n_heads + 2 * a.n_kv, M), dim3(256), 0, s, a);
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     dim3 grid(a.n_kv, parts_max);
@@ -257,7 +285,7 @@ int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
         case 2: hipLaunchKernelGGL(attend_kernel<2>, grid, dim3(256), 0, s, a); break;
         default: return -1;
     }
-    hipLaunchKernelGGL(combine_kernel, dim3(a.n_heads, M), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(combine_kernel, dim3(a.n_heads, M), dim3(kCombThreads), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -22,42 +22,78 @@ namespace snl {
 namespace {
 
 constexpr int DK = 128, DV = 128, kThreads = 512, kRowsPer = DK / (kThreads / DV);
+constexpr int kWaves = kThreads / 64;
 
+// Critical path per token: two barriers (the column sums of S^T k and S^T q).  Everything that
+// does not depend on the recurrence -- conv, q/k norms, beta and decay, the gate z -- is loaded
+// and computed before the token loop, and the gated RMS norm of all tokens runs after it.
 template <int M>
 __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     __shared__ float cq[M][DK], ck[M][DK], cv[M][DV];  // conv outputs (SiLU applied)
-    __shared__ float qs[DK], ks[DK];
-    __shared__ float part[4][DV];
-    __shared__ float red[16];
+    __shared__ float kvp[2][4][DV], op[2][4][DV];       // column partials, double-buffered by token
+    __shared__ float ob[M][DV];                          // head outputs before the gated norm
+    __shared__ float red[kWaves][2 * M];
 
     const StepDev* st = a.step;
     const int s_in = st->s_in, s_out = st->s_out, s_ck = st->s_ck, ckpt = st->ckpt;
-    const int h = blockIdx.x, tid = threadIdx.x;
+    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = tid & (DV - 1), g = tid >> 7;
     const int group = a.n_v / a.n_k, kh = h / group;
     const int key_dim = a.n_k * DK, cd = a.conv_dim;
+    const int z_off = cd, b_off = cd + a.n_v * DV, a_off = b_off + a.n_v;
 
-    // ---- causal conv (linear.wgsl:38-66) of this head's channels ----
+    // ---- every load up front: conv inputs, recurrent state, gate, per-token scalars ----
+    const int which = tid >> 7, c0 = tid & 127;  // conv lanes: tid < 384
+    const int ch = which == 0 ? kh * DK + c0 : which == 1 ? key_dim + kh * DK + c0 : 2 * key_dim + h * DV + c0;
+    float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, r0 = 0.0f, r1 = 0.0f, r2 = 0.0f, cur[M];
     if (tid < 3 * DK) {
-        const int which = tid >> 7, c0 = tid & 127;
-        const int ch = which == 0 ? kh * DK + c0 : which == 1 ? key_dim + kh * DK + c0 : 2 * key_dim + h * DV + c0;
-        const float* lw = a.lw + (size_t)ch * 4;
-        const float w0 = lw[0], w1 = lw[1], w2 = lw[2], w3 = lw[3];
+        const float4 w = *reinterpret_cast<const float4*>(a.lw + (size_t)ch * 4);
+        w4[0] = w.x, w4[1] = w.y, w4[2] = w.z, w4[3] = w.w;
         const float* cs = a.conv_state + (size_t)s_in * a.conv_slot;
-        float r0 = cs[ch], r1 = cs[cd + ch], r2 = cs[2 * cd + ch];
+        r0 = cs[ch];
+        r1 = cs[cd + ch];
+        r2 = cs[2 * cd + ch];
+#pragma unroll
+        for (int m = 0; m < M; ++m) cur[m] = a.proj[(size_t)m * a.proj_stride + ch];
+    }
+    const size_t hoff = (size_t)h * DK * DV;
+    const float* S0 = a.state + (size_t)s_in * a.state_slot + hoff;
+    float s[kRowsPer];
+#pragma unroll
+    for (int r = 0; r < kRowsPer; ++r) s[r] = S0[(size_t)(g * kRowsPer + r) * DV + j];
+    float z[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) z[m] = g == 0 ? a.proj[(size_t)m * a.proj_stride + z_off + h * DV + j] : 0.0f;
+    const float* lwp = a.lw + (size_t)cd * 4;
+    const float a_log = lwp[h], dt_bias = lwp[a.n_v + h], norm_w = lwp[2 * a.n_v + j];
+    float beta[M], decay[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {  // linear.wgsl:113-117
+        const float* prow = a.proj + (size_t)m * a.proj_stride;
+        beta[m] = 1.0f / (1.0f + expf(-prow[b_off + h]));
+        const float araw = prow[a_off + h] + dt_bias;
+        const float sp = araw <= 20.0f ? logf(1.0f + expf(araw)) : araw;
+        decay[m] = expf(-expf(a_log) * sp);
+    }
+
+    // ---- causal conv (linear.wgsl:38-66) of this head's channels, and the q/k sums of squares ----
+    float sq[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) sq[m] = 0.0f;
+    if (tid < 3 * DK) {
         // k-head channels are shared by `group` v-heads: the first one owns their state
         const bool owner = which == 2 || (h % group) == 0;
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const float cur = a.proj[(size_t)m * a.proj_stride + ch];
-            const float o = ((w0 * r0 + w1 * r1) + w2 * r2) + w3 * cur;
+            const float o = ((w4[0] * r0 + w4[1] * r1) + w4[2] * r2) + w4[3] * cur[m];
             const float v = o / (1.0f + expf(-o));
             if (which == 0) cq[m][c0] = v;
             else if (which == 1) ck[m][c0] = v;
             else cv[m][c0] = v;
+            if (which < 2) sq[m] = v * v;
             r0 = r1;
             r1 = r2;
-            r2 = cur;
+            r2 = cur[m];
             if (m + 1 == ckpt && owner) {
                 float* cc = a.conv_state + (size_t)s_ck * a.conv_slot;
                 cc[ch] = r0;
@@ -72,79 +108,70 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
             co[2 * cd + ch] = r2;
         }
     }
-
-    // ---- state columns into registers ----
-    const size_t hoff = (size_t)h * DK * DV;
-    const float* S0 = a.state + (size_t)s_in * a.state_slot + hoff;
-    float s[kRowsPer];
+    // waves 0-1 hold the q channels, waves 2-3 the k channels (linear.wgsl:104-110)
+    wave_sum_n(sq);
+    if (lane == 0 && wave < 4)
 #pragma unroll
-    for (int r = 0; r < kRowsPer; ++r) s[r] = S0[(size_t)(g * kRowsPer + r) * DV + j];
-
-    const float* lwp = a.lw + (size_t)cd * 4;
-    const float a_log = lwp[h], dt_bias = lwp[a.n_v + h], norm_w = lwp[2 * a.n_v + j];
-    const int z_off = cd, b_off = cd + a.n_v * DV, a_off = b_off + a.n_v;
+        for (int m = 0; m < M; ++m) red[wave][m] = sq[m];
     __syncthreads();
-
+    float qscale[M], kscale[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        // L2 norms of q and k (linear.wgsl:104-110)
-        float q2 = 0.0f, k2 = 0.0f;
-        if (tid < DK) {
-            q2 = cq[m][tid] * cq[m][tid];
-            k2 = ck[m][tid] * ck[m][tid];
-        }
-        const float sq = block_sum<kThreads>(q2, red);
-        const float sk = block_sum<kThreads>(k2, red + 8);
-        if (tid < DK) {
-            qs[tid] = (cq[m][tid] * (1.0f / sqrtf(sq + 1e-6f))) * (1.0f / sqrtf((float)DK));
-            ks[tid] = ck[m][tid] * (1.0f / sqrtf(sk + 1e-6f));
-        }
-        const float* prow = a.proj + (size_t)m * a.proj_stride;
-        const float beta = 1.0f / (1.0f + expf(-prow[b_off + h]));
-        const float araw = prow[a_off + h] + dt_bias;
-        const float sp = araw <= 20.0f ? logf(1.0f + expf(araw)) : araw;
-        const float decay = expf(-expf(a_log) * sp);
-        __syncthreads();
+        qscale[m] = (1.0f / sqrtf((red[0][m] + red[1][m]) + 1e-6f)) * (1.0f / sqrtf((float)DK));
+        kscale[m] = 1.0f / sqrtf((red[2][m] + red[3][m]) + 1e-6f);
+    }
 
+    // ---- the recurrence, token by token (linear.wgsl:118-136) ----
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const int b = m & 1;
         // kv_mem_j = sum_i decay*S[i][j] * k_i
         float kv = 0.0f;
 #pragma unroll
         for (int r = 0; r < kRowsPer; ++r) {
-            s[r] = s[r] * decay;
-            kv = fmaf(s[r], ks[g * kRowsPer + r], kv);
+            s[r] = s[r] * decay[m];
+            kv = fmaf(s[r], ck[m][g * kRowsPer + r] * kscale[m], kv);
         }
-        part[g][j] = kv;
+        kvp[b][g][j] = kv;
         __syncthreads();
-        const float kv_mem = ((part[0][j] + part[1][j]) + part[2][j]) + part[3][j];
-        const float dlt = (cv[m][j] - kv_mem) * beta;
+        const float kv_mem = ((kvp[b][0][j] + kvp[b][1][j]) + kvp[b][2][j]) + kvp[b][3][j];
+        const float dlt = (cv[m][j] - kv_mem) * beta[m];
         float o = 0.0f;
 #pragma unroll
         for (int r = 0; r < kRowsPer; ++r) {
-            s[r] = fmaf(ks[g * kRowsPer + r], dlt, s[r]);
-            o = fmaf(s[r], qs[g * kRowsPer + r], o);
+            s[r] = fmaf(ck[m][g * kRowsPer + r] * kscale[m], dlt, s[r]);
+            o = fmaf(s[r], cq[m][g * kRowsPer + r] * qscale[m], o);
         }
+        op[b][g][j] = o;
         __syncthreads();
-        part[g][j] = o;
-        __syncthreads();
-        const float oj = ((part[0][j] + part[1][j]) + part[2][j]) + part[3][j];
-        // gated RMS norm over the head's 128 outputs (linear.wgsl:131-133), plain w
-        const float ss = block_sum<kThreads>(g == 0 ? oj * oj : 0.0f, red);
-        if (g == 0) {
-            const float z = prow[z_off + h * DV + j];
-            const float var_o = ss / (float)DV;
-            a.out[(size_t)m * a.n_v * DV + h * DV + j] =
-                ((oj * (1.0f / sqrtf(var_o + a.eps))) * norm_w) * (z / (1.0f + expf(-z)));
-        }
+        if (g == 0) ob[m][j] = ((op[b][0][j] + op[b][1][j]) + op[b][2][j]) + op[b][3][j];
         if (m + 1 == ckpt) {
             float* SC = a.state + (size_t)s_ck * a.state_slot + hoff;
 #pragma unroll
             for (int r = 0; r < kRowsPer; ++r) SC[(size_t)(g * kRowsPer + r) * DV + j] = s[r];
         }
-        __syncthreads();
     }
     float* SO = a.state + (size_t)s_out * a.state_slot + hoff;
 #pragma unroll
     for (int r = 0; r < kRowsPer; ++r) SO[(size_t)(g * kRowsPer + r) * DV + j] = s[r];
+
+    // ---- gated RMS norm over the head's 128 outputs (linear.wgsl:131-133), plain w ----
+    float ss[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) ss[m] = g == 0 ? ob[m][j] * ob[m][j] : 0.0f;
+    wave_sum_n(ss);
+    if (lane == 0 && wave < 2)
+#pragma unroll
+        for (int m = 0; m < M; ++m) red[wave][M + m] = ss[m];
+    __syncthreads();
+    if (g == 0)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float var_o = (red[0][M + m] + red[1][M + m]) / (float)DV;
+            const float oj = ob[m][j];
+            a.out[(size_t)m * a.n_v * DV + h * DV + j] =
+                ((oj * (1.0f / sqrtf(var_o + a.eps))) * norm_w) * (z[m] / (1.0f + expf(-z[m])));
+        }
 }
 
 }  // namespace
