@@ -26,8 +26,13 @@
 //
 // Work split.  A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows).  A
 // superstep is 128*U elements of a row (U = 4 when K % 512 == 0, else 1), 8 KiB of a Q8 tile;
-// K is cut into KS equal slices of supersteps.  A block of 8 = KS*TW waves owns TW tiles and every
-// wave one (tile, slice) item; KS and TW are chosen from the matrix shape alone, never from M.
+// K is cut into KS equal slices of supersteps.  Up to 4096 tiles, the grid is one block per CU
+// (at most 256 blocks, one resident per CU): block b owns the consecutive tiles
+// [b*base + min(b, extra), +base + (b < extra)), and its wave w the item (tile w / KS, slice
+// w % KS), so every active wave streams the same bytes and every CU the same number of waves'
+// worth (a block with one tile fewer leaves KS waves idle).  Taller matrices (the vocabulary
+// head) run many short blocks of 4 slices x 2 tiles.  The split depends on the matrix shape
+// alone, never on M.
 // Weights stream through a three-chunk register ring (half supersteps), two chunks ahead of the
 // MFMAs, and the token rows are loaded before the first weight chunk.  Slices are added in slice order through LDS, so a token's
 // result does not depend on M, on its index or on timing (greedy output is then byte-identical
@@ -45,6 +50,12 @@
 
 #pragma clang fp contract(off)
 
+// two f32 through the raw buffer load intrinsic (clang's __builtin_amdgcn_raw_buffer_load_b64
+// lowers to a single dword load here)
+typedef float snl_f32x2_t __attribute__((ext_vector_type(2)));
+__device__ snl_f32x2_t snl_raw_buffer_load_f32x2(__amdgpu_buffer_rsrc_t rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.ptr.buffer.load.v2f32");
+
 namespace snl {
 
 namespace {
@@ -53,7 +64,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kMaxWaves = 8;
+constexpr int kMaxWaves = 16;
 constexpr int kCUs = 256;                 // MI355X compute units
 constexpr int kLdsLimit = 150 * 1024;     // dynamic LDS per block
 constexpr int kZeroBytes = 64;            // zero A fragment read by the lanes outside their slot
@@ -71,6 +82,25 @@ __device__ __forceinline__ int tile_row(const GemvArgs& a, int T, int j) {
 }
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+
+// Raw buffer descriptor over [base, base + bytes): a load at or past `bytes` returns zeros and
+// touches no memory, so a wave can issue its weight ring unconditionally past the end of its
+// slice.  Word 3 is the gfx9 raw (untyped) dword format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Block barrier that orders LDS only: this wave's LDS operations complete before the barrier and
+// vector memory loads stay in flight across it (a full __syncthreads also waits for every
+// outstanding global load, which would drain the weight ring).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 // 8 weights of one 16-byte load as exact f16: MFMA i (0..NM-1) of the load.
 // Q8 order: elements 8i..8i+7.  Q4 order (word i): elements 8i + {0, 4, 1, 5, 2, 6, 3, 7}.
@@ -106,8 +136,8 @@ __device__ __forceinline__ int a_pos(int e) {
 // QT: 0 Q8_0, 1 Q4_0.  P: token pairs (M <= 2P).  U: quant blocks per lane group per superstep.
 // UPT: 8-element units of each token row per thread (K <= 8 * UPT * 512).
 template <int QT, int P, int EPI, int PRO, int U, int UPT>
-__global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int TW, int nss_w,
-                                                               int tiles) {
+__global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int base, int extra,
+                                                               int nss_w, int tiles) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
     __shared__ float wred_s[kMaxWaves][2 * P][2];
@@ -118,37 +148,49 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
     constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
     const int K = a.K, nb = K >> 5, K4 = K >> 2;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nthr = KS * TW * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nthr = blockDim.x, nwv = nthr >> 6;
+    const int bi = blockIdx.x;
+    const int tile0 = bi * base + (bi < extra ? bi : extra);                 // first tile of the block
+    const int cnt = min(base + (bi < extra ? 1 : 0), tiles - tile0);        // its tiles
     const int tw = wave / KS, ks = wave - tw * KS;
-    const int T = blockIdx.x * TW + tw;
-    const int Tl = T < tiles ? T : tiles - 1;  // a block's spare waves read the last tile, unused
+    const bool active = tw < cnt;  // waves past the block's tiles only stage rows and reduce
+    const int Tl = tile0 + (active ? tw : 0);
     const int j = lane & 15, g = lane >> 4;
     const int nss = nss_w * KS;
-    // tile order (packing.h): load v of superstep S of tile T is 1 KiB at ((T*nss + S)*NI + v) KiB
-    const uint8_t* wp = static_cast<const uint8_t*>(a.wq) + ((size_t)Tl * nss + ks * nss_w) * NI * 1024 + lane * 16;
-    const float* sp = a.ws + (((size_t)Tl * nss + ks * nss_w) * 64 + lane) * U;
-
     // Weights stream through a ring of three chunks of CL loads (half a superstep when U == 4):
     // chunk q of the slice is loads [q*CL, q*CL + CL) counted from the slice start, with the
-    // CS = U*CL/NI scales of its quant blocks.
+    // CS = U*CL/NI scales of its quant blocks.  Tile order (packing.h): load v of superstep S of
+    // tile T is 1 KiB at ((T*nss + S)*NI + v) KiB; the scales of superstep S are [S][lane][U].
+    // Every issue is unconditional (a chunk past the slice reads zeros without a memory access),
+    // so the loads keep one fixed order and each wait names exactly the chunk it needs.
     constexpr int CL = U == 4 ? NI / 2 : NI;  // loads per chunk
     constexpr int CPS = NI / CL;              // chunks per superstep
     constexpr int CS = U / CPS;               // scales per chunk
     uint4 w0[CL], w1[CL], w2[CL];
     float s0[CS], s1[CS], s2[CS];
     const int nch = nss_w * CPS;
+    const size_t slice = (size_t)Tl * nss + ks * nss_w;  // first superstep of this wave's slice
+    const __amdgpu_buffer_rsrc_t wr =
+        make_rsrc(static_cast<const uint8_t*>(a.wq) + slice * NI * 1024, active ? (unsigned)nch * CL * 1024 : 0u);
+    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.ws + slice * 64 * U, active ? (unsigned)nss_w * 64 * U * 4 : 0u);
+    const int wv = lane * 16, sv = lane * U * 4;
+    // The scales first, then the quants; the scheduling barrier keeps chunks in issue order.  The
+    // whole offset goes in the per-lane operand: the range check covers that operand and the
+    // instruction offset, not the scalar one.
     auto issue = [&](uint4 (&w)[CL], float (&sc)[CS], int q) {
-        const uint8_t* p = wp + (size_t)q * CL * 1024;
-#pragma unroll
-        for (int v = 0; v < CL; ++v) w[v] = *reinterpret_cast<const uint4*>(p + 1024 * v);
-        const float* ps = sp + (size_t)(q / CPS) * 64 * U + (q % CPS) * CS;
+        const int so = sv + ((q / CPS) * 64 * U + (q % CPS) * CS) * 4;
         if constexpr (CS == 2) {
-            const float2 t = *reinterpret_cast<const float2*>(ps);
+            const snl_f32x2_t t = snl_raw_buffer_load_f32x2(sr, so, 0, 0);
             sc[0] = t.x, sc[1] = t.y;
         } else {
-            sc[0] = ps[0];
+            sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 0));
         }
+        const int wo = wv + q * CL * 1024;
+#pragma unroll
+        for (int v = 0; v < CL; ++v)
+            w[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo + v * 1024, 0, 0));
+        __builtin_amdgcn_sched_barrier(0);
     };
     // ---- prologue, part 1: every load of the token rows comes before the first weight load ----
     // Vector loads complete in issue order, so a row load issued after the weights would wait for
@@ -161,18 +203,27 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     for (int m = 0; m < 2 * P; ++m)
         xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
     // mHC site sums: wave w adds sums w, w + 8, w + 16 (sum n = 9m + o) over the producer's blocks,
-    // lane l taking blocks l, l + 64, ... (partials are laid out [m][o][block])
-    float rsum[3] = {0.0f, 0.0f, 0.0f};
+    // lane l taking blocks l, l + 64, ... in order (partials are laid out [m][o][block]).  The
+    // first kRinBatch per lane are loaded here, in one batch; more producer blocks than
+    // 64 * kRinBatch are added later by a loop.
+    constexpr int kRinBatch = 4;
+    float rv[3][kRinBatch];
+    float sw0 = 0.0f, sw1 = 0.0f;
     if constexpr (PRO == GEMV_NORM_MHC) {
+        // buffer loads: a block past the producer's count, or a sum this launch does not have,
+        // reads zero, so the batch has no branches and no waits
 #pragma unroll
         for (int pi = 0; pi < 3; ++pi) {
-            const int n = wave + kMaxWaves * pi;
-            if (n < 9 * M) {
-                const int m = n / 9, o = n - 9 * (n / 9);
-#pragma unroll 4
-                for (int b = lane; b < a.rin_n; b += 64) rsum[pi] = rsum[pi] + a.rin[(size_t)(m * 9 + o) * a.rin_n + b];
-            }
+            const int n = wave + nwv * pi;
+            const bool on = n < 9 * M;
+            const __amdgpu_buffer_rsrc_t rr =
+                make_rsrc(a.rin + (size_t)(on ? n : 0) * a.rin_n, on ? (unsigned)a.rin_n * 4 : 0u);
+#pragma unroll
+            for (int r = 0; r < kRinBatch; ++r)
+                rv[pi][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (lane + 64 * r) * 4, 0, 0));
         }
+        sw0 = a.site_w[(size_t)16 * K];
+        sw1 = a.site_w[(size_t)16 * K + 1];
     }
     float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2];
 #pragma unroll
@@ -199,11 +250,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         }
     }
 
-    // Thread tid owns output tid of the block (TW*16*M <= 64*TW outputs, fewer than the threads);
-    // the residual it will update is read now, also ahead of the weights.
+    // Thread tid owns output tid of the block (cnt*16*M <= 64*KS*cnt outputs, fewer than the
+    // threads); the residual it will update is read now, also ahead of the weights.
     const int e_m = tid % M, e_r = tid / M;
-    const int e_T = blockIdx.x * TW + (e_r >> 4), e_j = e_r & 15;
-    const int e_row = tid < TW * 16 * M && !(EPI == GEMV_SWIGLU && e_j >= 8) ? tile_row<EPI>(a, e_T, e_j) : -1;
+    const int e_T = tile0 + (e_r >> 4), e_j = e_r & 15;
+    const int e_row = tid < cnt * 16 * M && !(EPI == GEMV_SWIGLU && e_j >= 8) ? tile_row<EPI>(a, e_T, e_j) : -1;
     float e_y0 = 0.0f, e_y1 = 0.0f;
     if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
         if (e_row >= 0) {
@@ -230,9 +281,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             }
     }
 
-    // the first weight chunk (the next two follow the prologue, whose row registers they would
-    // otherwise share the register file with)
-    if (nch > 0) issue(w0, s0, 0);
+    // Every wave of the block has issued its row loads before any wave issues weights, so the rows
+    // are not queued behind the block's weight stream.  Only the first chunk of the ring goes out
+    // before the rows are staged: a CU holds a bounded number of vector memory instructions in
+    // flight, and a wave that issued its whole ring here would stall at issue, behind its own
+    // weights, before it could stage the rows that had already arrived.
+    __builtin_amdgcn_s_barrier();
+    issue(w0, s0, 0);
 
     float pre0[2 * P], pre1[2 * P];
 #pragma unroll
@@ -241,20 +296,33 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         pre1[m] = 0.0f;
     }
     if constexpr (PRO == GEMV_NORM_MHC) {
+        float rsum[3];
+#pragma unroll
+        for (int pi = 0; pi < 3; ++pi) {
+            float t = 0.0f;
+#pragma unroll
+            for (int r = 0; r < kRinBatch; ++r) t = t + rv[pi][r];
+            const int n = wave + nwv * pi;
+            if (n < 9 * M && a.rin_n > 64 * kRinBatch) {
+                const int m = n / 9, o = n - 9 * (n / 9);
+                for (int b = lane + 64 * kRinBatch; b < a.rin_n; b += 64) t = t + a.rin[(size_t)(m * 9 + o) * a.rin_n + b];
+            }
+            rsum[pi] = t;
+        }
         wave_sum_n(rsum);
 #pragma unroll
         for (int pi = 0; pi < 3; ++pi) {
-            const int n = wave + kMaxWaves * pi;
+            const int n = wave + nwv * pi;
             if (lane == 0 && n < 9 * M) raw_s[n / 9][n - 9 * (n / 9)] = rsum[pi];
         }
-        __syncthreads();
+        lds_barrier();
         const int d = 2 * K;
 #pragma unroll
         for (int m = 0; m < 2 * P; ++m) {
             if (m >= M) continue;
             const float rinv = 1.0f / sqrtf(raw_s[m][8] / (float)d + 1e-6f);
-            pre0[m] = 1.0f / (1.0f + __expf(-(raw_s[m][0] * rinv + a.site_w[(size_t)8 * d])));
-            pre1[m] = 1.0f / (1.0f + __expf(-(raw_s[m][1] * rinv + a.site_w[(size_t)8 * d + 1])));
+            pre0[m] = 1.0f / (1.0f + __expf(-(raw_s[m][0] * rinv + sw0)));
+            pre1[m] = 1.0f / (1.0f + __expf(-(raw_s[m][1] * rinv + sw1)));
         }
         if (blockIdx.x == 0 && tid < 9 * M) a.raw[tid] = raw_s[tid / 9][tid - 9 * (tid / 9)];
     }
@@ -308,11 +376,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         }
     if (tid < kZeroBytes / 16)
         reinterpret_cast<float4*>(lds + (size_t)P * nb * 256)[tid] = make_float4(0, 0, 0, 0);
-    __syncthreads();
+    lds_barrier();
     if (tid < 2 * P) {
         const int m = tid;
         float ss = 0.0f, mx = 0.0f;
-        for (int w = 0; w < KS * TW; ++w) {
+        for (int w = 0; w < nwv; ++w) {
             ss = ss + wred_s[w][m][0];
             mx = fmaxf(mx, wred_s[w][m][1]);
         }
@@ -323,7 +391,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         tok_s[m][0] = m < M ? ldexpf(rinv, -e) : 0.0f;
         tok_s[m][1] = ldexpf(1.0f, e);
     }
-    __syncthreads();
+    lds_barrier();
     // unit k8 of token m -> 8 hi then 8 lo f16 in fragment order inside region (pair, block, token)
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
@@ -349,9 +417,20 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             *reinterpret_cast<half8_t*>(base + 64) = lo;
         }
     }
-    if (nch > 1) issue(w1, s1, 1);
-    if (nch > 2) issue(w2, s2, 2);
-    __syncthreads();
+    // the next site's router rows wait in LDS (after the staged rows and the zero fragment) until
+    // the epilogue, instead of holding 16 registers through the main loop
+    if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
+        if (a.rpart && e_row >= 0) {
+            float4* st = reinterpret_cast<float4*>(lds + (size_t)P * nb * 256 + kZeroBytes) + tid * 4;
+            st[0] = make_float4(nr0[0], nr0[1], nr0[2], nr0[3]);
+            st[1] = make_float4(nr0[4], nr0[5], nr0[6], nr0[7]);
+            st[2] = make_float4(nr1[0], nr1[1], nr1[2], nr1[3]);
+            st[3] = make_float4(nr1[4], nr1[5], nr1[6], nr1[7]);
+        }
+    }
+    issue(w1, s1, 1);
+    issue(w2, s2, 2);
+    lds_barrier();
     if constexpr (EPI == GEMV_MHC) {
         if (tid < 8 * M) cf_s[tid >> 3][tid & 7] = cfv;
     }
@@ -396,18 +475,26 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         }
     };
 
-    for (int q = 0; q < nch; q += 3) {
+    // Steady state: compute a chunk, issue the one three ahead.  The last five chunks or fewer run
+    // as a straight-line tail that issues nothing past the slice.
+    const int nrun = active ? nch : 0;
+    int q = 0;
+    for (; q + 5 < nrun; q += 3) {
         compute(w0, s0, q);
-        if (q + 3 < nch) issue(w0, s0, q + 3);
-        if (q + 1 < nch) {
-            compute(w1, s1, q + 1);
-            if (q + 4 < nch) issue(w1, s1, q + 4);
-        }
-        if (q + 2 < nch) {
-            compute(w2, s2, q + 2);
-            if (q + 5 < nch) issue(w2, s2, q + 5);
-        }
+        issue(w0, s0, q + 3);
+        compute(w1, s1, q + 1);
+        issue(w1, s1, q + 4);
+        compute(w2, s2, q + 2);
+        issue(w2, s2, q + 5);
     }
+    const int rem = nrun - q;  // 0 (idle wave) .. 5
+    if (rem >= 1) compute(w0, s0, q);
+    if (rem >= 4) issue(w0, s0, q + 3);
+    if (rem >= 2) compute(w1, s1, q + 1);
+    if (rem >= 5) issue(w1, s1, q + 4);
+    if (rem >= 3) compute(w2, s2, q + 2);
+    if (rem >= 4) compute(w0, s0, q + 3);
+    if (rem >= 5) compute(w1, s1, q + 4);
 
     // ---- reduction: hi + lo, then the 4 lane groups, then the K slices in order ----
 #pragma unroll
@@ -459,19 +546,28 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             // add 32-row groups in a butterfly (stride M), then the groups are added in order, so
             // the association is the same for every M
             float c[9];
+            if (e_row >= 0) {
+                const float4* st = reinterpret_cast<const float4*>(lds + (size_t)P * nb * 256 + kZeroBytes) + tid * 4;
+                const float4 q0 = st[0], q1 = st[1], q2 = st[2], q3 = st[3];
+                const float r0[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+                const float r1[8] = {q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
 #pragma unroll
-            for (int o = 0; o < 8; ++o) c[o] = nr0[o] * x0n + nr1[o] * x1n;
+                for (int o = 0; o < 8; ++o) c[o] = r0[o] * x0n + r1[o] * x1n;
+            } else {
+#pragma unroll
+                for (int o = 0; o < 8; ++o) c[o] = 0.0f;
+            }
             c[8] = x0n * x0n + x1n * x1n;
             for (int off = M; off < 32 * M; off <<= 1)
 #pragma unroll
                 for (int o = 0; o < 9; ++o) c[o] = c[o] + __shfl_xor(c[o], off, 64);
-            if (((tid / M) & 31) == 0 && tid < TW * 16 * M)
+            if (((tid / M) & 31) == 0 && tid < cnt * 16 * M)
 #pragma unroll
                 for (int o = 0; o < 9; ++o) pr_s[(tid / M) >> 5][tid % M][o] = c[o];
             __syncthreads();
             if (tid < 9 * M) {
                 const int m = tid / 9, o = tid - 9 * (tid / 9);
-                const int groups = (TW * 16 + 31) / 32;
+                const int groups = (cnt * 16 + 31) / 32;
                 float t = 0.0f;
                 for (int gi = 0; gi < groups; ++gi) t = t + pr_s[gi][m][o];
                 a.rpart[(size_t)(m * 9 + o) * gridDim.x + blockIdx.x] = t;
@@ -490,7 +586,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     }
 }
 
-using KernelFn = void (*)(GemvArgs, int, int, int, int, int);
+using KernelFn = void (*)(GemvArgs, int, int, int, int, int, int);
 
 template <int QT, int U, int UPT>
 KernelFn pick_fn(int P, int epi, int pro) {
@@ -499,13 +595,16 @@ KernelFn pick_fn(int P, int epi, int pro) {
     if (P == 1) {
         SNL_G(GEMV_STORE, GEMV_PLAIN)
         SNL_G(GEMV_STORE, GEMV_NORM)
-        SNL_G(GEMV_STORE, GEMV_NORM_MHC)
         SNL_G(GEMV_ADD, GEMV_PLAIN)
         SNL_G(GEMV_ADD, GEMV_NORM)
         SNL_G(GEMV_MHC, GEMV_PLAIN)
         SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
         SNL_G(GEMV_SWIGLU, GEMV_NORM)
-        SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
+        // the mHC pre-mix reads two residual streams of the hidden size: K <= 8192 (one unit per thread)
+        if constexpr (UPT == 1) {
+            SNL_G(GEMV_STORE, GEMV_NORM_MHC)
+            SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
+        }
     }
 #undef SNL_G
     // two token pairs: the plain product at K <= 4096 only (kernel-level calls with M = 3, 4)
@@ -525,9 +624,6 @@ KernelFn pick(int quant, int U, int UPT, int P, int epi, int pro) {
     }
     return nullptr;
 }
-
-// token-row units per thread: one 8-element unit per 512 threads, 1 up to K = 4096, 3 up to 12288
-int upt_for(int K) { return K <= 8 * 512 ? 1 : (K <= 3 * 8 * 512 ? 3 : 0); }
 
 __global__ __launch_bounds__(256) void pack_q_kernel(PackGeom g, const uint8_t* q, uint8_t* qp) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece
@@ -580,28 +676,68 @@ int mgemv_init() {
     return 0;
 }
 
-// Launch shape from the matrix shape only: blocks of kMaxWaves waves; K slices KS (the fewest that
-// still give every CU a block), tiles per block TW = kMaxWaves / KS, supersteps per wave.
-void mgemv_shape(const PackGeom& g, int* KS, int* TW, int* nss_w) {
-    *KS = 1;
-    while (*KS < kMaxWaves && g.nss % (2 * *KS) == 0 && (long)g.tiles * *KS < (long)kCUs * kMaxWaves) *KS *= 2;
-    *TW = kMaxWaves / *KS;
-    *nss_w = g.nss / *KS;
+// Launch shape, from the matrix shape only.
+namespace {
+struct Shape {
+    int KS, base, extra, blocks, waves, nss_w, upt;
+    size_t lds_floor;  // dynamic LDS requested at least (keeps one block per CU)
+};
+
+// Up to 16 tiles per CU: one block per CU (fewer when there are fewer tiles), tiles spread
+// base / base + 1 per block, and the most K slices (a divisor of the supersteps) that keep
+// KS x (base + 1) within 16 waves.  Such a block asks for more than half a CU's LDS, so no CU
+// holds two.  Beyond 16 tiles per CU (the vocabulary head), short blocks of 4 slices x 2 tiles,
+// several per CU (measured: 248320 x 4096 Q8_0, 215 us with 1 slice x 8 tiles, 180 us at 4 x 2).
+// Blocks have at least 8 waves and enough threads that a token row is at most 3 units of 8
+// elements per thread.
+bool mgemv_shape(const PackGeom& g, Shape* sh) {
+    int KS, TW;
+    if (g.tiles <= 16 * kCUs) {
+        sh->blocks = g.tiles < kCUs ? g.tiles : kCUs;
+        sh->base = g.tiles / sh->blocks;
+        sh->extra = g.tiles % sh->blocks;
+        TW = sh->base + (sh->extra ? 1 : 0);
+        KS = 1;
+        for (int d = 1; d <= g.nss && d * TW <= kMaxWaves; ++d)
+            if (g.nss % d == 0) KS = d;
+        sh->lds_floor = 84 * 1024;
+    } else {
+        KS = 1;
+        while (KS < 4 && g.nss % (2 * KS) == 0) KS *= 2;
+        TW = 8 / KS;
+        sh->base = TW;
+        sh->extra = 0;
+        sh->blocks = (g.tiles + TW - 1) / TW;
+        sh->lds_floor = 0;
+    }
+    const int K8 = g.K / 8;
+    int waves = KS * TW;
+    if (waves < 8) waves = 8;
+    while (waves < kMaxWaves && waves * 64 < K8) ++waves;  // one unit per thread where that fits
+    const int upt = (K8 + waves * 64 - 1) / (waves * 64);
+    if (upt > 3) return false;
+    sh->KS = KS;
+    sh->waves = waves;
+    sh->nss_w = g.nss / KS;
+    sh->upt = upt == 1 ? 1 : 3;
+    return true;
 }
+}  // namespace
 
 int mgemv_blocks(int quant, int N, int K, int inter) {
     PackGeom g;
-    if (!pack_geom(quant, N, K, inter, &g)) return 0;
-    int KS, TW, nss_w;
-    mgemv_shape(g, &KS, &TW, &nss_w);
-    return (g.tiles + TW - 1) / TW;
+    Shape sh;
+    if (!pack_geom(quant, N, K, inter, &g) || !mgemv_shape(g, &sh)) return 0;
+    return sh.blocks;
 }
 
 size_t mgemv_lds_bytes(int M, int K) { return (size_t)(M <= 2 ? 1 : 2) * (K / 32) * 256 + kZeroBytes; }
 
 bool mgemv_fits(int M, int K) {
-    const int upt = upt_for(K);
-    return upt && (M <= 2 || upt == 1) && mgemv_lds_bytes(M, K) <= (size_t)kLdsLimit;
+    PackGeom g;
+    Shape sh;
+    if (!pack_geom(0, 16, K, 0, &g) || !mgemv_shape(g, &sh)) return false;
+    return (M <= 2 || sh.upt == 1) && mgemv_lds_bytes(M, K) <= (size_t)kLdsLimit;
 }
 
 // 0: launched; 1: this call is not served (M too large for LDS at this K); < 0 error.
@@ -609,11 +745,13 @@ bool mgemv_fits(int M, int K) {
 int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     PackGeom g;
     if (!pack_geom(quant, a.N, a.K, a.epi == GEMV_SWIGLU ? a.inter : 0, &g)) return -1;
-    int KS, TW, nss_w;
-    mgemv_shape(g, &KS, &TW, &nss_w);
+    Shape sh;
+    if (!mgemv_shape(g, &sh)) return 1;
     const int P = M <= 2 ? 1 : 2;
-    const size_t lds = mgemv_lds_bytes(M, a.K);
-    if (!mgemv_fits(M, a.K)) return 1;
+    const int tw_max = sh.base + (sh.extra ? 1 : 0);
+    const size_t need = mgemv_lds_bytes(M, a.K) + (a.rpart ? (size_t)tw_max * 16 * M * 64 : 0);
+    if (need > (size_t)kLdsLimit || (P == 2 && sh.upt != 1)) return 1;
+    const size_t lds = need > sh.lds_floor ? need : sh.lds_floor;
     if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
         (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_stride & 3))
         return -1;
@@ -621,10 +759,10 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if (a.epi == GEMV_MHC && !a.coef) return -1;
     if (a.rpart && (!a.next_w || (a.epi != GEMV_ADD && a.epi != GEMV_MHC) || (M & (M - 1)))) return -1;
     if (a.epi == GEMV_ADD && a.rpart && !a.expand) return -1;  // an ADD producer starts the mHC range
-    KernelFn f = pick(quant, g.U, upt_for(a.K), P, a.epi, a.pro);
+    KernelFn f = pick(quant, g.U, sh.upt, P, a.epi, a.pro);
     if (!f) return 1;
-    dim3 grid((g.tiles + TW - 1) / TW);
-    hipLaunchKernelGGL(f, grid, dim3(KS * TW * 64), lds, s, a, M, KS, TW, nss_w, g.tiles);
+    hipLaunchKernelGGL(f, dim3(sh.blocks), dim3(sh.waves * 64), lds, s, a, M, sh.KS, sh.base, sh.extra, sh.nss_w,
+                       g.tiles);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
