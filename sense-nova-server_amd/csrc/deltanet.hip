@@ -1,17 +1,22 @@
-// Gated DeltaNet decode step: causal depthwise conv (k=4) + SiLU, then the recurrent
-// gated delta rule with L2-normalised q/k and the gated RMS norm, for M = 1..4 tokens
-// (src/shaders/linear.wgsl:38-140 conv + delta, fused into one launch).
+// Gated DeltaNet decode step: causal depthwise conv (k=4) + SiLU, then the recurrent gated delta
+// rule with L2-normalised q/k, for M = 1..4 tokens (src/shaders/linear.wgsl:38-140 conv + delta,
+// fused into one launch).  Of the gated RMS norm over each head's 128 outputs (linear.wgsl:131-133),
+// out = ((o * rsqrt(mean(o^2) + eps)) * w) * silu(z), this kernel applies the per-column part: it
+// writes (o * w) * silu(z) and, per (token, head, column group), the partial sum of o^2.  The
+// consumer multiplies by the head's rsqrt factor (the out_proj GEMV prologue, or
+// gated_norm_kernel for the kernel-level entry).
 //
-// One block per value head h (k-head h / (n_v / n_k)), 512 threads: thread (j, g) owns
-// column j of the head's [128 (i), 128 (j)] f32 state, rows i in [32g, 32g+32), kept in
-// registers for all M tokens.  The conv of the head's 384 channels (q, k of its k-head,
-// v of the head) runs first, token by token, into LDS.
+// The recurrence of state column j only reads column j (kv_mem_j = sum_i S[i][j] k_i, then
+// S[:, j] += k (v_j - kv_mem_j) beta, o_j = sum_i S[i][j] q_i), so each value head's 128 columns
+// split over kCG blocks of kCols columns: 4 * n_v blocks, each streaming a quarter of the head's
+// state.  Thread (wave w, lane c + 4 rg) owns column 4w + c of the group, rows [8 rg, 8 rg + 8);
+// the sums over rows are 16-lane butterflies, so the token loop has no block barrier.
 //
-// Recurrent state lives in three slots per visit.  A call reads slot s_in, writes the
-// state after its last token to s_out and, when ckpt > 0, the state after token ckpt-1
-// to s_ck; s_out and s_ck are never s_in, so no block overwrites what another block
-// still reads (two v-heads share each k-head's conv channels).  A rejected draft
-// becomes a change of the current slot on the host instead of a copy.
+// Recurrent state lives in three slots per visit.  A call reads slot s_in, writes the state
+// after its last token to s_out and, when ckpt > 0, the state after token ckpt-1 to s_ck; s_out
+// and s_ck are never s_in, so no block overwrites what another block still reads (the blocks of
+// the v-heads that share a k-head all read its conv channels).  A rejected draft becomes a change
+// of the current slot on the host instead of a copy.
 #include "common.h"
 #include "kernels.h"
 
@@ -21,32 +26,34 @@ namespace snl {
 
 namespace {
 
-constexpr int DK = 128, DV = 128, kThreads = 512, kRowsPer = DK / (kThreads / DV);
-constexpr int kWaves = kThreads / 64;
+constexpr int DK = 128, DV = 128;
+constexpr int kCG = kDeltaGroups, kCols = DV / kCG;  // column groups per head, columns per group
+constexpr int kThreads = 512, kWaves = kThreads / 64, kRows = 8;  // rows per thread
 
-// Critical path per token: two barriers (the column sums of S^T k and S^T q).  Everything that
-// does not depend on the recurrence -- conv, q/k norms, beta and decay, the gate z -- is loaded
-// and computed before the token loop, and the gated RMS norm of all tokens runs after it.
 template <int M>
 __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
-    __shared__ float cq[M][DK], ck[M][DK], cv[M][DV];  // conv outputs (SiLU applied)
-    __shared__ float kvp[2][4][DV], op[2][4][DV];       // column partials, double-buffered by token
-    __shared__ float ob[M][DV];                          // head outputs before the gated norm
-    __shared__ float red[kWaves][2 * M];
+    __shared__ float cq[M][DK], ck[M][DK], cv[M][kCols];  // conv outputs (SiLU applied)
+    __shared__ float red[kWaves][M];                       // q / k sums of squares (waves 0-3)
+    __shared__ float ored[kWaves][M];                      // sums of o^2 per wave
 
     const StepDev* st = a.step;
     const int s_in = st->s_in, s_out = st->s_out, s_ck = st->s_ck, ckpt = st->ckpt;
-    const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int j = tid & (DV - 1), g = tid >> 7;
+    const int h = blockIdx.x / kCG, cg = blockIdx.x - (blockIdx.x / kCG) * kCG;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 3, rg = lane >> 2;
+    const int jl = 4 * wave + c, j = cg * kCols + jl;  // column in the group, in the head
     const int group = a.n_v / a.n_k, kh = h / group;
     const int key_dim = a.n_k * DK, cd = a.conv_dim;
-    const int z_off = cd, b_off = cd + a.n_v * DV, a_off = b_off + a.n_v;
+    const int b_off = cd + a.n_v * DV, a_off = b_off + a.n_v;
 
-    // ---- every load up front: conv inputs, recurrent state, gate, per-token scalars ----
-    const int which = tid >> 7, c0 = tid & 127;  // conv lanes: tid < 384
-    const int ch = which == 0 ? kh * DK + c0 : which == 1 ? key_dim + kh * DK + c0 : 2 * key_dim + h * DV + c0;
+    // ---- every load up front: conv inputs, the state slice, per-token scalars ----
+    // conv lanes: tid < 128 q channel, < 256 k channel, < 288 v channel of this column group
+    const int which = tid < DK ? 0 : tid < 2 * DK ? 1 : tid < 2 * DK + kCols ? 2 : 3;
+    const int ch = which == 0 ? kh * DK + tid
+                 : which == 1 ? key_dim + kh * DK + (tid - DK)
+                              : 2 * key_dim + h * DV + cg * kCols + (tid - 2 * DK);
     float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, r0 = 0.0f, r1 = 0.0f, r2 = 0.0f, cur[M];
-    if (tid < 3 * DK) {
+    if (which < 3) {
         const float4 w = *reinterpret_cast<const float4*>(a.lw + (size_t)ch * 4);
         w4[0] = w.x, w4[1] = w.y, w4[2] = w.z, w4[3] = w.w;
         const float* cs = a.conv_state + (size_t)s_in * a.conv_slot;
@@ -58,14 +65,17 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     }
     const size_t hoff = (size_t)h * DK * DV;
     const float* S0 = a.state + (size_t)s_in * a.state_slot + hoff;
-    float s[kRowsPer];
+    float s[kRows];
 #pragma unroll
-    for (int r = 0; r < kRowsPer; ++r) s[r] = S0[(size_t)(g * kRowsPer + r) * DV + j];
-    float z[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) z[m] = g == 0 ? a.proj[(size_t)m * a.proj_stride + z_off + h * DV + j] : 0.0f;
+    for (int r = 0; r < kRows; ++r) s[r] = S0[(size_t)(kRows * rg + r) * DV + j];
     const float* lwp = a.lw + (size_t)cd * 4;
     const float a_log = lwp[h], dt_bias = lwp[a.n_v + h], norm_w = lwp[2 * a.n_v + j];
+    float gz[M];  // silu of the output gate of column j
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float z = rg == 0 ? a.proj[(size_t)m * a.proj_stride + cd + h * DV + j] : 0.0f;
+        gz[m] = z / (1.0f + expf(-z));
+    }
     float beta[M], decay[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {  // linear.wgsl:113-117
@@ -76,20 +86,20 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
         decay[m] = expf(-expf(a_log) * sp);
     }
 
-    // ---- causal conv (linear.wgsl:38-66) of this head's channels, and the q/k sums of squares ----
+    // ---- causal conv (linear.wgsl:38-66) and the q / k sums of squares ----
     float sq[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) sq[m] = 0.0f;
-    if (tid < 3 * DK) {
-        // k-head channels are shared by `group` v-heads: the first one owns their state
-        const bool owner = which == 2 || (h % group) == 0;
+    if (which < 3) {
+        // the k-head's q/k conv state is owned by the first column group of its first v-head
+        const bool owner = which == 2 || ((h % group) == 0 && cg == 0);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             const float o = ((w4[0] * r0 + w4[1] * r1) + w4[2] * r2) + w4[3] * cur[m];
             const float v = o / (1.0f + expf(-o));
-            if (which == 0) cq[m][c0] = v;
-            else if (which == 1) ck[m][c0] = v;
-            else cv[m][c0] = v;
+            if (which == 0) cq[m][tid] = v;
+            else if (which == 1) ck[m][tid - DK] = v;
+            else cv[m][tid - 2 * DK] = v;
             if (which < 2) sq[m] = v * v;
             r0 = r1;
             r1 = r2;
@@ -122,69 +132,85 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     }
 
     // ---- the recurrence, token by token (linear.wgsl:118-136) ----
+    float osq[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const int b = m & 1;
         // kv_mem_j = sum_i decay*S[i][j] * k_i
         float kv = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kRowsPer; ++r) {
+        for (int r = 0; r < kRows; ++r) {
             s[r] = s[r] * decay[m];
-            kv = fmaf(s[r], ck[m][g * kRowsPer + r] * kscale[m], kv);
+            kv = fmaf(s[r], ck[m][kRows * rg + r] * kscale[m], kv);
         }
-        kvp[b][g][j] = kv;
-        __syncthreads();
-        const float kv_mem = ((kvp[b][0][j] + kvp[b][1][j]) + kvp[b][2][j]) + kvp[b][3][j];
-        const float dlt = (cv[m][j] - kv_mem) * beta[m];
+#pragma unroll
+        for (int sh = 4; sh < 64; sh <<= 1) kv = kv + __shfl_xor(kv, sh, 64);
+        const float dlt = (cv[m][jl] - kv) * beta[m];
         float o = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kRowsPer; ++r) {
-            s[r] = fmaf(ck[m][g * kRowsPer + r] * kscale[m], dlt, s[r]);
-            o = fmaf(s[r], cq[m][g * kRowsPer + r] * qscale[m], o);
+        for (int r = 0; r < kRows; ++r) {
+            s[r] = fmaf(ck[m][kRows * rg + r] * kscale[m], dlt, s[r]);
+            o = fmaf(s[r], cq[m][kRows * rg + r] * qscale[m], o);
         }
-        op[b][g][j] = o;
-        __syncthreads();
-        if (g == 0) ob[m][j] = ((op[b][0][j] + op[b][1][j]) + op[b][2][j]) + op[b][3][j];
+#pragma unroll
+        for (int sh = 4; sh < 64; sh <<= 1) o = o + __shfl_xor(o, sh, 64);
+        if (rg == 0) a.out[(size_t)m * a.n_v * DV + h * DV + j] = (o * norm_w) * gz[m];
+        // this wave's 4 columns: o^2 added over lanes 0-3
+        float q2 = o * o;
+        q2 = q2 + __shfl_xor(q2, 1, 64);
+        q2 = q2 + __shfl_xor(q2, 2, 64);
+        osq[m] = q2;
         if (m + 1 == ckpt) {
             float* SC = a.state + (size_t)s_ck * a.state_slot + hoff;
 #pragma unroll
-            for (int r = 0; r < kRowsPer; ++r) SC[(size_t)(g * kRowsPer + r) * DV + j] = s[r];
+            for (int r = 0; r < kRows; ++r) SC[(size_t)(kRows * rg + r) * DV + j] = s[r];
         }
     }
     float* SO = a.state + (size_t)s_out * a.state_slot + hoff;
 #pragma unroll
-    for (int r = 0; r < kRowsPer; ++r) SO[(size_t)(g * kRowsPer + r) * DV + j] = s[r];
+    for (int r = 0; r < kRows; ++r) SO[(size_t)(kRows * rg + r) * DV + j] = s[r];
 
-    // ---- gated RMS norm over the head's 128 outputs (linear.wgsl:131-133), plain w ----
-    float ss[M];
+    // partial sums of o^2 of this column group, waves in order
+    if (lane == 0)
 #pragma unroll
-    for (int m = 0; m < M; ++m) ss[m] = g == 0 ? ob[m][j] * ob[m][j] : 0.0f;
-    wave_sum_n(ss);
-    if (lane == 0 && wave < 2)
-#pragma unroll
-        for (int m = 0; m < M; ++m) red[wave][M + m] = ss[m];
+        for (int m = 0; m < M; ++m) ored[wave][m] = osq[m];
     __syncthreads();
-    if (g == 0)
+    if (tid < M) {
+        float t = 0.0f;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const float var_o = (red[0][M + m] + red[1][M + m]) / (float)DV;
-            const float oj = ob[m][j];
-            a.out[(size_t)m * a.n_v * DV + h * DV + j] =
-                ((oj * (1.0f / sqrtf(var_o + a.eps))) * norm_w) * (z[m] / (1.0f + expf(-z[m])));
-        }
+        for (int w = 0; w < kWaves; ++w) t = t + ored[w][tid];
+        a.ssq[((size_t)tid * a.n_v + h) * kCG + cg] = t;
+    }
+}
+
+// The head factor of the gated RMS norm (linear.wgsl:131-133) in place, for the kernel-level
+// entry: block (head, token), thread j: out *= rsqrt(mean(o^2) + eps), the mean from the
+// column-group partials added in order.
+__global__ __launch_bounds__(DV) void gated_norm_kernel(DeltaArgs a) {
+    const int h = blockIdx.x, m = blockIdx.y, j = threadIdx.x;
+    const float* ps = a.ssq + ((size_t)m * a.n_v + h) * kCG;
+    const float var_o = (((ps[0] + ps[1]) + ps[2]) + ps[3]) / (float)DV;
+    float* o = a.out + (size_t)m * a.n_v * DV + h * DV + j;
+    *o = *o * (1.0f / sqrtf(var_o + a.eps));
 }
 
 }  // namespace
 
 int launch_deltanet(const DeltaArgs& a, int M, hipStream_t s) {
-    if (a.n_k < 1 || a.n_v % a.n_k) return -1;
+    if (a.n_k < 1 || a.n_v % a.n_k || !a.ssq) return -1;
+    const dim3 grid(a.n_v * kCG);
     switch (M) {
-        case 1: hipLaunchKernelGGL(deltanet_kernel<1>, dim3(a.n_v), dim3(kThreads), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(deltanet_kernel<2>, dim3(a.n_v), dim3(kThreads), 0, s, a); break;
-        case 3: hipLaunchKernelGGL(deltanet_kernel<3>, dim3(a.n_v), dim3(kThreads), 0, s, a); break;
-        case 4: hipLaunchKernelGGL(deltanet_kernel<4>, dim3(a.n_v), dim3(kThreads), 0, s, a); break;
+        case 1: hipLaunchKernelGGL(deltanet_kernel<1>, grid, dim3(kThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(deltanet_kernel<2>, grid, dim3(kThreads), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(deltanet_kernel<3>, grid, dim3(kThreads), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(deltanet_kernel<4>, grid, dim3(kThreads), 0, s, a); break;
         default: return -1;
     }
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_deltanet_norm(const DeltaArgs& a, int M, hipStream_t s) {
+    if (M < 1 || M > 4 || !a.ssq) return -1;
+    hipLaunchKernelGGL(gated_norm_kernel, dim3(a.n_v, M), dim3(DV), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -116,6 +116,7 @@ struct snl_engine {
     int h = 0, q_dim = 0, kv_dim = 0, conv_dim = 0, lin_proj_rows = 0, attn_proj_rows = 0, lin_value_dim = 0;
 
     float *x = nullptr, *xn = nullptr, *proj = nullptr, *act = nullptr, *attn_out = nullptr, *qbuf = nullptr;
+    float* dn_ssq = nullptr;  // DeltaNet partial sums of squares [M][n_v][kDeltaGroups]
     float *coef = nullptr, *mhc_raw = nullptr, *mhc_part = nullptr, *partial = nullptr, *logits = nullptr, *hid = nullptr,
           *hlast = nullptr;
     float *mx = nullptr, *hn = nullptr, *m_logits = nullptr;
@@ -299,8 +300,8 @@ struct snl_engine {
         g.site_w = mr.site;
         g.raw = mhc_raw;
         g.coef = coef;
-        g.rin = mhc_part;
-        g.rin_n = pro == GEMV_NORM_MHC ? consumed_n : 0;
+        g.rin = pro == GEMV_GNORM ? dn_ssq : mhc_part;
+        g.rin_n = pro == GEMV_NORM_MHC ? consumed_n : pro == GEMV_GNORM ? kDeltaGroups : 0;
         g.iterations = cfg.mhc_iterations;
         g.next_w = mr.next;
         g.rpart = mr.next ? mhc_part : nullptr;
@@ -449,6 +450,7 @@ int snl_engine::init() {
         (rc = dalloc(&proj, (size_t)M * proj_w)) || (rc = dalloc(&act, (size_t)M * act_w)) ||
         (rc = dalloc(&attn_out, (size_t)M * attn_w)) || (rc = dalloc(&qbuf, (size_t)M * q_dim)) ||
         (rc = dalloc(&coef, (size_t)M * 8)) || (rc = dalloc(&mhc_raw, (size_t)M * 9)) ||
+        (rc = dalloc(&dn_ssq, (size_t)M * std::max(c.lin_v_heads, 1) * kDeltaGroups)) ||
         (rc = dalloc(&mhc_part, (size_t)kPartBlocks * M * 9)) ||
         (rc = dalloc(&partial, (size_t)M * c.n_heads * parts_max * (c.head_dim + 2))) ||
         (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)(M + 1) * h)) ||
@@ -542,6 +544,7 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             d.conv_slot = nl * conv_floats;
             d.state_slot = nl * state_floats;
             d.out = attn_out;
+            d.ssq = dn_ssq;
             d.conv_dim = conv_dim;
             d.n_k = c.lin_k_heads;
             d.n_v = c.lin_v_heads;
@@ -549,8 +552,9 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
             d.step = d_step;
             const double dn_bytes = 2.0 * 4.0 * (double)state_floats + (ckpt ? 4.0 * (double)state_floats : 0.0);
             if (op("deltanet", dn_bytes)) rc |= launch_deltanet(d, M, stream);
+            // the gated head norm of the DeltaNet output is the prologue of the output projection
             rc |= gemv("gemv_out_proj", L.mix_out, attn_out, lin_value_dim, x, 2 * h, M, mhc ? GEMV_MHC : GEMV_ADD,
-                       1, GEMV_PLAIN, nullptr, nullptr, merge_attn);
+                       1, GEMV_GNORM, nullptr, nullptr, merge_attn);
             ++lslot;
         }
         consumed_n = mhc ? part_n : 0;
@@ -1345,7 +1349,19 @@ int snl_deltanet(const float* proj, int proj_stride, const float* lw, float* con
     a.n_v = n_v;
     a.eps = eps;
     a.step = d;
-    if (launch_deltanet(a, M, s)) return SNL_EDEVICE;
+    // the partial sums of squares between the step and the gated norm: kernel-level scratch
+    static float* g_ssq = nullptr;
+    static size_t g_ssq_n = 0;
+    const size_t nss = (size_t)M * n_v * kDeltaGroups;
+    if (nss > g_ssq_n) {
+        hipFree(g_ssq);
+        g_ssq = nullptr;
+        g_ssq_n = 0;
+        if (hipMalloc((void**)&g_ssq, nss * sizeof(float)) != hipSuccess) return SNL_ENOMEM;
+        g_ssq_n = nss;
+    }
+    a.ssq = g_ssq;
+    if (launch_deltanet(a, M, s) || launch_deltanet_norm(a, M, s)) return SNL_EDEVICE;
     return hipStreamSynchronize(s) == hipSuccess ? SNL_OK : SNL_EDEVICE;
 }
 

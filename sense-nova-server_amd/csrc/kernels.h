@@ -11,10 +11,10 @@ namespace snl {
 
 // ---------------------------------------------------------------- GEMV (gemv.hip)
 enum GemvEpi { GEMV_STORE = 0, GEMV_ADD = 1, GEMV_MHC = 2, GEMV_SWIGLU = 3 };
-// Prologue applied to the token rows before the product: none, RMSNorm (1 + w) of stream 0, or
-// the mHC pre-mix pre0*x0 + pre1*x1 of both streams (pre from coef, written by launch_mhc) then
-// RMSNorm.
-enum GemvPro { GEMV_PLAIN = 0, GEMV_NORM = 1, GEMV_NORM_MHC = 2 };
+// Prologue applied to the token rows before the product: none, RMSNorm (1 + w) of stream 0, the
+// mHC pre-mix pre0*x0 + pre1*x1 of both streams (pre from the router sums) then RMSNorm, or the
+// gated RMS norm of each 128-wide DeltaNet head (GNORM).
+enum GemvPro { GEMV_PLAIN = 0, GEMV_NORM = 1, GEMV_NORM_MHC = 2, GEMV_GNORM = 3 };
 
 struct GemvArgs {
     const void* wq;      // quants [N, K] (Q8) or [N, K/2] (Q4), or tile order when packed
@@ -33,7 +33,8 @@ struct GemvArgs {
     int inter;           // SWIGLU: intermediate size (N == 2*inter; gate rows then up rows)
     int pro;             // GemvPro
     const float* norm_w; // NORM*: weights w of the (1 + w) RMSNorm [K]
-    float eps;
+    float eps;           // (GNORM: x is the gated DeltaNet output of 128-wide heads and rin the
+                         //  partial sums of squares [M][K/128][4] of their raw values)
     // mHC router (layers.wgsl:75-126).  A site's router sums (the 8 router-row dots with the
     // 2-stream row and its sum of squares) arrive as per-block partials [M][9][blocks] from the
     // GEMV that produced the row.  The NORM_MHC launch of the site adds them in block order and
@@ -119,12 +120,16 @@ struct DeltaArgs {
     float* state;        // 3 slots of [n_v, 128, 128]
     size_t conv_slot;    // floats per conv slot
     size_t state_slot;   // floats per state slot
-    float* out;          // [M, n_v*128]
+    float* out;          // [M, n_v*128] (o * w) * silu(z), before the head factor of the norm
+    float* ssq;          // [M, n_v, 4] partial sums of out^2 per column group of 32
     int conv_dim, n_k, n_v;
     float eps;
     const StepDev* step;  // s_in / s_out / s_ck / ckpt
 };
+constexpr int kDeltaGroups = 4;  // column groups per value head (partials per head in ssq)
 int launch_deltanet(const DeltaArgs& a, int M, hipStream_t s);
+// the gated RMS norm in place on out (kernel-level entry; the engine folds it into out_proj)
+int launch_deltanet_norm(const DeltaArgs& a, int M, hipStream_t s);
 
 // ---------------------------------------------------------------- gated attention (attention.hip)
 struct AttnArgs {

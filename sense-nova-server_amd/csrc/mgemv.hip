@@ -225,12 +225,14 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         sw0 = a.site_w[(size_t)16 * K];
         sw1 = a.site_w[(size_t)16 * K + 1];
     }
-    float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2];
+    // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
+    // of squares.
+    float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
         const int k8 = tid + u * nthr;
         const int kk = k8 < K8 ? k8 : 0;
-        if constexpr (PRO != GEMV_PLAIN) {
+        if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
             nw[u][0] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk];
             nw[u][1] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk + 1];
         }
@@ -242,10 +244,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                 if constexpr (PRO == GEMV_NORM_MHC) {
                     xb[m][u][0] = xrow[m][K4 + 2 * kk];
                     xb[m][u][1] = xrow[m][K4 + 2 * kk + 1];
+                } else if constexpr (PRO == GEMV_GNORM) {
+                    gp[m][u] = reinterpret_cast<const float4*>(a.rin)[(size_t)m * (K / 128) + kk / 16];
                 }
             } else {
                 xa[m][u][0] = xa[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 xb[m][u][0] = xb[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                gp[m][u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
         }
     }
@@ -350,7 +355,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                     t.z = pre0[m] * t.z + pre1[m] * v1.z;
                     t.w = pre0[m] * t.w + pre1[m] * v1.w;
                 }
-                if constexpr (PRO != GEMV_PLAIN) {
+                if constexpr (PRO == GEMV_GNORM) {  // the head factor of linear.wgsl:131-133
+                    const float4 pp = gp[m][u];
+                    const float var_o = (((pp.x + pp.y) + pp.z) + pp.w) / 128.0f;
+                    const float rr = 1.0f / sqrtf(var_o + a.eps);
+                    t.x = t.x * rr;
+                    t.y = t.y * rr;
+                    t.z = t.z * rr;
+                    t.w = t.w * rr;
+                }
+                if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
                     ssq[m] = fmaf(t.x, t.x, ssq[m]);
                     ssq[m] = fmaf(t.y, t.y, ssq[m]);
                     ssq[m] = fmaf(t.z, t.z, ssq[m]);
@@ -384,7 +398,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             ss = ss + wred_s[w][m][0];
             mx = fmaxf(mx, wred_s[w][m][1]);
         }
-        const float rinv = PRO == GEMV_PLAIN ? 1.0f : 1.0f / sqrtf(ss / (float)K + a.eps);
+        const float rinv = PRO == GEMV_NORM || PRO == GEMV_NORM_MHC ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
         const float top = mx * rinv;
         // keep |x| * factor below 2^14 so the f16 high part cannot overflow
         const int e = top >= 16384.0f ? ilogbf(top) - 13 : 0;
@@ -600,10 +614,14 @@ KernelFn pick_fn(int P, int epi, int pro) {
         SNL_G(GEMV_MHC, GEMV_PLAIN)
         SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
         SNL_G(GEMV_SWIGLU, GEMV_NORM)
-        // the mHC pre-mix reads two residual streams of the hidden size: K <= 8192 (one unit per thread)
+        // the mHC pre-mix reads two residual streams of the hidden size, the gated head norm the
+        // DeltaNet output: K <= 8192 (one unit per thread)
         if constexpr (UPT == 1) {
             SNL_G(GEMV_STORE, GEMV_NORM_MHC)
             SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
+            SNL_G(GEMV_ADD, GEMV_GNORM)
+            SNL_G(GEMV_MHC, GEMV_GNORM)
+            SNL_G(GEMV_STORE, GEMV_GNORM)
         }
     }
 #undef SNL_G
@@ -666,7 +684,7 @@ int mgemv_init() {
             for (int upt = 1; upt <= 3; upt += 2)
                 for (int P = 1; P <= 2; ++P)
                     for (int e = 0; e < 4; ++e)
-                        for (int p = 0; p < 3; ++p) {
+                        for (int p = 0; p < 4; ++p) {
                             KernelFn f = pick(q, U, upt, P, e, p);
                             if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -756,6 +774,7 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
         (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_stride & 3))
         return -1;
     if (a.pro == GEMV_NORM_MHC && (!a.site_w || !a.raw || !a.coef || !a.rin || a.rin_n < 1 || M > 2)) return -1;
+    if (a.pro == GEMV_GNORM && (!a.rin || a.rin_n != kDeltaGroups || a.K % 128)) return -1;
     if (a.epi == GEMV_MHC && !a.coef) return -1;
     if (a.rpart && (!a.next_w || (a.epi != GEMV_ADD && a.epi != GEMV_MHC) || (M & (M - 1)))) return -1;
     if (a.epi == GEMV_ADD && a.rpart && !a.expand) return -1;  // an ADD producer starts the mHC range
