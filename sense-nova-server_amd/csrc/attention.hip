@@ -65,20 +65,40 @@ __global__ __launch_bounds__(256) void prep_kernel(AttnArgs a) {
 
 __device__ __forceinline__ float h2f(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// Block barrier that orders LDS only (vector memory loads stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Raw buffer descriptor over [base, base + bytes): a load past `bytes` reads zero and touches no
+// memory.  Word 3 is the gfx9 raw (untyped) dword format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // Block (kv head, part of kPart keys) for all M tokens and the 4 query heads of the GQA group
 // (NC = 4M head-token combinations).  256 threads = 4 waves.
-//  scores: wave w takes keys [16w, 16w+16) of the part, 4 at a time: 16-lane row r of the wave
-//          holds key 4i+r, lane j of the row dims [16j, 16j+16); the 16 lanes of a row are reduced
-//          by a transposed butterfly (every combination takes the same shuffle sequence);
-//  softmax: exact within the part, 32 threads per combination;
-//  values: thread (dim pair, key half) accumulates its 32 keys with all loads in flight.
+//  loads:   the queries, then every key of the part, then every value, all in flight at once;
+//           rows past the part's last key read zero through the buffer range check;
+//  scores:  wave w takes keys [16w, 16w+16) of the part, 4 at a time: 16-lane row r of the wave
+//           holds key 4i+r, lane j of the row dims [16j, 16j+16); the 16 lanes of a row are reduced
+//           by a transposed butterfly (every combination takes the same shuffle sequence);
+//  softmax: exact within the part, 32 threads per combination; keys a token may not see get
+//           weight 0;
+//  values:  thread (dim pair, key half) accumulates its 32 keys (weight 0 adds nothing).
 // Each combination's arithmetic only depends on its own token's keys, so a token's result does
 // not depend on M or on its row index.
 template <int M>
 __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     constexpr int NC = G * M;
     static_assert(NC == 4 || NC == 8, "M = 1 or 2");
-    __shared__ float sc[NC][kPart];
+    constexpr int KI = kPart / 16;  // keys per 16-lane row
+    constexpr int KH = kPart / 2;   // keys per value thread
+    __shared__ __align__(16) float sc[NC][kPart];
     __shared__ float smax[NC], ssum[NC];
     __shared__ float2 vred[NC][128];
     const int kh = blockIdx.x, p = blockIdx.y;
@@ -95,20 +115,7 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) valid[m] = min(nkeys, pos0 + m + 1 - kstart);
 
-    // the part's values do not depend on the scores: their loads go out first
-    const int dp = tid & 127, kh2 = tid >> 7;
-    constexpr int KH = kPart / 2;
-    uint32_t vw[KH];
-    {
-        const uint32_t* vb = reinterpret_cast<const uint32_t*>(a.vcache + (size_t)kh * HD) + dp;
-#pragma unroll
-        for (int i = 0; i < KH; ++i) {
-            const int t = kh2 * KH + i;
-            vw[i] = t < nkeys ? vb[(size_t)(kstart + t) * (kv_dim / 2)] : 0u;
-        }
-    }
-
-    // ---- scores ----
+    // ---- loads: queries, keys, values ----
     float q[NC][16];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -119,26 +126,42 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
             q[c][4 * v] = t.x, q[c][4 * v + 1] = t.y, q[c][4 * v + 2] = t.z, q[c][4 * v + 3] = t.w;
         }
     }
-    const uint16_t* kb = a.kcache + (size_t)kh * HD + 16 * j;
+    __builtin_amdgcn_sched_barrier(0);
+    // the part's rows of the cache (all kv heads), nkeys of them in range
+    const unsigned row_bytes = (unsigned)kv_dim * 2;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.kcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.vcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
+    u32x4_t kraw[KI][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < KI; ++i) {
         const int t = 16 * w + 4 * i + r;  // key of this 16-lane row
+        const int off = t * (int)row_bytes + (kh * HD + 16 * j) * 2;
+        kraw[i][0] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
+        kraw[i][1] = __builtin_amdgcn_raw_buffer_load_b128(kr, off + 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int dp = tid & 127, kh2 = tid >> 7;
+    uint32_t vw[KH];
+#pragma unroll
+    for (int i = 0; i < KH; ++i) {
+        const int t = kh2 * KH + i;
+        vw[i] = __builtin_amdgcn_raw_buffer_load_b32(vr, t * (int)row_bytes + (kh * HD + 2 * dp) * 2, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- scores ----
+#pragma unroll
+    for (int i = 0; i < KI; ++i) {
+        const int t = 16 * w + 4 * i + r;
         float kf[16];
-        if (t < nkeys) {
-            const uint4* kp = reinterpret_cast<const uint4*>(kb + (size_t)(kstart + t) * kv_dim);
 #pragma unroll
-            for (int v = 0; v < 2; ++v) {
-                const uint4 raw = kp[v];
-                const uint32_t ws[4] = {raw.x, raw.y, raw.z, raw.w};
+        for (int v = 0; v < 2; ++v) {
+            const u32x4_t raw = kraw[i][v];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    kf[8 * v + 2 * e] = h2f(ws[e] & 0xFFFF);
-                    kf[8 * v + 2 * e + 1] = h2f(ws[e] >> 16);
-                }
+            for (int e = 0; e < 4; ++e) {
+                kf[8 * v + 2 * e] = h2f(raw[e] & 0xFFFF);
+                kf[8 * v + 2 * e + 1] = h2f(raw[e] >> 16);
             }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) kf[e] = 0.0f;
         }
         float d[NC];
 #pragma unroll
@@ -167,9 +190,9 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
         for (int mask = 8 / NC; mask > 0; mask >>= 1) tot = tot + __shfl_xor(tot, mask, 64);
         // lane j of the row holds combination j / (16 / NC)
-        if ((j & (16 / NC - 1)) == 0 && t < nkeys) sc[j / (16 / NC)][t] = tot * a.scale;
+        if ((j & (16 / NC - 1)) == 0) sc[j / (16 / NC)][t] = tot * a.scale;
     }
-    __syncthreads();
+    lds_barrier();
 
     // ---- exact softmax over the part, 32 threads per combination ----
     if (tid < 32 * NC) {
@@ -190,21 +213,25 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
             ssum[c] = sum;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
-    // ---- values: thread (dim pair dp, key half kh2), loaded with the keys above ----
+    // ---- values: thread (dim pair dp, key half kh2) ----
     float2 acc[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) acc[c] = make_float2(0.0f, 0.0f);
 #pragma unroll
-    for (int i = 0; i < KH; ++i) {
-        const int t = kh2 * KH + i;
-        const float v0 = h2f(vw[i] & 0xFFFF), v1 = h2f(vw[i] >> 16);
+    for (int i4 = 0; i4 < KH; i4 += 4) {
+        float4 wt[NC];
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            if (t < valid[c / G]) {
-                acc[c].x = fmaf(sc[c][t], v0, acc[c].x);
-                acc[c].y = fmaf(sc[c][t], v1, acc[c].y);
+        for (int c = 0; c < NC; ++c) wt[c] = *reinterpret_cast<const float4*>(&sc[c][kh2 * KH + i4]);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const float v0 = h2f(vw[i4 + ii] & 0xFFFF), v1 = h2f(vw[i4 + ii] >> 16);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float wv = ii == 0 ? wt[c].x : ii == 1 ? wt[c].y : ii == 2 ? wt[c].z : wt[c].w;
+                acc[c].x = fmaf(wv, v0, acc[c].x);
+                acc[c].y = fmaf(wv, v1, acc[c].y);
             }
         }
     }
