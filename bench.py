@@ -33,7 +33,7 @@ sys.path.insert(0, os.path.join(REPO, "sense-nova-server_amd"))
 METRIC = "9B Q8_0 MTP greedy decode tok/s (1 GPU); Q8 GEMV GB/s vs HBM peak"
 HBM_PEAK_GBS = 8000.0
 PROMPT = 1024
-ROOFLINE_KERNEL = "mgemv_kernel<0, 1, 3, 2, 4>"  # Q8_0, one token pair, SwiGLU epilogue, mHC prologue, U=4
+ROOFLINE_KERNEL = "mgemv_kernel<0, 1, 3, 2, 4, 1>"  # Q8_0, one token pair, SwiGLU epilogue, mHC prologue, U=4, UPT=1
 # HBM traffic of the roofline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (see summarize_pmc);
 # reported only while the kernel sources hash to the value recorded with it.
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_gate_up_9b_q8_traffic.json")
