@@ -1217,7 +1217,7 @@ int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s) {
                     if (s)
                         for (int u = 0; u < g.U; ++u)
                             s[(size_t)row * (cols / 32) + 4 * g.U * S + g.U * (lane >> 4) + u] =
-                                hs[pack_scale(g, T, S, lane) + u];
+                                hs[pack_scale(g, T, S, lane, u)];
                 }
         return SNL_OK;
     }

@@ -137,7 +137,7 @@ __device__ __forceinline__ int a_pos(int e) {
 // UPT: 8-element units of each token row per thread (K <= 8 * UPT * 512).
 template <int QT, int P, int EPI, int PRO, int U, int UPT>
 __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int base, int extra,
-                                                               int nss_w, int tiles) {
+                                                               int nss_w, int tiles, int il) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
     __shared__ float wred_s[kMaxWaves][2 * P][2];
@@ -158,35 +158,41 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const int Tl = tile0 + (active ? tw : 0);
     const int j = lane & 15, g = lane >> 4;
     const int nss = nss_w * KS;
-    // Weights stream through a ring of three chunks of CL loads (half a superstep when U == 4):
-    // chunk q of the slice is loads [q*CL, q*CL + CL) counted from the slice start, with the
-    // CS = U*CL/NI scales of its quant blocks.  Tile order (packing.h): load v of superstep S of
-    // tile T is 1 KiB at ((T*nss + S)*NI + v) KiB; the scales of superstep S are [S][lane][U].
-    // Every issue is unconditional (a chunk past the slice reads zeros without a memory access),
-    // so the loads keep one fixed order and each wait names exactly the chunk it needs.
+    // Weights stream through a ring of three chunks of CL loads (half a superstep when U == 4)
+    // with the CS = U*CL/NI scales of their quant blocks.  Chunk q of this wave's item
+    // i = T*KS + ks is at chunk index q*items + i (chunk-major, il) or i*nch + q (tile-major) of
+    // the packed matrix (packing.h): in both, a base for the item plus q times a stride.
+    // Every issue is unconditional: the descriptor ends at the item's last chunk, so a chunk past
+    // it reads zero without a memory access, and the loads keep one fixed order in which each
+    // wait names exactly the chunk it needs.
     constexpr int CL = U == 4 ? NI / 2 : NI;  // loads per chunk
     constexpr int CPS = NI / CL;              // chunks per superstep
     constexpr int CS = U / CPS;               // scales per chunk
     uint4 w0[CL], w1[CL], w2[CL];
     float s0[CS], s1[CS], s2[CS];
     const int nch = nss_w * CPS;
-    const size_t slice = (size_t)Tl * nss + ks * nss_w;  // first superstep of this wave's slice
+    const size_t item = (size_t)Tl * KS + ks;
+    const size_t items = (size_t)tiles * KS;
+    const size_t cbase = il ? item : item * nch;         // chunk index of chunk 0
+    const unsigned cstride = il ? (unsigned)items : 1u;  // chunk indices between chunks q and q + 1
     const __amdgpu_buffer_rsrc_t wr =
-        make_rsrc(static_cast<const uint8_t*>(a.wq) + slice * NI * 1024, active ? (unsigned)nch * CL * 1024 : 0u);
-    const __amdgpu_buffer_rsrc_t sr = make_rsrc(a.ws + slice * 64 * U, active ? (unsigned)nss_w * 64 * U * 4 : 0u);
-    const int wv = lane * 16, sv = lane * U * 4;
+        make_rsrc(static_cast<const uint8_t*>(a.wq) + cbase * CL * 1024,
+                  active ? ((unsigned)(nch - 1) * cstride + 1u) * CL * 1024 : 0u);
+    const __amdgpu_buffer_rsrc_t sr =
+        make_rsrc(a.ws + cbase * 64 * CS, active ? ((unsigned)(nch - 1) * cstride + 1u) * 64 * CS * 4 : 0u);
+    const int wv = lane * 16, sv = lane * CS * 4;
     // The scales first, then the quants; the scheduling barrier keeps chunks in issue order.  The
     // whole offset goes in the per-lane operand: the range check covers that operand and the
-    // instruction offset, not the scalar one.
+    // instruction offset.
     auto issue = [&](uint4 (&w)[CL], float (&sc)[CS], int q) {
-        const int so = sv + ((q / CPS) * 64 * U + (q % CPS) * CS) * 4;
+        const int so = sv + q * (int)cstride * 64 * CS * 4;
         if constexpr (CS == 2) {
             const snl_f32x2_t t = snl_raw_buffer_load_f32x2(sr, so, 0, 0);
             sc[0] = t.x, sc[1] = t.y;
         } else {
             sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 0));
         }
-        const int wo = wv + q * CL * 1024;
+        const int wo = wv + q * (int)cstride * CL * 1024;
 #pragma unroll
         for (int v = 0; v < CL; ++v)
             w[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo + v * 1024, 0, 0));
@@ -600,7 +606,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     }
 }
 
-using KernelFn = void (*)(GemvArgs, int, int, int, int, int, int);
+using KernelFn = void (*)(GemvArgs, int, int, int, int, int, int, int);
 
 template <int QT, int U, int UPT>
 KernelFn pick_fn(int P, int epi, int pro) {
@@ -643,8 +649,10 @@ KernelFn pick(int quant, int U, int UPT, int P, int epi, int pro) {
     return nullptr;
 }
 
+// Reference layout -> packed order: thread i takes the 16-byte piece (T, S, v, lane) i in tile-major
+// enumeration and writes it where packing.h places it.
 __global__ __launch_bounds__(256) void pack_q_kernel(PackGeom g, const uint8_t* q, uint8_t* qp) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= g.q_bytes / 16) return;
     const int lane = (int)(i & 63);
     size_t r = i >> 6;
@@ -654,7 +662,7 @@ __global__ __launch_bounds__(256) void pack_q_kernel(PackGeom g, const uint8_t* 
     const int row = pack_row(g, T, lane & 15);
     uint4 val = make_uint4(0u, 0u, 0u, 0u);
     if (row >= 0) val = *reinterpret_cast<const uint4*>(q + (size_t)row * g.row_bytes + pack_row_offset(g, S, v, lane >> 4));
-    *reinterpret_cast<uint4*>(qp + i * 16) = val;
+    *reinterpret_cast<uint4*>(qp + pack_piece(g, T, S, v, lane)) = val;
 }
 
 __global__ __launch_bounds__(256) void pack_s_kernel(PackGeom g, const float* s, float* sp) {
@@ -665,7 +673,8 @@ __global__ __launch_bounds__(256) void pack_s_kernel(PackGeom g, const float* s,
     const int S = (int)(r % g.nss), T = (int)(r / g.nss);
     const int row = pack_row(g, T, lane & 15);
     for (int u = 0; u < g.U; ++u)
-        sp[i * g.U + u] = row >= 0 ? s[(size_t)row * (g.K / 32) + 4 * g.U * S + g.U * (lane >> 4) + u] : 0.0f;
+        sp[pack_scale(g, T, S, lane, u)] =
+            row >= 0 ? s[(size_t)row * (g.K / 32) + 4 * g.U * S + g.U * (lane >> 4) + u] : 0.0f;
 }
 
 }  // namespace
@@ -694,49 +703,43 @@ int mgemv_init() {
     return 0;
 }
 
-// Launch shape, from the matrix shape only.
 namespace {
+
+// Launch shape, from the matrix shape only (the K split is the packing's, packing.h).
 struct Shape {
     int KS, base, extra, blocks, waves, nss_w, upt;
     size_t lds_floor;  // dynamic LDS requested at least (keeps one block per CU)
 };
 
-// Up to 16 tiles per CU: one block per CU (fewer when there are fewer tiles), tiles spread
-// base / base + 1 per block, and the most K slices (a divisor of the supersteps) that keep
-// KS x (base + 1) within 16 waves.  Such a block asks for more than half a CU's LDS, so no CU
-// holds two.  Beyond 16 tiles per CU (the vocabulary head), short blocks of 4 slices x 2 tiles,
-// several per CU (measured: 248320 x 4096 Q8_0, 215 us with 1 slice x 8 tiles, 180 us at 4 x 2).
-// Blocks have at least 8 waves and enough threads that a token row is at most 3 units of 8
-// elements per thread.
+// Chunk-major matrices: one block per CU (fewer when there are fewer tiles), tiles spread base /
+// base + 1 per block; such a block asks for more than half a CU's LDS, so no CU holds two.
+// Tile-major (the vocabulary head): short blocks of 2 tiles x KS slices, several per CU
+// (measured: 248320 x 4096 Q8_0, 215 us with 1 slice x 8 tiles, 180 us at 4 x 2).  Blocks have at
+// least 8 waves and enough threads that a token row is at most 3 units of 8 elements per thread.
 bool mgemv_shape(const PackGeom& g, Shape* sh) {
-    int KS, TW;
-    if (g.tiles <= 16 * kCUs) {
+    int TW;
+    if (g.il) {
         sh->blocks = g.tiles < kCUs ? g.tiles : kCUs;
         sh->base = g.tiles / sh->blocks;
         sh->extra = g.tiles % sh->blocks;
         TW = sh->base + (sh->extra ? 1 : 0);
-        KS = 1;
-        for (int d = 1; d <= g.nss && d * TW <= kMaxWaves; ++d)
-            if (g.nss % d == 0) KS = d;
         sh->lds_floor = 84 * 1024;
     } else {
-        KS = 1;
-        while (KS < 4 && g.nss % (2 * KS) == 0) KS *= 2;
-        TW = 8 / KS;
+        TW = 8 / g.KS;
         sh->base = TW;
         sh->extra = 0;
         sh->blocks = (g.tiles + TW - 1) / TW;
         sh->lds_floor = 0;
     }
     const int K8 = g.K / 8;
-    int waves = KS * TW;
+    int waves = g.KS * TW;
     if (waves < 8) waves = 8;
     while (waves < kMaxWaves && waves * 64 < K8) ++waves;  // one unit per thread where that fits
     const int upt = (K8 + waves * 64 - 1) / (waves * 64);
-    if (upt > 3) return false;
-    sh->KS = KS;
+    if (upt > 3 || g.KS * TW > kMaxWaves) return false;
+    sh->KS = g.KS;
     sh->waves = waves;
-    sh->nss_w = g.nss / KS;
+    sh->nss_w = g.nss_w;
     sh->upt = upt == 1 ? 1 : 3;
     return true;
 }
@@ -781,7 +784,7 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     KernelFn f = pick(quant, g.U, sh.upt, P, a.epi, a.pro);
     if (!f) return 1;
     hipLaunchKernelGGL(f, dim3(sh.blocks), dim3(sh.waves * 64), lds, s, a, M, sh.KS, sh.base, sh.extra, sh.nss_w,
-                       g.tiles);
+                       g.tiles, g.il);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

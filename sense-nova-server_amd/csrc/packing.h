@@ -13,13 +13,22 @@
 //   load v        NI loads per superstep (Q8: 2U, Q4: U) of 16 bytes per lane
 //   lane l        row j = l & 15 of the tile, lane group g = l >> 4
 //
-//   quants  [T][S][v][l][16 bytes] = row bytes [S*RB + g*GB + 16v, +16) with RB = 128U (Q8) or
-//           64U (Q4) bytes of a row per superstep and GB = RB/4 bytes per lane group
-//   scales  [T][S][l][U] = row scales [4U*S + U*g, +U)
+// Lane (j, g) of load v holds row j's bytes [S*RB + g*GB + 16v, +16) (RB = 128U (Q8) or 64U (Q4)
+// bytes of a row per superstep, GB = RB/4 per lane group): one 16-element half block (Q8) or one
+// whole block (Q4), and its scales are row scales [4U*S + U*g, +U).
 //
-// so lane (j, g) of load v holds one 16-element half block (Q8) or one whole block (Q4) of
-// row j, and its U scales arrive in one load.  Sizes: tiles*16*K (Q8) or tiles*8*K (Q4) bytes
-// and tiles*16*K/32 scales, the reference's sizes whenever the tile count divides the rows.
+// The GEMV streams each tile in KS slices of nss_w = nss/KS supersteps, one wave per (tile,
+// slice) item, in chunks of CL loads (half a superstep when U == 4, else a whole one) with the
+// CS = U/CPS scales of their blocks.  The order of the chunks in memory follows the launch shape:
+//   tile-major (il = 0):  chunk q of item i at ((i*nch + q)*CL + vv) KiB, scales likewise
+//                         (each wave streams one contiguous run; many short blocks, the
+//                         vocabulary head)
+//   chunk-major (il = 1): chunk q of item i at ((q*items + i)*CL + vv) KiB (one block per CU:
+//                         the whole grid sweeps memory together, which streams ~5-7% faster than
+//                         one contiguous run per wave)
+// with vv the load inside the chunk and the scales of chunk (q, i) at ((q*items + i)*64 + l)*CS.
+// Sizes: tiles*16*K (Q8) or tiles*8*K (Q4) bytes and tiles*16*K/32 scales, the reference's
+// sizes whenever the tile count divides the rows.
 #pragma once
 
 #include <stddef.h>
@@ -35,7 +44,40 @@ struct PackGeom {
     int row_bytes;           // bytes of one reference row
     int ss_bytes;            // bytes of one row per superstep
     size_t q_bytes, s_floats;
+    // streaming split (chosen from the shape alone)
+    int KS, nss_w;           // K slices per tile, supersteps per slice
+    int CPS, CL, CS;         // chunks per superstep, loads and scales per chunk
+    int nch, items;          // chunks per item, items (tiles * KS)
+    int il;                  // 1: chunk-major order (one block per CU), 0: tile-major
 };
+
+constexpr int kPackCUs = 256;       // MI355X compute units
+constexpr int kPackMaxWaves = 16;   // waves per GEMV block
+
+// The K split: up to 16 tiles per CU, one block per CU holds base or base + 1 tiles and KS is the
+// largest divisor of the superstep count with KS * (base + 1) <= 16 waves (chunk-major order);
+// taller matrices run many blocks of 2 tiles x KS <= 4 slices (tile-major order).
+__host__ __device__ inline void pack_split(PackGeom* g) {
+    int KS = 1;
+    // (chunk-major offsets are 32-bit: matrices up to 2 GiB)
+    if (g->tiles <= 16 * kPackCUs && g->q_bytes < ((size_t)1 << 31)) {
+        const int blocks = g->tiles < kPackCUs ? g->tiles : kPackCUs;
+        const int tw = g->tiles / blocks + (g->tiles % blocks ? 1 : 0);
+        for (int d = 1; d <= g->nss && d * tw <= kPackMaxWaves; ++d)
+            if (g->nss % d == 0) KS = d;
+        g->il = 1;
+    } else {
+        while (KS < 4 && g->nss % (2 * KS) == 0) KS *= 2;
+        g->il = 0;
+    }
+    g->KS = KS;
+    g->nss_w = g->nss / KS;
+    g->CPS = g->U == 4 ? 2 : 1;
+    g->CL = g->NI / g->CPS;
+    g->CS = g->U / g->CPS;
+    g->nch = g->nss_w * g->CPS;
+    g->items = g->tiles * KS;
+}
 
 // false when the shape has no tile order (K % 128 != 0, or a SwiGLU matrix with N != 2*inter)
 __host__ __device__ inline bool pack_geom(int quant, int N, int K, int inter, PackGeom* g) {
@@ -53,6 +95,7 @@ __host__ __device__ inline bool pack_geom(int quant, int N, int K, int inter, Pa
     g->ss_bytes = quant == 0 ? 128 * g->U : 64 * g->U;
     g->q_bytes = (size_t)g->tiles * g->nss * g->NI * 1024;
     g->s_floats = (size_t)g->tiles * g->nss * 64 * g->U;
+    pack_split(g);
     return true;
 }
 
@@ -72,14 +115,21 @@ __host__ __device__ inline int pack_row_offset(const PackGeom& g, int S, int v, 
     return S * g.ss_bytes + gg * (g.ss_bytes / 4) + 16 * v;
 }
 
-// offset of the 16-byte piece (T, S, v, lane) in the packed quants
-__host__ __device__ inline size_t pack_piece(const PackGeom& g, int T, int S, int v, int lane) {
-    return (((size_t)T * g.nss + S) * g.NI + v) * 1024 + (size_t)lane * 16;
+// chunk index of (item, chunk) in memory order
+__host__ __device__ inline size_t pack_chunk(const PackGeom& g, int item, int q) {
+    return g.il ? (size_t)q * g.items + item : (size_t)item * g.nch + q;
 }
 
-// offset of the first of the U scales of (T, S, lane) in the packed scales
-__host__ __device__ inline size_t pack_scale(const PackGeom& g, int T, int S, int lane) {
-    return (((size_t)T * g.nss + S) * 64 + lane) * g.U;
+// offset of the 16-byte piece (T, S, v, lane) in the packed quants
+__host__ __device__ inline size_t pack_piece(const PackGeom& g, int T, int S, int v, int lane) {
+    const int item = T * g.KS + S / g.nss_w, q = (S % g.nss_w) * g.CPS + v / g.CL;
+    return (pack_chunk(g, item, q) * g.CL + v % g.CL) * 1024 + (size_t)lane * 16;
+}
+
+// offset of scale u (0..U-1) of (T, S, lane) in the packed scales
+__host__ __device__ inline size_t pack_scale(const PackGeom& g, int T, int S, int lane, int u) {
+    const int item = T * g.KS + S / g.nss_w, q = (S % g.nss_w) * g.CPS + u / g.CS;
+    return (pack_chunk(g, item, q) * 64 + lane) * g.CS + u % g.CS;
 }
 
 // Reference layout -> tile order on the device (q, s: reference quants and scales).
