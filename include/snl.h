@@ -64,6 +64,18 @@ typedef struct snl_engine snl_engine;
  * DeltaNet in_proj and the MTP head stay Q8_0 as in src/convert.rs:228-311).
  * ctx = KV positions per attention layer.  Returns SNL_OK and *out, or an error. */
 int snl_engine_create(const snl_config* cfg, uint64_t seed, int quant, int ctx, snl_engine** out);
+/* Engine::load (src/engine.rs:230-644) from the reference's `.snl` weight files
+ * (src/weights.rs:1-121): `path` the text model, `mtp_path` (nullable) the MTP head, as written
+ * by the converter (src/convert.rs:316-427).  Matrices keep each tensor's dtype (q8_0 / q4_0);
+ * ctx is clamped to the model's max_position.  The vision tower is not loaded.  Errors (missing
+ * or misshapen tensors, bad header) return SNL_EARG with the message in snl_create_error(). */
+int snl_engine_load(const char* path, const char* mtp_path, int ctx, snl_engine** out);
+/* The converter's output (src/convert.rs:316-427) for the engine's current weights: the text model
+ * to `path` and, when mtp_path is not NULL, the MTP head to mtp_path, so that snl_engine_load
+ * (or the reference) reads them back unchanged.  model_name (nullable) goes in the header. */
+int snl_engine_save(snl_engine* e, const char* path, const char* mtp_path, const char* model_name);
+/* The engine's model configuration (for a loaded engine, the one its weight file holds). */
+int snl_engine_config(const snl_engine* e, snl_config* out);
 void snl_engine_destroy(snl_engine* e);
 /* Message of the last failed call on this handle ("" if none). */
 const char* snl_last_error(const snl_engine* e);

@@ -21,6 +21,7 @@
 #include "../../include/snl.h"
 #include "kernels.h"
 #include "packing.h"
+#include "snl_file.h"
 
 namespace snl {
 
@@ -46,6 +47,33 @@ enum Kind {
     K_FC_E = 20, K_FC_H = 21, K_NORM_E = 22, K_NORM_H = 23, K_MTP_NORM = 24
 };
 constexpr int kMtpLayer = 0xFFF;
+
+// Name of tensor (layer, kind) in the reference's weight files (src/convert.rs:203-311): the
+// main file holds the globals and l{i}.*, the MTP file mtp.*.
+std::string tensor_name(int layer, int kind) {
+    if (layer == -1) return kind == K_EMBED ? "embed" : kind == K_LM_HEAD ? "lm_head" : "norm";
+    const std::string p = layer == kMtpLayer ? std::string("mtp.") : "l" + std::to_string(layer) + ".";
+    switch (kind) {
+        case K_IN_LN: return p + "in_ln";
+        case K_POST_LN: return p + "post_ln";
+        case K_QK_NORM: return p + "qk_norm";
+        case K_LIN: return p + "lin";
+        case K_QKV: return p + "qkv";
+        case K_O_PROJ: return p + "o_proj";
+        case K_IN_PROJ: return p + "in_proj";
+        case K_OUT_PROJ: return p + "out_proj";
+        case K_GATE_UP: return p + "gate_up";
+        case K_DOWN: return p + "down";
+        case K_MHC_ATTN: return p + "mhc_attn";
+        case K_MHC_FFN: return p + "mhc_ffn";
+        case K_FC_E: return p + "fc_e";
+        case K_FC_H: return p + "fc_h";
+        case K_NORM_E: return p + "norm_e";
+        case K_NORM_H: return p + "norm_h";
+        case K_MTP_NORM: return p + "norm";
+    }
+    return p + "?";
+}
 
 uint64_t host_smix(uint64_t x) {
     x += 0x9E3779B97F4A7C15ull;
@@ -98,6 +126,10 @@ struct snl_engine {
     snl_config cfg{};
     int ctx = 0, quant = 0;
     uint64_t seed = 0;
+    int64_t max_position = 262144;  // ModelConfig::max_position, kept for snl_engine_save
+    // weight files while snl_engine_load runs init (null: the seeded generator draws the weights)
+    const SnlFile* src = nullptr;
+    const SnlFile* msrc = nullptr;
     hipStream_t stream = nullptr;
     std::vector<void*> allocs;
     // reference-layout staging of one matrix while the weights are drawn and packed (init only)
@@ -200,20 +232,38 @@ struct snl_engine {
 
     // Draw a rows x cols quantised matrix (reference layout, src/weights.rs:48-55).  GEMV matrices
     // (pack_inter >= 0) are then stored in tile order; pack_inter > 0 pairs gate and up rows.
+    // With a weight file the matrix is read from it instead (its own dtype; the shape must match).
     int gen_q(QW& w, int layer, int kind, int rows, int cols, int qt, int pack_inter = 0) {
+        const SnlFile* f = layer == kMtpLayer ? msrc : src;
+        const FileTensor* ft = nullptr;
+        if (f) {
+            const std::string name = tensor_name(layer, kind);
+            ft = f->find(name);
+            if (!ft) return fail(SNL_EARG, "weight file is missing tensor `%s`", name.c_str());
+            if (ft->dtype == FD_F32 || ft->shape.size() != 2 || ft->rows() != rows || ft->cols() != cols)
+                return fail(SNL_EARG, "tensor `%s`: expected a quantised [%d, %d] matrix", name.c_str(), rows, cols);
+            qt = ft->dtype == FD_Q8_0 ? 0 : 1;
+        }
         w.rows = rows;
         w.cols = cols;
         w.quant = qt;
         const size_t n = (size_t)rows * cols;
+        const size_t qn = qt == 0 ? n : n / 2;
         const uint64_t key = stream_key(seed, layer, kind);
         int rc;
+        // fill reference-layout quants and scales, from the file or the generator
+        auto fill = [&](void* q, float* sc) {
+            if (ft)
+                return hipMemcpyAsync(q, f->quants(*ft), qn, hipMemcpyHostToDevice, stream) != hipSuccess ||
+                       hipMemcpyAsync(sc, f->scales(*ft), n / 32 * 4, hipMemcpyHostToDevice, stream) != hipSuccess;
+            return launch_gen_matrix(key, rows, cols, 0.02f, qt, q, sc, stream) != 0;
+        };
         if (pack_inter < 0) {
             uint8_t* q;
-            if ((rc = dalloc(&q, qt == 0 ? n : n / 2))) return rc;
+            if ((rc = dalloc(&q, qn))) return rc;
             w.q = q;
             if ((rc = dalloc(&w.s, n / 32))) return rc;
-            if (launch_gen_matrix(key, rows, cols, 0.02f, qt, w.q, w.s, stream))
-                return fail(SNL_EDEVICE, "weight init launch failed");
+            if (fill(w.q, w.s)) return fail(SNL_EDEVICE, "weight init failed");
             return SNL_OK;
         }
         PackGeom g;
@@ -236,9 +286,8 @@ struct snl_engine {
         if ((rc = dalloc(&w.s, g.s_floats))) return rc;
         w.packed = true;
         w.inter = pack_inter;
-        if (launch_gen_matrix(key, rows, cols, 0.02f, qt, gen_tmp_q, gen_tmp_s, stream) ||
-            launch_pack_matrix(g, gen_tmp_q, gen_tmp_s, w.q, w.s, stream))
-            return fail(SNL_EDEVICE, "weight init launch failed");
+        if (fill(gen_tmp_q, gen_tmp_s) || launch_pack_matrix(g, gen_tmp_q, gen_tmp_s, w.q, w.s, stream))
+            return fail(SNL_EDEVICE, "weight init failed");
         return SNL_OK;
     }
 
@@ -255,6 +304,16 @@ struct snl_engine {
         v.n = n;
         int rc = dalloc(&v.p, n);
         if (rc) return rc;
+        if (const SnlFile* f = layer == kMtpLayer ? msrc : src) {
+            const std::string name = tensor_name(layer, kind);
+            const FileTensor* ft = f->find(name);
+            if (!ft) return fail(SNL_EARG, "weight file is missing tensor `%s`", name.c_str());
+            if (ft->dtype != FD_F32 || ft->rows() * ft->cols() != n)
+                return fail(SNL_EARG, "tensor `%s`: expected %d f32 values", name.c_str(), n);
+            if (hipMemcpyAsync(v.p, f->quants(*ft), (size_t)n * 4, hipMemcpyHostToDevice, stream) != hipSuccess)
+                return fail(SNL_EDEVICE, "weight upload failed");
+            return SNL_OK;
+        }
         if (launch_gen_vector(stream_key(seed, layer, kind), n, vkind, stdv, aux0, aux1, v.p, stream))
             return fail(SNL_EDEVICE, "vector init launch failed");
         return SNL_OK;
@@ -669,6 +728,156 @@ int snl_engine_create(const snl_config* cfg, uint64_t seed, int quant, int ctx, 
     }
     *out = e;
     return SNL_OK;
+}
+
+// Engine::load (src/engine.rs:230-644) from the reference's weight files: `path` the text model,
+// `mtp_path` (nullable) the MTP head.  ctx is clamped to the model's max_position as the
+// reference does.
+int snl_engine_load(const char* path, const char* mtp_path, int ctx, snl_engine** out) {
+    if (!out) return SNL_EARG;
+    *out = nullptr;
+    if (!path) {
+        g_create_error = "null path";
+        return SNL_EARG;
+    }
+    SnlFile main_file, mtp_file;
+    FileConfig fc;
+    std::string err;
+    if (!main_file.open(path, &err) || !main_file.config(&fc, &err) || (mtp_path && !mtp_file.open(mtp_path, &err))) {
+        g_create_error = err;
+        return SNL_EARG;
+    }
+    snl_config cfg = fc.cfg;
+    cfg.has_mtp = mtp_path ? 1 : 0;
+    if (const char* why = validate(&cfg)) {
+        g_create_error = std::string("unsupported model configuration: ") + why;
+        return SNL_EARG;
+    }
+    const std::string& q = main_file.quant();
+    if (q != "q8_0" && q != "q4_0") {
+        g_create_error = "unknown quantization `" + q + "`";
+        return SNL_EARG;
+    }
+    if (fc.max_position < ctx) ctx = (int)fc.max_position;
+    if (ctx < 2 || ctx > (1 << 22)) {
+        g_create_error = "bad ctx";
+        return SNL_EARG;
+    }
+    snl_engine* e = new snl_engine();
+    e->cfg = cfg;
+    e->ctx = ctx;
+    e->quant = q == "q4_0" ? 1 : 0;
+    e->max_position = fc.max_position;
+    e->src = &main_file;
+    e->msrc = mtp_path ? &mtp_file : nullptr;
+    int rc = e->init();
+    // every upload from the mapped files has finished before they are unmapped
+    if (e->stream && hipStreamSynchronize(e->stream) != hipSuccess && !rc) rc = e->fail(SNL_EDEVICE, "weight upload failed");
+    e->src = e->msrc = nullptr;
+    if (rc) {
+        g_create_error = e->err;
+        snl_engine_destroy(e);
+        return rc;
+    }
+    *out = e;
+    return SNL_OK;
+}
+
+namespace {
+
+// The tensors of one file in the converter's order (src/convert.rs:203-311, plan_mtp and plan).
+std::vector<std::pair<int, int>> file_tensors(const snl_config& c, bool mtp) {
+    std::vector<std::pair<int, int>> t;
+    if (mtp) {
+        const int L = kMtpLayer;
+        for (int k : {K_FC_E, K_FC_H, K_NORM_E, K_NORM_H, K_MTP_NORM, K_IN_LN, K_POST_LN, K_QK_NORM, K_QKV, K_O_PROJ,
+                      K_GATE_UP, K_DOWN})
+            t.emplace_back(L, k);
+        return t;
+    }
+    t.emplace_back(-1, K_EMBED);
+    t.emplace_back(-1, K_LM_HEAD);
+    t.emplace_back(-1, K_NORM);
+    for (int i = 0; i < c.n_layers; ++i) {
+        t.emplace_back(i, K_IN_LN);
+        t.emplace_back(i, K_POST_LN);
+        t.emplace_back(i, c.full_attention[i] ? K_QK_NORM : K_LIN);
+        if (c.mhc_streams > 0 && c.mhc_start <= i && i < c.mhc_end) {
+            t.emplace_back(i, K_MHC_ATTN);
+            t.emplace_back(i, K_MHC_FFN);
+        }
+    }
+    for (int i = 0; i < c.n_layers; ++i) {
+        if (c.full_attention[i]) {
+            t.emplace_back(i, K_QKV);
+            t.emplace_back(i, K_O_PROJ);
+        } else {
+            t.emplace_back(i, K_IN_PROJ);
+            t.emplace_back(i, K_OUT_PROJ);
+        }
+        t.emplace_back(i, K_GATE_UP);
+        t.emplace_back(i, K_DOWN);
+    }
+    return t;
+}
+
+int save_file(snl_engine* e, const char* path, bool mtp, const char* model_name) {
+    const auto list = file_tensors(e->cfg, mtp);
+    std::vector<WriteTensor> wt;
+    for (const auto& lk : list) {
+        int rows = 0, cols = 0;
+        const int type = snl_tensor_info(e, lk.first, lk.second, &rows, &cols);
+        if (type < 0) return e->fail(SNL_EDEVICE, "tensor `%s` is missing", tensor_name(lk.first, lk.second).c_str());
+        WriteTensor w;
+        w.name = tensor_name(lk.first, lk.second);
+        w.dtype = type == 2 ? FD_F32 : type == 0 ? FD_Q8_0 : FD_Q4_0;
+        if (type == 2) w.shape = {cols};
+        else w.shape = {rows, cols};
+        wt.push_back(w);
+    }
+    FileConfig fc;
+    fc.cfg = e->cfg;
+    fc.max_position = e->max_position;
+    SnlWriter wr;
+    std::vector<FileTensor> placed;
+    std::string err;
+    // the MTP file is always 8-bit (src/convert.rs:326)
+    const std::string quant = mtp || e->quant == 0 ? "q8_0" : "q4_0";
+    if (!wr.begin(path, model_name ? model_name : "", quant, fc, wt, &placed, &err)) return e->fail(SNL_EARG, "%s", err.c_str());
+    std::vector<uint8_t> q;
+    std::vector<float> sc;
+    for (size_t i = 0; i < list.size(); ++i) {
+        const FileTensor& ft = placed[i];
+        q.resize(ft.quant_bytes());
+        sc.resize(ft.scale_bytes() / 4);
+        const int rc = snl_tensor_read(e, list[i].first, list[i].second, q.data(), sc.empty() ? nullptr : sc.data());
+        if (rc) return rc;
+        if (!wr.write_region(ft.offset, q.data(), q.size(), &err) ||
+            (!sc.empty() && !wr.write_region(ft.scales_offset, sc.data(), sc.size() * 4, &err)))
+            return e->fail(SNL_EARG, "%s", err.c_str());
+    }
+    if (!wr.finish(&err)) return e->fail(SNL_EARG, "%s", err.c_str());
+    return SNL_OK;
+}
+
+}  // namespace
+
+// The model configuration of an engine (a loaded engine's comes from its weight file).
+int snl_engine_config(const snl_engine* e, snl_config* out) {
+    if (!e || !out) return SNL_EARG;
+    *out = e->cfg;
+    return SNL_OK;
+}
+
+// The converter's output (src/convert.rs:316-427) for the engine's weights: the text model to
+// `path` and, when mtp_path is given, the MTP head to mtp_path.
+int snl_engine_save(snl_engine* e, const char* path, const char* mtp_path, const char* model_name) {
+    if (!e || !path) return SNL_EARG;
+    e->err.clear();
+    if (mtp_path && !e->cfg.has_mtp) return e->fail(SNL_EARG, "the engine has no MTP head");
+    int rc = save_file(e, path, false, model_name);
+    if (!rc && mtp_path) rc = save_file(e, mtp_path, true, model_name);
+    return rc;
 }
 
 void snl_engine_destroy(snl_engine* e) {

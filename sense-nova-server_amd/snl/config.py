@@ -144,6 +144,22 @@ class ModelConfig:
                     or inside(self.loop_end, self.n_layers)):
                 raise ValueError("mHC range crosses a loop boundary")
 
+    @staticmethod
+    def from_struct(s: SnlConfig) -> "ModelConfig":
+        """The inverse of to_struct (used for models loaded from a weight file)."""
+        mhc = None
+        if s.mhc_streams > 0:
+            mhc = (s.mhc_start, s.mhc_end, s.mhc_streams, s.mhc_iterations)
+        return ModelConfig(
+            hidden=s.hidden, intermediate=s.intermediate, vocab=s.vocab, n_layers=s.n_layers,
+            full_attention=[bool(s.full_attention[i]) for i in range(s.n_layers)],
+            n_heads=s.n_heads, n_kv_heads=s.n_kv_heads, head_dim=s.head_dim, rot_dim=s.rot_dim,
+            rope_theta=float(s.rope_theta), mrope_section=tuple(int(s.mrope_section[i]) for i in range(3)),
+            lin_k_heads=s.lin_k_heads, lin_v_heads=s.lin_v_heads, lin_k_dim=s.lin_k_dim, lin_v_dim=s.lin_v_dim,
+            conv_kernel=s.conv_kernel, eps=float(s.eps), loop_start=s.loop_start, loop_end=s.loop_end,
+            loop_count=s.loop_count, mhc=mhc, has_mtp=bool(s.has_mtp),
+            eos=tuple(int(s.eos[i]) for i in range(s.n_eos)))
+
     def to_struct(self) -> SnlConfig:
         s = SnlConfig()
         for f in ("hidden", "intermediate", "vocab", "n_layers", "n_heads", "n_kv_heads", "head_dim", "rot_dim",

@@ -59,6 +59,9 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(LIB_PATH)
         L.snl_engine_create.argtypes = [ctypes.POINTER(SnlConfig), ctypes.c_uint64, ctypes.c_int, ctypes.c_int,
                                         ctypes.POINTER(vp)]
+        L.snl_engine_load.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(vp)]
+        L.snl_engine_save.argtypes = [vp, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p]
+        L.snl_engine_config.argtypes = [vp, ctypes.POINTER(SnlConfig)]
         L.snl_engine_destroy.argtypes = [vp]
         L.snl_last_error.restype = ctypes.c_char_p
         L.snl_last_error.argtypes = [vp]
@@ -109,7 +112,8 @@ def _ptr(a: np.ndarray, t):
 
 class Engine:
     """Engine API of the reference (src/engine.rs) on one MI355X.  Weights are drawn on the device
-    from `seed` (quant 0 = Q8_0, 1 = Q4_0)."""
+    from `seed` (quant 0 = Q8_0, 1 = Q4_0), or read from the reference's `.snl` files with
+    Engine.load."""
 
     def __init__(self, cfg: ModelConfig, seed: int = 1, quant: int = 0, ctx: int = 512):
         cfg.validate()
@@ -121,6 +125,28 @@ class Engine:
             raise SnlError(rc, lib().snl_create_error().decode())
         self.h = h
         self.vocab = cfg.vocab
+
+    @classmethod
+    def load(cls, path: str, mtp_path: str | None = None, ctx: int = 512) -> "Engine":
+        """Engine::load (src/engine.rs:230) from a text-model `.snl` file and an optional MTP file."""
+        h = vp()
+        rc = lib().snl_engine_load(os.fsencode(path), os.fsencode(mtp_path) if mtp_path else None, ctx,
+                                   ctypes.byref(h))
+        if rc != SNL_OK:
+            raise SnlError(rc, lib().snl_create_error().decode())
+        self = cls.__new__(cls)
+        self.h = h
+        cs = SnlConfig()
+        lib().snl_engine_config(h, ctypes.byref(cs))
+        self._cs = cs
+        self.cfg = ModelConfig.from_struct(cs)
+        self.vocab = self.cfg.vocab
+        return self
+
+    def save(self, path: str, mtp_path: str | None = None, model_name: str = "") -> None:
+        """Write the weights as the converter does (src/convert.rs:316-427)."""
+        self._check(lib().snl_engine_save(self.h, os.fsencode(path), os.fsencode(mtp_path) if mtp_path else None,
+                                          model_name.encode()))
 
     def close(self):
         if getattr(self, "h", None):
