@@ -126,7 +126,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
 /* Engine::rollback (src/engine.rs:688-697): undo the second token of the last 2-token
  * checkpointed forward. */
 int snl_rollback(snl_engine* e);
-/* Engine::snapshot / restore / reset (src/engine.rs:646-683). slot < 4. */
+/* Engine::snapshot / restore / reset (src/engine.rs:646-683). slot < SNL_SNAPSHOTS. */
 int snl_snapshot(snl_engine* e, int slot);
 int snl_restore(snl_engine* e, int slot, int pos);
 int snl_reset(snl_engine* e);
@@ -162,6 +162,43 @@ int snl_decoder_create(snl_engine* e, const uint32_t* prompt, int n, int spec, s
 int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out);
 int snl_decoder_stats(const snl_decoder* d, snl_gen_stats* out);
 void snl_decoder_destroy(snl_decoder* d);
+
+/* ---- the generation worker with its prefix cache (src/worker.rs:57-272) ------------------- */
+
+/* Snapshot slots of an engine (SNAPSHOTS, src/engine.rs:20). */
+#define SNL_SNAPSHOTS 4
+
+/* Finish (src/worker.rs:43-55) of one request: reason 0 = length, 1 = stop (EOS). */
+typedef struct snl_finish {
+    int32_t reason, prompt_tokens, completion_tokens, cached_tokens, drafted, accepted;
+    double prefill_s, decode_s;
+} snl_finish;
+
+/* The Worker (src/worker.rs:57-73) over one engine.  It owns the engine's state between its
+ * requests: the keys of the tokens the caches hold ("live") and what each snapshot slot holds,
+ * with a last-used clock.  A call on the engine from elsewhere (snl_forward, snl_generate, ...)
+ * makes the worker forget both at its next request.  self_pause = 1 keeps the reference's
+ * speculation self-pause (src/worker.rs:222-234); 0 drafts in every request. */
+typedef struct snl_worker snl_worker;
+int snl_worker_create(snl_engine* e, int self_pause, snl_worker** out);
+void snl_worker_destroy(snl_worker* w);
+
+/* Worker::run (src/worker.rs:123-272) for one text prompt with greedy sampling: reuse the live
+ * state or the snapshot whose keys are the longest strict prefix of the prompt (or reset),
+ * feed the prompt, snapshot after its first snapshot_at tokens into the least recently used
+ * slot when snapshot_at is past the reused part and short of n (< 0: none, as server.rs:262
+ * sets it at the last <|im_start|>), then decode as snl_generate does, drafting when spec is
+ * set, the model has an MTP head and no self-pause is running.  out receives
+ * max(1, min(max_tokens, ctx - n)) tokens at most; gaps (nullable) the top-2 margins; fin
+ * (nullable) the Finish record, whose cached_tokens counts the prompt tokens not fed again.
+ * Unlike the reference, a snapshot is dropped once a request writes the attention caches
+ * under its prefix with another sequence (a snapshot holds only the recurrent state).  On an
+ * error the engine is reset and the cache emptied (src/worker.rs:94-101). */
+int snl_worker_run(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at, int max_tokens, int spec,
+                   uint32_t* out, float* gaps, snl_finish* fin);
+
+/* The cache bookkeeping: live length, and per slot the key count (-1 = empty) and last use. */
+int snl_worker_cache(const snl_worker* w, int* live_len, int* snap_len, uint64_t* snap_used);
 
 /* ---- inspection (tests) ------------------------------------------------------------------- */
 

@@ -2,8 +2,8 @@
 // state, the per-visit op sequence of the reference's Engine, and one captured hipGraph
 // per pass shape (forward M=1/M=2 with 0..2 logit rows and optional checkpoint, MTP head
 // M=1/M=2 with or without a draft).  Mirrors src/engine.rs (op graph :383-493, MTP
-// :495-580 and :713-774, forward_mm :801-936, rollback/snapshot/restore/reset :646-697)
-// and the greedy loop of src/worker.rs:123-255.
+// :495-580 and :713-774, forward_mm :801-936, rollback/snapshot/restore/reset :646-697).
+// The worker's decode loop and prefix cache over these entry points are in worker.cpp.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -33,7 +33,7 @@ int device_error(hipError_t e, const char* what) {
 
 namespace {
 
-constexpr int kSnapshots = 4;
+constexpr int kSnapshots = SNL_SNAPSHOTS;
 constexpr int kLogitRows = 2;
 // Token rows per captured pass.  The kernels take up to SNL_MAX_M; passes use 1 or 2.
 constexpr int kMaxM = 2;
@@ -163,6 +163,9 @@ struct snl_engine {
 
     int cur = 0, ck_slot = -1;
     int pos = 0, hid_rows = 0;
+    // Counts the calls that change the caches, the recurrent state or a snapshot slot, so that a
+    // holder of cache bookkeeping (the worker) can tell whether someone else has moved the engine.
+    uint64_t epoch = 0;
     std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
     std::string err;
 
@@ -906,6 +909,7 @@ int snl_prefill_chunk(const snl_engine* e) {
 int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows, int ckpt,
                 float* logits_out, snl_pick* picks_out) {
     if (!e) return SNL_EARG;
+    ++e->epoch;
     e->err.clear();
     // src/engine.rs:810-821
     if (logit_rows < 0 || logit_rows > kLogitRows || (ckpt && n != 2))
@@ -960,6 +964,7 @@ int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uin
                          int ckpt, snl_op_time* recs, int max_recs, int* n_recs) {
     if (!e || !recs || !n_recs) return SNL_EARG;
     e->err.clear();
+    ++e->epoch;
     *n_recs = 0;
     if (logit_rows < 0 || logit_rows > kLogitRows || (ckpt && n != 2) || n <= 0 || n > kMaxM || !tokens)
         return e->fail(SNL_EARG, "forward_profiled: one pass of 1..%d tokens", kMaxM);
@@ -1012,6 +1017,7 @@ int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch
                 int* launches_per_pass) {
     if (!e || !name || reps < 1 || !ms_per_launch) return SNL_EARG;
     e->err.clear();
+    ++e->epoch;
     if (!strcmp(name, "copy")) return e->fail(SNL_EARG, "time_op: 'copy' moves the carried hidden row");
     if (e->pos + 2 > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + 2, e->ctx);
     // a verify pass (2 rows, checkpoint) at the current position; nothing is committed
@@ -1057,6 +1063,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
             uint32_t* draft_out, snl_pick* pick_out, float* logits_out) {
     if (!e) return SNL_EARG;
     e->err.clear();
+    ++e->epoch;
     if (!e->cfg.has_mtp) return e->fail(SNL_ESTATE, "this model has no MTP head");
     if (n <= 0 || !tokens || !pos3 || r0 < 0 || r0 + n > e->hid_rows + 1 || slot0 < 0 || slot0 + n > e->ctx)
         return e->fail(SNL_EARG, "mtp: rows out of range");
@@ -1093,6 +1100,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
 int snl_rollback(snl_engine* e) {
     if (!e) return SNL_EARG;
     if (e->ck_slot < 0) return e->fail(SNL_ESTATE, "rollback without a checkpointed 2-token step");
+    ++e->epoch;
     e->cur = e->ck_slot;
     e->ck_slot = -1;
     if (launch_copy(e->hlast, e->hid + e->h, e->h, e->stream) || hipStreamSynchronize(e->stream) != hipSuccess)
@@ -1104,6 +1112,7 @@ int snl_rollback(snl_engine* e) {
 
 int snl_snapshot(snl_engine* e, int slot) {
     if (!e || slot < 0 || slot >= kSnapshots) return SNL_EARG;
+    ++e->epoch;
     const size_t nl = std::max(e->n_lin, 1);
     const size_t sb = nl * e->state_floats * 4, cb = nl * e->conv_floats * 4;
     if (hipMemcpyAsync(e->snap_lin[slot], e->lin_state + (size_t)e->cur * nl * e->state_floats, sb,
@@ -1119,6 +1128,7 @@ int snl_snapshot(snl_engine* e, int slot) {
 
 int snl_restore(snl_engine* e, int slot, int pos) {
     if (!e || slot < 0 || slot >= kSnapshots || pos < 0 || pos > e->ctx) return SNL_EARG;
+    ++e->epoch;
     const size_t nl = std::max(e->n_lin, 1);
     const size_t sb = nl * e->state_floats * 4, cb = nl * e->conv_floats * 4;
     if (hipMemcpyAsync(e->lin_state + (size_t)e->cur * nl * e->state_floats, e->snap_lin[slot], sb,
@@ -1137,6 +1147,7 @@ int snl_restore(snl_engine* e, int slot, int pos) {
 
 int snl_reset(snl_engine* e) {
     if (!e) return SNL_EARG;
+    ++e->epoch;
     const size_t nl = std::max(e->n_lin, 1);
     if (hipMemsetAsync(e->lin_state + (size_t)e->cur * nl * e->state_floats, 0, nl * e->state_floats * 4,
                        e->stream) != hipSuccess ||
@@ -1153,183 +1164,15 @@ int snl_reset(snl_engine* e) {
 
 }  // extern "C"
 
-// Host-side state of the greedy MTP loop of Worker::run (src/worker.rs:182-255).
-struct snl_decoder {
-    snl_engine* e = nullptr;
-    bool spec = false;
-    uint32_t tok = 0;  // sampled, not yet emitted
-    float gap = 0.0f;
-    uint32_t rope = 0;
-    int mr0 = 0, mn = 1, mslot = 0;  // MTP input: (r0, tokens, positions, first cache slot)
-    uint32_t mtok[2] = {0, 0};
-    uint32_t mpos[6] = {0, 0, 0, 0, 0, 0};
-    snl_gen_stats st{};
-};
+namespace snl {
+
+uint64_t engine_epoch(const snl_engine* e) { return e->epoch; }
+
+int engine_fail(snl_engine* e, int code, const char* msg) { return e->fail(code, "%s", msg); }
+
+}  // namespace snl
 
 extern "C" {
-
-int snl_decoder_create(snl_engine* e, const uint32_t* prompt, int n, int spec, snl_decoder** out) {
-    using clk = std::chrono::steady_clock;
-    if (!e || !prompt || !out) return SNL_EARG;
-    *out = nullptr;
-    if (n <= 0) return e->fail(SNL_EARG, "empty prompt");
-    if (n >= e->ctx) return e->fail(SNL_EARG, "prompt is %d tokens but the context size is %d", n, e->ctx);
-    int rc = snl_reset(e);
-    if (rc) return rc;
-    auto d = new snl_decoder();
-    d->e = e;
-    d->spec = spec && e->cfg.has_mtp;
-    auto t0 = clk::now();
-    std::vector<uint32_t> pos3((size_t)n * 3);
-    for (int i = 0; i < n; ++i) pos3[i * 3] = pos3[i * 3 + 1] = pos3[i * 3 + 2] = (uint32_t)i;
-    snl_pick picks[2];
-    const int chunk = snl_prefill_chunk(e);
-    // Worker::feed (src/worker.rs:291-323): forward a chunk, then catch the MTP cache up
-    for (int c0 = 0; c0 < n; c0 += chunk) {
-        const int c1 = std::min(c0 + chunk, n);
-        rc = snl_forward(e, prompt + c0, c1 - c0, pos3.data() + c0 * 3, c1 == n ? 1 : 0, 0, nullptr, picks);
-        const int r0 = c0 == 0;
-        if (!rc && d->spec && r0 < c1 - c0)
-            rc = snl_mtp(e, r0, prompt + c0 + r0, c1 - c0 - r0, pos3.data() + (c0 + r0 - 1) * 3, c0 + r0 - 1, 0,
-                         nullptr, nullptr, nullptr);
-        if (rc) {
-            delete d;
-            return rc;
-        }
-    }
-    d->st.prefill_s = std::chrono::duration<double>(clk::now() - t0).count();
-    d->rope = (uint32_t)n;
-    d->tok = picks[0].token;
-    d->gap = picks[0].top1 - picks[0].top2;
-    d->mr0 = e->hid_rows;
-    d->mn = 1;
-    d->mslot = n - 1;
-    d->mtok[0] = d->tok;
-    for (int k = 0; k < 3; ++k) d->mpos[k] = (uint32_t)(n - 1);
-    *out = d;
-    return SNL_OK;
-}
-
-void snl_decoder_destroy(snl_decoder* d) { delete d; }
-
-int snl_decoder_stats(const snl_decoder* d, snl_gen_stats* out) {
-    if (!d || !out) return SNL_EARG;
-    *out = d->st;
-    return SNL_OK;
-}
-
-int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out) {
-    using clk = std::chrono::steady_clock;
-    if (!d || !out || !n_out) return SNL_EARG;
-    snl_engine* e = d->e;
-    *n_out = 0;
-    auto ts = clk::now();
-    int rc;
-    // emit the pending token (Emit::push, src/worker.rs:346-381)
-    out[0] = d->tok;
-    if (gaps) gaps[0] = d->gap;
-    *n_out = 1;
-    d->st.generated++;
-    snl_pick picks[2];
-    if (!d->spec) {
-        uint32_t p1[3] = {d->rope, d->rope, d->rope};
-        if ((rc = snl_forward(e, &d->tok, 1, p1, 1, 0, nullptr, picks))) return rc;
-        d->rope += 1;
-        d->tok = picks[0].token;
-        d->gap = picks[0].top1 - picks[0].top2;
-        d->st.decode_s += std::chrono::duration<double>(clk::now() - ts).count();
-        return SNL_OK;
-    }
-    uint32_t draft = 0;
-    if ((rc = snl_mtp(e, d->mr0, d->mtok, d->mn, d->mpos, d->mslot, 1, &draft, nullptr, nullptr))) return rc;
-    auto tb = clk::now();
-    const int slot = e->pos;
-    const uint32_t rope = d->rope;
-    uint32_t pair[2] = {d->tok, draft};
-    uint32_t p2[6] = {rope, rope, rope, rope + 1, rope + 1, rope + 1};
-    if ((rc = snl_forward(e, pair, 2, p2, 2, 1, nullptr, picks))) return rc;
-    auto tc = clk::now();
-    d->st.draft_s += std::chrono::duration<double>(tb - ts).count();
-    d->st.verify_s += std::chrono::duration<double>(tc - tb).count();
-    d->st.drafted++;
-    // Sampler::verify, greedy (src/sampler.rs:63-66, :87-89)
-    const uint32_t next = picks[0].token;
-    if (next == draft) {
-        d->st.accepted++;
-        d->st.generated++;
-        out[1] = draft;
-        if (gaps) gaps[1] = picks[0].top1 - picks[0].top2;
-        *n_out = 2;
-        d->tok = picks[1].token;
-        d->gap = picks[1].top1 - picks[1].top2;
-        d->mr0 = 1;
-        d->mn = 2;
-        d->mtok[0] = draft;
-        d->mtok[1] = d->tok;
-        for (int k = 0; k < 3; ++k) {
-            d->mpos[k] = rope;
-            d->mpos[3 + k] = rope + 1;
-        }
-        d->rope = rope + 2;
-    } else {
-        if ((rc = snl_rollback(e))) return rc;
-        d->tok = next;
-        d->gap = picks[0].top1 - picks[0].top2;
-        d->mr0 = 1;
-        d->mn = 1;
-        d->mtok[0] = d->tok;
-        for (int k = 0; k < 3; ++k) d->mpos[k] = rope;
-        d->rope = rope + 1;
-    }
-    d->mslot = slot;
-    d->st.decode_s += std::chrono::duration<double>(clk::now() - ts).count();
-    return SNL_OK;
-}
-
-int snl_generate(snl_engine* e, const uint32_t* prompt, int n, int max_tokens, int spec, uint32_t* out, float* gaps,
-                 snl_gen_stats* stats) {
-    if (!e || !prompt || !out) return SNL_EARG;
-    if (n > 0 && max_tokens > e->ctx - n) max_tokens = e->ctx - n;
-    if (max_tokens <= 0) return e->fail(SNL_EARG, "max_tokens must be positive");
-    snl_decoder* d = nullptr;
-    int rc = snl_decoder_create(e, prompt, n, spec, &d);
-    if (rc) return rc;
-    auto is_eos = [&](uint32_t t) {
-        for (int k = 0; k < e->cfg.n_eos; ++k)
-            if (e->cfg.eos[k] == t) return true;
-        return false;
-    };
-    int generated = 0;
-    bool done = false;
-    while (!done) {
-        // A step emits the pending token and, after an accepted draft, the draft.  The
-        // reference stops before feeding a token that ends generation; so does this loop:
-        // the last step's extra work on a token past the limit is not observable.
-        if (generated + 1 >= max_tokens || is_eos(d->tok)) {
-            out[generated] = d->tok;
-            if (gaps) gaps[generated] = d->gap;
-            generated++;
-            d->st.generated++;
-            break;
-        }
-        uint32_t o[2];
-        float g[2];
-        int k = 0;
-        if ((rc = snl_decoder_step(d, o, g, &k))) break;
-        for (int i = 0; i < k && !done; ++i) {
-            out[generated] = o[i];
-            if (gaps) gaps[generated] = g[i];
-            generated++;
-            if (is_eos(o[i]) || generated >= max_tokens) done = true;
-        }
-    }
-    if (stats) {
-        *stats = d->st;
-        stats->generated = generated;
-    }
-    snl_decoder_destroy(d);
-    return rc;
-}
 
 // ---- inspection ----
 static const void* find_tensor(const snl_engine* e, int layer, int kind, int* type, int* rows, int* cols,

@@ -40,6 +40,16 @@ class GenStats(ctypes.Structure):
                 ("draft_s", ctypes.c_double), ("verify_s", ctypes.c_double)]
 
 
+class Finish(ctypes.Structure):
+    _fields_ = [("reason", ctypes.c_int32), ("prompt_tokens", ctypes.c_int32),
+                ("completion_tokens", ctypes.c_int32), ("cached_tokens", ctypes.c_int32),
+                ("drafted", ctypes.c_int32), ("accepted", ctypes.c_int32), ("prefill_s", ctypes.c_double),
+                ("decode_s", ctypes.c_double)]
+
+
+SNAPSHOTS = 4
+
+
 class OpTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 24), ("bytes", ctypes.c_double), ("ms", ctypes.c_double)]
 
@@ -86,6 +96,11 @@ def lib() -> ctypes.CDLL:
         L.snl_decoder_step.argtypes = [vp, u32p, f32p, i32p]
         L.snl_decoder_stats.argtypes = [vp, ctypes.POINTER(GenStats)]
         L.snl_decoder_destroy.argtypes = [vp]
+        L.snl_worker_create.argtypes = [vp, ctypes.c_int, ctypes.POINTER(vp)]
+        L.snl_worker_destroy.argtypes = [vp]
+        L.snl_worker_run.argtypes = [vp, u32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, u32p, f32p,
+                                     ctypes.POINTER(Finish)]
+        L.snl_worker_cache.argtypes = [vp, i32p, i32p, ctypes.POINTER(ctypes.c_uint64)]
         L.snl_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.c_int, i32p, i32p]
         L.snl_tensor_read.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, f32p]
         L.snl_buffer_read.argtypes = [vp, ctypes.c_int, vp, ctypes.c_size_t]
@@ -303,6 +318,51 @@ class Decoder:
     def close(self):
         if getattr(self, "h", None):
             lib().snl_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Worker:
+    """The generation worker with its prefix cache (src/worker.rs:57-272) over one engine."""
+
+    def __init__(self, engine: Engine, self_pause: bool = True):
+        self.engine = engine
+        h = vp()
+        engine._check(lib().snl_worker_create(engine.h, int(self_pause), ctypes.byref(h)))
+        self.h = h
+
+    def run(self, prompt: Sequence[int], max_tokens: int, snapshot_at: Optional[int] = None, spec: bool = True):
+        """One request (Worker::run, greedy); returns the tokens, their top-2 margins and the Finish fields."""
+        p = _u32(prompt)
+        cap = max(1, max_tokens)
+        out = np.zeros(cap, np.uint32)
+        gaps = np.zeros(cap, np.float32)
+        fin = Finish()
+        rc = lib().snl_worker_run(self.h, _ptr(p, u32p), len(p), -1 if snapshot_at is None else snapshot_at,
+                                  max_tokens, int(spec), _ptr(out, u32p), _ptr(gaps, f32p), ctypes.byref(fin))
+        self.engine._check(rc)
+        n = fin.completion_tokens
+        res = {f: getattr(fin, f) for f, _ in Finish._fields_}
+        res["reason"] = "stop" if fin.reason == 1 else "length"
+        res.update(tokens=out[:n].tolist(), gaps=gaps[:n])
+        return res
+
+    def cache(self):
+        """(live length, per-slot key counts with -1 for empty, per-slot last use)."""
+        live = ctypes.c_int32()
+        lens = (ctypes.c_int32 * SNAPSHOTS)()
+        used = (ctypes.c_uint64 * SNAPSHOTS)()
+        self.engine._check(lib().snl_worker_cache(self.h, ctypes.byref(live), lens, used))
+        return live.value, list(lens), list(used)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().snl_worker_destroy(self.h)
             self.h = None
 
     def __del__(self):
