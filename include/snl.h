@@ -222,6 +222,15 @@ size_t snl_buffer_size(const snl_engine* e, int id);
 int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K,
              int x_stride, int y_stride, void* stream);
 
+/* The prefill GEMM (src/shaders/matmul.wgsl:200-318, MatKind::Tiled): y[m*y_stride + n] =
+ * sum_k x[m*x_stride + k] * W[n, k] for M in 1..SNL_PREFILL_M token rows, K % 128 == 0, W in
+ * the reference layout as for snl_gemv.  The call packs W into the GEMM's panel order and the
+ * rows into f16 hi/lo fragments in staging buffers the library keeps, and returns after the
+ * product has finished on `stream`. */
+#define SNL_PREFILL_M 512
+int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K,
+             int x_stride, int y_stride, void* stream);
+
 /* One Gated DeltaNet step over M = 1..4 tokens (linear.wgsl conv + delta).  conv_state and
  * state hold three slots each ([3][3, conv_dim] and [3][n_v, 128, 128]); the call reads
  * slot s_in, writes slot s_out and, if ckpt > 0, the state after token ckpt-1 to slot s_ck. */

@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsnl.so")
 BUILD = os.path.join(os.path.dirname(HERE), "_build")
-SOURCES = ["gemv.hip", "mgemv.hip", "gemv_ksplit.hip", "layers.hip", "deltanet.hip", "attention.hip", "init.hip", "engine.cpp",
+SOURCES = ["gemv.hip", "mgemv.hip", "mgemm.hip", "gemv_ksplit.hip", "layers.hip", "deltanet.hip", "attention.hip", "attention_prefill.hip", "prefill.hip", "init.hip", "engine.cpp",
            "snl_file.cpp", "worker.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

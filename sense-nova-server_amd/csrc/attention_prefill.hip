@@ -1,0 +1,246 @@
+// Gated GQA attention over a prefill chunk (src/shaders/attention.wgsl: prep :59-127, attend
+// :129-246, combine :248-269), on the matrix cores.
+//
+// prep: block (slot, token) as in the decode kernel: RMSNorm (1 + w) of each q / k head, partial
+// rotate-half RoPE at the token's rotary position, q rows to qbuf (f32), k / v rows into the f16
+// cache at the token's cache position.
+//
+// attend: block (kv head, 16 queries), wave w = query head 4*kv + w of the GQA group; the block
+// streams the keys [0, last query's position] in steps of 32 through LDS (K rows, and V
+// transposed so that each MFMA A fragment is two 8-byte reads), shared by the group's 4 heads.
+//   scores  S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (exact f16),
+//           B = the query's dims split into f16 hi + lo under a per-query power of two, so the
+//           f32 score carries the decode kernel's precision; lane (query j, group g) ends with
+//           keys 4g..4g+3 of each 16-key half;
+//   softmax online per query (running max, rescaled partial sums), keys past the query's own
+//           position weigh 0;
+//   values  O^T += V^T P^T: B = the lane's own 8 probabilities as f16 hi + lo (keys 4g..4g+3 and
+//           16+4g..16+4g+3, the same order in the V^T fragment), A = 16 dims x those keys.
+// The output is divided by the softmax sum and multiplied by the sigmoid gate, as in combine.
+#include <float.h>
+#include <hip/hip_fp16.h>
+
+#include "common.h"
+#include "kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace snl {
+
+namespace {
+
+constexpr int HD = 256, G = 4;
+constexpr int QTILE = 16, KB = 32;
+constexpr int KROW = HD + 8;  // K tile row (halfs): 528 bytes keeps the 16 rows of a read on distinct banks
+constexpr int VROW = KB + 4;  // V^T row (halfs): 72 bytes
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void pf_prep_kernel(AttnArgs a, const PrefillDev* st) {
+    __shared__ float sh[HD];
+    __shared__ float red[4];
+    const int slot = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+    const int pos = st->pos0 + m;
+    const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
+    const float* row = a.proj + (size_t)m * a.proj_stride;
+    if (slot >= a.n_heads + a.n_kv) {
+        const int kh = slot - a.n_heads - a.n_kv;
+        const float v = row[2 * q_dim + kv_dim + kh * HD + d];
+        a.vcache[(size_t)pos * kv_dim + kh * HD + d] = __half_as_ushort(__float2half_rn(v));
+        return;
+    }
+    const bool is_q = slot < a.n_heads;
+    float v = is_q ? row[slot * 2 * HD + d] : row[2 * q_dim + (slot - a.n_heads) * HD + d];
+    const float total = block_sum<256>(v * v, red);
+    v = (v * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + a.norms[(is_q ? 0 : HD) + d]);
+    sh[d] = v;
+    __syncthreads();
+    const int half = a.rot_dim / 2;
+    if (d < a.rot_dim) {
+        const int fi = d % half;
+        const float inv_freq = powf(a.rope_theta, -(float)(2 * fi) / (float)a.rot_dim);
+        const uint32_t* rp = st->rpos[m];
+        uint32_t rot_pos = rp[0];
+        if (fi % 3 == 1 && (uint32_t)fi < (a.mrope >> 16)) rot_pos = rp[1];
+        else if (fi % 3 == 2 && (uint32_t)fi < (a.mrope & 0xFFFFu)) rot_pos = rp[2];
+        const float ang = (float)rot_pos * inv_freq;
+        const float cs = cosf(ang), sn = sinf(ang);
+        v = d < half ? sh[d] * cs - sh[d + half] * sn : sh[d] * cs + sh[d - half] * sn;
+    }
+    if (is_q) {
+        a.qbuf[(size_t)m * q_dim + slot * HD + d] = v;
+    } else {
+        const int kh = slot - a.n_heads;
+        a.kcache[(size_t)pos * kv_dim + kh * HD + d] = __half_as_ushort(__float2half_rn(v));
+    }
+}
+
+__global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const PrefillDev* st, int M) {
+    __shared__ __align__(16) _Float16 ks[KB * KROW];
+    __shared__ __align__(16) _Float16 vt[HD * VROW];
+    const int kh = blockIdx.x, q0 = blockIdx.y * QTILE;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int hh = kh * G + w;
+    const int pos0 = st->pos0;
+    const int qn = min(QTILE, M - q0);
+    const int kend = pos0 + q0 + qn;  // keys of the block's last query
+    const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
+    const int j = lane & 15, g = lane >> 4;
+    const int mq = q0 + j;
+    const bool qvalid = j < qn;
+    const int qlim = pos0 + mq;  // the last key this lane's query sees
+
+    // ---- the query as B fragments (dims 32s + 8g + i), hi + lo under a power of two ----
+    float qv[8][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const float4* qp = reinterpret_cast<const float4*>(a.qbuf + (size_t)(qvalid ? mq : q0) * q_dim + hh * HD + 32 * s + 8 * g);
+        const float4 u0 = qp[0], u1 = qp[1];
+        qv[s][0] = u0.x, qv[s][1] = u0.y, qv[s][2] = u0.z, qv[s][3] = u0.w;
+        qv[s][4] = u1.x, qv[s][5] = u1.y, qv[s][6] = u1.z, qv[s][7] = u1.w;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            if (!qvalid) qv[s][i] = 0.0f;
+            amax = fmaxf(amax, fabsf(qv[s][i]));
+        }
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const int e = amax > 0.0f ? max(ilogbf(amax) - 14, -110) : 0;
+    const float down = ldexpf(1.0f, -e), up = ldexpf(1.0f, e) * a.scale;
+    half8_t qh[8], ql[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float v = qv[s][i] * down;
+            const _Float16 hv = (_Float16)v;
+            qh[s][i] = hv;
+            ql[s][i] = (_Float16)(v - (float)hv);
+        }
+
+    f32x4_t o[16];
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float mrun = -1e30f, lpart = 0.0f;
+    const uint16_t* kc = a.kcache + kh * HD;
+    const uint16_t* vc = a.vcache + kh * HD;
+
+    for (int kb = 0; kb < kend; kb += KB) {
+        __syncthreads();  // the previous step's tiles are consumed
+        {   // K rows: thread (key t >> 3, 32 dims)
+            const int key = tid >> 3, part = tid & 7;
+            const int kk = kb + key;
+            uint4 r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (kk < kend) {
+                const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)kk * kv_dim + part * 32);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r[i] = src[i];
+            }
+            uint4* dst = reinterpret_cast<uint4*>(ks + key * KROW + part * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = r[i];
+        }
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {  // V transposed: item (key pair, 8 dims)
+            const int item = tid + 256 * it;
+            const int kp = item >> 5, dg = item & 31;
+            const int k0 = kb + 2 * kp;
+            uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = make_uint4(0u, 0u, 0u, 0u);
+            if (k0 < kend) v0 = *reinterpret_cast<const uint4*>(vc + (size_t)k0 * kv_dim + dg * 8);
+            if (k0 + 1 < kend) v1 = *reinterpret_cast<const uint4*>(vc + (size_t)(k0 + 1) * kv_dim + dg * 8);
+            const uint32_t a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t lo = (a0[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+                const uint32_t hi = (a1[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+                *reinterpret_cast<uint32_t*>(vt + (dg * 8 + i) * VROW + 2 * kp) = lo | (hi << 16);
+            }
+        }
+        __syncthreads();
+
+        // ---- scores: two 16-key halves ----
+        f32x4_t sc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const half8_t kf = *reinterpret_cast<const half8_t*>(ks + (16 * kt + j) * KROW + 32 * s + 8 * g);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[s], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[s], c, 0, 0, 0);
+            }
+            sc[kt] = c;
+        }
+        // ---- online softmax for this lane's query ----
+        float val[8];
+        bool ok[8];
+        float bmax = -1e30f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kk = kb + 16 * kt + 4 * g + r;
+                const int i = 4 * kt + r;
+                ok[i] = qvalid && kk <= qlim;
+                val[i] = sc[kt][r] * up;
+                if (ok[i]) bmax = fmaxf(bmax, val[i]);
+            }
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        const float mnew = fmaxf(mrun, bmax);
+        const float factor = expf(mrun - mnew);
+        half8_t ph, pl;
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float p = ok[i] ? expf(val[i] - mnew) : 0.0f;
+            psum = psum + p;
+            const _Float16 hv = (_Float16)p;
+            ph[i] = hv;
+            pl[i] = (_Float16)(p - (float)hv);
+        }
+        lpart = lpart * factor + psum;
+        mrun = mnew;
+        // ---- values ----
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt) {
+            o[dt] = o[dt] * factor;
+            const _Float16* vr = vt + (16 * dt + j) * VROW;
+            const half4_t va = *reinterpret_cast<const half4_t*>(vr + 4 * g);
+            const half4_t vb = *reinterpret_cast<const half4_t*>(vr + 16 + 4 * g);
+            const half8_t vf = half8_t{va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[dt], 0, 0, 0);
+        }
+    }
+    // ---- normalise, gate, store: lane (query j) holds dims 16dt + 4g + r ----
+    float l = lpart + __shfl_xor(lpart, 16, 64);
+    l = l + __shfl_xor(l, 32, 64);
+    if (!qvalid) return;
+    const float* grow = a.proj + (size_t)mq * a.proj_stride + hh * 2 * HD + HD;
+    float* orow = a.out + (size_t)mq * q_dim + hh * HD;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int d = 16 * dt + 4 * g + r;
+            orow[d] = o[dt][r] / l / (1.0f + expf(-grow[d]));
+        }
+}
+
+}  // namespace
+
+int launch_attention_prefill(const AttnArgs& a, const PrefillDev* pstep, int M, hipStream_t s) {
+    if (M < 1 || M > SNL_PF_M || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2 || !pstep) return -1;
+    hipLaunchKernelGGL(pf_prep_kernel, dim3(a.n_heads + 2 * a.n_kv, M), dim3(256), 0, s, a, pstep);
+    hipLaunchKernelGGL(pf_attend_kernel, dim3(a.n_kv, (M + QTILE - 1) / QTILE), dim3(256), 0, s, a, pstep, M);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // namespace snl

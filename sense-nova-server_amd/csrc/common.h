@@ -34,6 +34,16 @@ struct StepDev {
     uint32_t rpos[SNL_MAX_M][4];  // rotary (t, h, w, 0) position of each row
 };
 
+// Token rows of one prefill pass (chunked prefill and the MTP head's catch-up over a prompt).
+#define SNL_PF_M 512
+struct PrefillDev {
+    int32_t pos0;   // cache position of row 0
+    int32_t m;      // rows
+    int32_t _pad[2];
+    uint32_t tokens[SNL_PF_M];
+    uint32_t rpos[SNL_PF_M][4];  // rotary (t, h, w, 0) position of each row
+};
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SNL_WAVE);

@@ -102,6 +102,8 @@ struct QW {
     int rows = 0, cols = 0, quant = 0;
     bool packed = false;  // tile order (packing.h); otherwise the reference's row-major layout
     int inter = 0;        // packed with SwiGLU pairing of gate/up rows when > 0
+    void* pq = nullptr;   // panel order for the prefill GEMM (mgemm.hip), rows in reference order
+    float* ps = nullptr;
 };
 
 struct Vec {
@@ -152,6 +154,14 @@ struct snl_engine {
     float *coef = nullptr, *mhc_raw = nullptr, *mhc_part = nullptr, *partial = nullptr, *logits = nullptr, *hid = nullptr,
           *hlast = nullptr;
     float *mx = nullptr, *hn = nullptr, *m_logits = nullptr;
+    // chunked prefill: up to SNL_PF_M rows per pass, launched eagerly (prefill.hip, mgemm.hip,
+    // attention_prefill.hip)
+    float *pf_x = nullptr, *pf_proj = nullptr, *pf_act = nullptr, *pf_attn = nullptr, *pf_qbuf = nullptr,
+          *pf_br = nullptr, *pf_xs = nullptr, *pf_part = nullptr, *pf_coef = nullptr, *pf_ssq = nullptr;
+    float *pf_dq = nullptr, *pf_dk = nullptr, *pf_dv = nullptr, *pf_gz = nullptr, *pf_beta = nullptr,
+          *pf_decay = nullptr;
+    void* pf_frags = nullptr;
+    PrefillDev *d_pstep = nullptr, *h_pstep = nullptr;  // h_pstep: pinned
     uint16_t *kcache = nullptr, *vcache = nullptr, *m_kc = nullptr, *m_vc = nullptr;
     float *lin_state = nullptr, *conv_state = nullptr;
     size_t state_floats = 0, conv_floats = 0;  // per visit
@@ -234,9 +244,10 @@ struct snl_engine {
     }
 
     // Draw a rows x cols quantised matrix (reference layout, src/weights.rs:48-55).  GEMV matrices
-    // (pack_inter >= 0) are then stored in tile order; pack_inter > 0 pairs gate and up rows.
+    // (pack_inter >= 0) are then stored in tile order; pack_inter > 0 pairs gate and up rows; with
+    // `panel` a second copy in the prefill GEMM's panel order is kept.
     // With a weight file the matrix is read from it instead (its own dtype; the shape must match).
-    int gen_q(QW& w, int layer, int kind, int rows, int cols, int qt, int pack_inter = 0) {
+    int gen_q(QW& w, int layer, int kind, int rows, int cols, int qt, int pack_inter = 0, bool panel = true) {
         const SnlFile* f = layer == kMtpLayer ? msrc : src;
         const FileTensor* ft = nullptr;
         if (f) {
@@ -291,6 +302,14 @@ struct snl_engine {
         w.inter = pack_inter;
         if (fill(gen_tmp_q, gen_tmp_s) || launch_pack_matrix(g, gen_tmp_q, gen_tmp_s, w.q, w.s, stream))
             return fail(SNL_EDEVICE, "weight init failed");
+        if (panel) {
+            uint8_t* pq;
+            if ((rc = dalloc(&pq, gemm_q_bytes(qt, rows, cols))) || (rc = dalloc(&w.ps, gemm_s_floats(rows, cols))))
+                return rc;
+            w.pq = pq;
+            if (launch_panel_pack(qt, rows, cols, gen_tmp_q, gen_tmp_s, w.pq, w.ps, stream))
+                return fail(SNL_EDEVICE, "weight init failed");
+        }
         return SNL_OK;
     }
 
@@ -327,6 +346,54 @@ struct snl_engine {
     int init();
     int record_forward(int M, int rows, int ckpt);
     int record_mtp(int M, int draft);
+    int record_prefill(int M, int rows);
+    int record_mtp_prefill(int M, int r0);
+    int prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int m, int cache_pos0, int rows, bool mtp, int r0);
+    const uint32_t* pf_tokens() const {
+        return reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(d_pstep) + offsetof(PrefillDev, tokens));
+    }
+    // token rows -> GEMM fragments (the branch input on the way) -> panel GEMM
+    int pf_mat(const char* name, const QW& w, const float* xin, int x_stride, int M, int mode, const float* nw,
+               float* y, int y_stride) {
+        int rc = 0;
+        if (op("rows", 0.0)) {
+            RowsArgs r{};
+            r.x = xin;
+            r.x_stride = x_stride;
+            r.M = M;
+            r.K = w.cols;
+            r.mode = mode;
+            r.w = nw;
+            r.coef = pf_coef;
+            r.h = h;
+            r.ssq = pf_ssq;
+            r.eps = cfg.eps;
+            r.perm4 = w.quant;
+            r.frags = pf_frags;
+            r.xs = pf_xs;
+            rc |= launch_rows_to_frags(r, stream);
+        }
+        if (op(name, 0.0)) {
+            GemmArgs g{};
+            g.wq = w.pq;
+            g.ws = w.ps;
+            g.frags = pf_frags;
+            g.xs = pf_xs;
+            g.y = y;
+            g.y_stride = y_stride;
+            g.M = M;
+            g.N = w.rows;
+            g.K = w.cols;
+            rc |= launch_mgemm(g, w.quant, stream);
+        }
+        return rc;
+    }
+    // an mHC site over prefill rows: router sums, then the token coefficients in pf_coef
+    int pf_site(const float* w, int M) {
+        if (!op("mhc", 0.0)) return 0;
+        return launch_mhc(pf_x, w, pf_part, h, M, stream) |
+               launch_mhc_coef(pf_part, w, h, cfg.mhc_iterations, pf_coef, M, stream);
+    }
     int run(int kind, int M, int a, int b);
     static constexpr int kPartBlocks = 4096;  // partial-sum slots of mhc_part per token
     int part_n = 0;                           // partials currently in mhc_part (0: none)
@@ -459,7 +526,7 @@ int snl_engine::init() {
     if (gemv_init()) return fail(SNL_EDEVICE, "GEMV LDS configuration failed");
     int rc;
     // ---- weights (convert.rs:228-311 layout; seeded values) ----
-    if ((rc = gen_q(lm_head, -1, K_LM_HEAD, c.vocab, h, 0))) return rc;
+    if ((rc = gen_q(lm_head, -1, K_LM_HEAD, c.vocab, h, 0, 0, false))) return rc;
     if ((rc = gen_q(embed, -1, K_EMBED, c.vocab, h, 0, -1))) return rc;  // gathered by row
     if ((rc = gen_v(final_norm, -1, K_NORM, h, 0, 0.1f))) return rc;
     layers.resize(c.n_layers);
@@ -515,12 +582,31 @@ int snl_engine::init() {
         (rc = dalloc(&dn_ssq, (size_t)M * std::max(c.lin_v_heads, 1) * kDeltaGroups)) ||
         (rc = dalloc(&mhc_part, (size_t)kPartBlocks * M * 9)) ||
         (rc = dalloc(&partial, (size_t)M * c.n_heads * parts_max * (c.head_dim + 2))) ||
-        (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)(M + 1) * h)) ||
+        (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)(SNL_PF_M + 1) * h)) ||
         (rc = dalloc(&hlast, (size_t)h)) || (rc = dalloc(&mx, (size_t)M * 2 * h)) ||
         (rc = dalloc(&hn, (size_t)M * h)) || (rc = dalloc(&m_logits, (size_t)c.vocab)) ||
         (rc = dalloc(&pick_scratch, pick_scratch_floats(c.vocab, kLogitRows))) || (rc = dalloc(&d_picks, 2)) ||
         (rc = dalloc(&d_mpick, 1)) || (rc = dalloc(&d_step, 1)) || (rc = dalloc(&d_mstep, 1)))
         return rc;
+    // ---- chunked prefill rows ----
+    {
+        const size_t P = SNL_PF_M;
+        const int kmax = std::max(std::max(h, c.intermediate), std::max(q_dim, lin_value_dim));
+        const int nv = std::max(c.lin_v_heads, 1);
+        const size_t key_dim = (size_t)c.lin_k_heads * c.lin_k_dim;
+        if ((rc = dalloc(&pf_x, P * 2 * h)) || (rc = dalloc(&pf_proj, P * proj_w)) ||
+            (rc = dalloc(&pf_act, P * c.intermediate)) || (rc = dalloc(&pf_attn, P * attn_w)) ||
+            (rc = dalloc(&pf_qbuf, P * q_dim)) || (rc = dalloc(&pf_br, P * h)) || (rc = dalloc(&pf_xs, P)) ||
+            (rc = dalloc(&pf_part, P * 9)) || (rc = dalloc(&pf_coef, P * 8)) ||
+            (rc = dalloc(&pf_ssq, P * nv * kDeltaGroups)) || (rc = dalloc(&pf_dq, P * std::max<size_t>(key_dim, 1))) ||
+            (rc = dalloc(&pf_dk, P * std::max<size_t>(key_dim, 1))) || (rc = dalloc(&pf_dv, P * lin_value_dim + 1)) ||
+            (rc = dalloc(&pf_gz, P * lin_value_dim + 1)) || (rc = dalloc(&pf_beta, P * nv)) ||
+            (rc = dalloc(&pf_decay, P * nv)) || (rc = dalloc((uint8_t**)&pf_frags, frags_bytes(SNL_PF_M, kmax))) ||
+            (rc = dalloc(&d_pstep, 1)))
+            return rc;
+        if (hipHostMalloc((void**)&h_pstep, sizeof(PrefillDev), hipHostMallocDefault) != hipSuccess)
+            return fail(SNL_ENOMEM, "pinned host allocation failed");
+    }
     // ---- caches and recurrent state ----
     const size_t kvn = (size_t)ctx * kv_dim;
     if ((rc = dalloc(&kcache, kvn * std::max(n_full, 1))) || (rc = dalloc(&vcache, kvn * std::max(n_full, 1))) ||
@@ -541,7 +627,7 @@ int snl_engine::init() {
     // zero everything a pass may read before writing (the reference's buffers start zeroed)
     if (hipMemsetAsync(x, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
         hipMemsetAsync(mx, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
-        hipMemsetAsync(hid, 0, sizeof(float) * (M + 1) * h, stream) != hipSuccess ||
+        hipMemsetAsync(hid, 0, sizeof(float) * (SNL_PF_M + 1) * h, stream) != hipSuccess ||
         hipMemsetAsync(hlast, 0, sizeof(float) * h, stream) != hipSuccess ||
         hipMemsetAsync(lin_state, 0, sizeof(float) * 3 * nl * state_floats, stream) != hipSuccess ||
         hipMemsetAsync(conv_state, 0, sizeof(float) * 3 * nl * conv_floats, stream) != hipSuccess ||
@@ -668,6 +754,126 @@ int snl_engine::record_mtp(int M, int draft) {
     }
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
+}
+
+// One prefill pass of M token rows (up to SNL_PF_M) over the execution plan, the same op order as
+// record_forward with the matrix products on the panel GEMM and the per-token work in prefill
+// kernels: branch inputs become GEMM fragments (rows_to_frags), each mHC site computes its router
+// sums and coefficients over all rows, and merges and SwiGLU run as their own launches.
+int snl_engine::record_prefill(int M, int rows) {
+    const snl_config& c = cfg;
+    int rc = 0;
+    const int X2 = 2 * h;
+    if (op("embed", 0.0)) rc |= launch_embed_tokens(pf_tokens(), (const int8_t*)embed.q, embed.s, c.vocab, h, pf_x, M, stream);
+    if (op("copy", 0.0)) rc |= launch_copy(hid, hlast, h, stream);  // row 0 = hidden of the token before
+    int fslot = 0, lslot = 0;
+    const size_t kvn = (size_t)ctx * kv_dim;
+    const size_t nl = std::max(n_lin, 1);
+    for (size_t vi = 0; vi < plan.size(); ++vi) {
+        const int li = plan[vi];
+        const Layer& L = layers[li];
+        const bool mhc = is_mhc(li);
+        if (mhc) {
+            if (li == c.mhc_start && op("expand", 0.0)) rc |= launch_expand(pf_x, h, M, stream);
+            rc |= pf_site(L.mhc_attn.p, M);
+        }
+        const int pro = mhc ? ROWS_NORM_MHC : ROWS_NORM;
+        rc |= pf_mat(L.full ? "gemm_qkv" : "gemm_in_proj", L.mix_in, pf_x, X2, M, pro, L.in_ln.p, pf_proj,
+                     L.mix_in.rows);
+        if (L.full) {
+            AttnArgs a = attn_args(nullptr, kcache + kvn * fslot, vcache + kvn * fslot, L.small.p);
+            a.proj = pf_proj;
+            a.qbuf = pf_qbuf;
+            a.out = pf_attn;
+            if (op("attention", 0.0)) rc |= launch_attention_prefill(a, d_pstep, M, stream);
+            rc |= pf_mat("gemm_o", L.mix_out, pf_attn, q_dim, M, ROWS_PLAIN, nullptr, pf_br, h);
+            ++fslot;
+        } else {
+            DnPrefillArgs d{};
+            d.proj = pf_proj;
+            d.proj_stride = lin_proj_rows;
+            d.lw = L.small.p;
+            d.conv_state = conv_state + ((size_t)cur * nl + lslot) * conv_floats;
+            d.state = lin_state + ((size_t)cur * nl + lslot) * state_floats;
+            d.q = pf_dq;
+            d.k = pf_dk;
+            d.v = pf_dv;
+            d.gz = pf_gz;
+            d.beta = pf_beta;
+            d.decay = pf_decay;
+            d.out = pf_attn;
+            d.ssq = pf_ssq;
+            d.conv_dim = conv_dim;
+            d.n_k = c.lin_k_heads;
+            d.n_v = c.lin_v_heads;
+            if (op("deltanet", 0.0)) rc |= launch_deltanet_prefill(d, M, stream);
+            // the head factor of the gated norm is applied while the rows become fragments
+            rc |= pf_mat("gemm_out_proj", L.mix_out, pf_attn, lin_value_dim, M, ROWS_GNORM, nullptr, pf_br, h);
+            ++lslot;
+        }
+        if (op("merge", 0.0)) rc |= launch_merge(pf_x, pf_coef, pf_br, h, M, mhc ? 1 : 0, stream);
+        if (mhc) rc |= pf_site(L.mhc_ffn.p, M);
+        rc |= pf_mat("gemm_gate_up", L.gate_up, pf_x, X2, M, pro, L.post_ln.p, pf_proj, 2 * c.intermediate);
+        if (op("swiglu", 0.0)) rc |= launch_swiglu(pf_proj, pf_act, c.intermediate, M, stream);
+        rc |= pf_mat("gemm_down", L.down, pf_act, c.intermediate, M, ROWS_PLAIN, nullptr, pf_br, h);
+        const int mode = !mhc ? 0 : (li + 1 == c.mhc_end ? 2 : 1);
+        if (op("merge", 0.0)) rc |= launch_merge(pf_x, pf_coef, pf_br, h, M, mode, stream);
+    }
+    rc |= norm(pf_x, X2, nullptr, 0, final_norm.p, hid + h, 0, M);
+    if (rows > 0) {
+        rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
+        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
+    }
+    if (op("copy", 0.0)) rc |= launch_copy(hlast, hid + (size_t)M * h, h, stream);
+    mark("end", 0.0);
+    return rc ? SNL_EDEVICE : SNL_OK;
+}
+
+// The MTP head over M pairs (hidden row r0 + i, token i) of a prompt chunk, as record_mtp without
+// the draft (src/engine.rs:549-570, src/worker.rs:312-318).
+int snl_engine::record_mtp_prefill(int M, int r0) {
+    const snl_config& c = cfg;
+    int rc = 0;
+    const int X2 = 2 * h;
+    if (op("embed", 0.0)) rc |= launch_embed_tokens(pf_tokens(), (const int8_t*)embed.q, embed.s, c.vocab, h, pf_x, M, stream);
+    // x = fc_e(norm_e(emb)) + fc_h(norm_h(hid[r0..])): the fragments are taken before fc_e overwrites x
+    rc |= pf_mat("gemm_fc_e", fc_e, pf_x, X2, M, ROWS_NORM, norm_e.p, pf_x, X2);
+    rc |= pf_mat("gemm_fc_h", fc_h, hid + (size_t)r0 * h, h, M, ROWS_NORM, norm_h.p, pf_br, h);
+    if (op("merge", 0.0)) rc |= launch_merge(pf_x, pf_coef, pf_br, h, M, 0, stream);
+    rc |= pf_mat("gemm_mtp_qkv", m_qkv, pf_x, X2, M, ROWS_NORM, m_in_ln.p, pf_proj, attn_proj_rows);
+    AttnArgs a = attn_args(nullptr, m_kc, m_vc, m_qk_norm.p);
+    a.proj = pf_proj;
+    a.qbuf = pf_qbuf;
+    a.out = pf_attn;
+    if (op("attention", 0.0)) rc |= launch_attention_prefill(a, d_pstep, M, stream);
+    rc |= pf_mat("gemm_mtp_o", m_o, pf_attn, q_dim, M, ROWS_PLAIN, nullptr, pf_br, h);
+    if (op("merge", 0.0)) rc |= launch_merge(pf_x, pf_coef, pf_br, h, M, 0, stream);
+    rc |= pf_mat("gemm_mtp_gate_up", m_gate_up, pf_x, X2, M, ROWS_NORM, m_post_ln.p, pf_proj, 2 * c.intermediate);
+    if (op("swiglu", 0.0)) rc |= launch_swiglu(pf_proj, pf_act, c.intermediate, M, stream);
+    rc |= pf_mat("gemm_mtp_down", m_down, pf_act, c.intermediate, M, ROWS_PLAIN, nullptr, pf_br, h);
+    if (op("merge", 0.0)) rc |= launch_merge(pf_x, pf_coef, pf_br, h, M, 0, stream);
+    mark("end", 0.0);
+    return rc ? SNL_EDEVICE : SNL_OK;
+}
+
+// Upload one prefill chunk's tokens and positions and run it (main model, or the MTP head over
+// hidden rows r0..), waiting for it: the pinned record is reused by the next chunk.
+int snl_engine::prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int m, int cache_pos0, int rows,
+                              bool mtp, int r0) {
+    PrefillDev& st = *h_pstep;
+    st.pos0 = cache_pos0;
+    st.m = m;
+    for (int i = 0; i < m; ++i) {
+        st.tokens[i] = tokens[i];
+        for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[(size_t)i * 3 + k] : (uint32_t)(cache_pos0 + i);
+        st.rpos[i][3] = 0;
+    }
+    if (hipMemcpyAsync(d_pstep, h_pstep, sizeof(PrefillDev), hipMemcpyHostToDevice, stream) != hipSuccess)
+        return fail(SNL_EDEVICE, "prefill step upload failed");
+    int rc = mtp ? record_mtp_prefill(m, r0) : record_prefill(m, rows);
+    if (rc) return fail(SNL_EDEVICE, "prefill launch failed (M %d)", m);
+    if (hipStreamSynchronize(stream) != hipSuccess) return fail(SNL_EDEVICE, "prefill failed on device");
+    return SNL_OK;
 }
 
 // Replay (capturing on first use) the pass (kind, M, a, b): kind 0 forward (a = rows,
@@ -891,6 +1097,7 @@ void snl_engine_destroy(snl_engine* e) {
     for (void* p : e->allocs) hipFree(p);
     if (e->h_picks) hipHostFree(e->h_picks);
     if (e->h_step) hipHostFree(e->h_step);
+    if (e->h_pstep) hipHostFree(e->h_pstep);
     if (e->stream) hipStreamDestroy(e->stream);
     delete e;
 }
@@ -903,7 +1110,7 @@ int snl_hid_rows(const snl_engine* e) { return e->hid_rows; }
 int snl_has_mtp(const snl_engine* e) { return e->cfg.has_mtp != 0; }
 int snl_prefill_chunk(const snl_engine* e) {
     (void)e;
-    return kMaxM;
+    return SNL_PF_M;
 }
 
 int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* pos3, int logit_rows, int ckpt,
@@ -918,36 +1125,47 @@ int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* po
     if (e->pos + n > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + n, e->ctx);
     for (int i = 0; i < n; ++i)
         if (tokens[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tokens[i]);
-    // chunks of at most kMaxM rows; the last chunk holds the logit rows
-    int last = n <= kMaxM ? n : std::max(logit_rows, n % kMaxM ? n % kMaxM : kMaxM);
     int rows = 0;
-    for (int c0 = 0; c0 < n;) {
-        const int rem = n - c0;
-        const int m = rem == last ? last : std::min(kMaxM, rem - last);
-        const bool is_last = c0 + m == n;
-        rows = is_last ? std::min(logit_rows, m) : 0;
+    if (n > kMaxM) {
+        // chunked prefill: passes of up to SNL_PF_M rows (the reference's MAX_M, src/engine.rs:18);
+        // the last holds the logit rows
+        int last = n % SNL_PF_M ? n % SNL_PF_M : SNL_PF_M;
+        if (last < logit_rows) last = logit_rows;
+        for (int c0 = 0; c0 < n;) {
+            const int rem = n - c0;
+            const int m = rem == last ? last : std::min(SNL_PF_M, rem - last);
+            rows = c0 + m == n ? std::min(logit_rows, m) : 0;
+            int rc = e->prefill_chunk(tokens + c0, pos3 ? pos3 + (size_t)c0 * 3 : nullptr, m, e->pos, rows, false, 0);
+            if (rc) return rc;
+            e->ck_slot = -1;
+            e->pos += m;
+            e->hid_rows = m;
+            c0 += m;
+        }
+    } else {
+        // one captured decode pass of n <= kMaxM rows
+        rows = std::min(logit_rows, n);
         StepDev& st = e->h_step[0];
         memset(&st, 0, sizeof st);
         st.pos0 = e->pos;
-        st.m = m;
+        st.m = n;
         st.ckpt = ckpt ? 1 : 0;
         st.s_in = e->cur;
         st.s_ck = (e->cur + 1) % 3;
         st.s_out = ckpt ? (e->cur + 2) % 3 : (e->cur + 1) % 3;
-        for (int i = 0; i < m; ++i) {
-            st.tokens[i] = tokens[c0 + i];
-            for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[(c0 + i) * 3 + k] : (uint32_t)(e->pos + i);
+        for (int i = 0; i < n; ++i) {
+            st.tokens[i] = tokens[i];
+            for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[i * 3 + k] : (uint32_t)(e->pos + i);
             st.rpos[i][3] = 0;
         }
-        int rc = e->run(0, m, rows, ckpt ? 1 : 0);
+        int rc = e->run(0, n, rows, ckpt ? 1 : 0);
         if (rc) return rc;
         // the step record is reused by the next call: wait for this one
         if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "forward failed on device");
         e->ck_slot = ckpt ? st.s_ck : -1;
         e->cur = st.s_out;
-        e->pos += m;
-        e->hid_rows = m;
-        c0 += m;
+        e->pos += n;
+        e->hid_rows = n;
     }
     if (rows > 0) {
         if (logits_out &&
@@ -1069,7 +1287,19 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
         return e->fail(SNL_EARG, "mtp: rows out of range");
     for (int i = 0; i < n; ++i)
         if (tokens[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tokens[i]);
-    for (int c0 = 0; c0 < n; c0 += kMaxM) {
+    int c0 = 0;
+    if (n > kMaxM) {
+        // a prompt's catch-up (src/worker.rs:312-318): prefill passes of up to SNL_PF_M pairs; a
+        // drafting call leaves its last pair to the captured one-row pass below
+        const int np = draft ? n - 1 : n;
+        while (c0 < np) {
+            const int m = std::min(SNL_PF_M, np - c0);
+            int rc = e->prefill_chunk(tokens + c0, pos3 + (size_t)c0 * 3, m, slot0 + c0, 0, true, r0 + c0);
+            if (rc) return rc;
+            c0 += m;
+        }
+    }
+    for (; c0 < n; c0 += kMaxM) {
         const int m = std::min(kMaxM, n - c0);
         const bool last = c0 + m == n;
         StepDev& st = e->h_step[1];
@@ -1366,6 +1596,62 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
     int rc = launch_gemv(g, quant, M, st);
     if (rc == 0 && g.packed && hipStreamSynchronize(st) != hipSuccess) rc = -2;
     return rc == -1 ? SNL_EARG : (rc ? SNL_EDEVICE : SNL_OK);
+}
+
+int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K, int x_stride,
+             int y_stride, void* stream) {
+    if ((quant != 0 && quant != 1) || !wq || !ws || !x || !y || K % 128 || M < 1 || M > SNL_PREFILL_M || N < 1 ||
+        x_stride < K || y_stride < N)
+        return SNL_EARG;
+    hipStream_t st = (hipStream_t)stream;
+    // panel-order weights and the token fragments in staging buffers held under the lock until the
+    // call has finished on the stream
+    static uint8_t* pq = nullptr;
+    static float *ps = nullptr, *xs = nullptr;
+    static void* fr = nullptr;
+    static size_t cap_q = 0, cap_s = 0, cap_f = 0;
+    std::lock_guard<std::mutex> lk(g_kstep_mu);
+    const size_t qb = gemm_q_bytes(quant, N, K), sf = gemm_s_floats(N, K), fb = frags_bytes(SNL_PREFILL_M, K);
+    if (qb > cap_q || sf > cap_s || fb > cap_f) {
+        if (hipStreamSynchronize(st) != hipSuccess) return SNL_EDEVICE;
+        hipFree(pq);
+        hipFree(ps);
+        hipFree(fr);
+        hipFree(xs);
+        pq = nullptr;
+        ps = xs = nullptr;
+        fr = nullptr;
+        cap_q = cap_s = cap_f = 0;
+        if (hipMalloc((void**)&pq, qb) != hipSuccess || hipMalloc((void**)&ps, sf * 4) != hipSuccess ||
+            hipMalloc(&fr, fb) != hipSuccess || hipMalloc((void**)&xs, SNL_PREFILL_M * 4) != hipSuccess)
+            return SNL_ENOMEM;
+        cap_q = qb;
+        cap_s = sf;
+        cap_f = fb;
+    }
+    if (launch_panel_pack(quant, N, K, wq, ws, pq, ps, st)) return SNL_EDEVICE;
+    RowsArgs r{};
+    r.x = x;
+    r.x_stride = x_stride;
+    r.M = M;
+    r.K = K;
+    r.mode = ROWS_PLAIN;
+    r.perm4 = quant;
+    r.frags = fr;
+    r.xs = xs;
+    if (launch_rows_to_frags(r, st)) return SNL_EDEVICE;
+    GemmArgs g{};
+    g.wq = pq;
+    g.ws = ps;
+    g.frags = fr;
+    g.xs = xs;
+    g.y = y;
+    g.y_stride = y_stride;
+    g.M = M;
+    g.N = N;
+    g.K = K;
+    if (launch_mgemm(g, quant, st) || hipStreamSynchronize(st) != hipSuccess) return SNL_EDEVICE;
+    return SNL_OK;
 }
 
 int snl_deltanet(const float* proj, int proj_stride, const float* lw, float* conv_state, float* state, float* out,

@@ -63,6 +63,42 @@ int mgemv_init();
 // Set the LDS limit of every streaming-GEMV instantiation (call once, outside graph capture).
 int gemv_init();
 
+// ---------------------------------------------------------------- prefill GEMM (mgemm.hip)
+// Token rows -> the GEMM's f16 hi/lo A fragments, with the branch input computed on the way:
+// the rows as they are, RMSNorm(x0) * (1 + w), the mHC pre-mix then that norm (coef[m][0..1]),
+// or the head factor of the DeltaNet gated norm (ssq partials [M][K/128][4]).
+enum RowsMode { ROWS_PLAIN = 0, ROWS_NORM = 1, ROWS_NORM_MHC = 2, ROWS_GNORM = 3 };
+struct RowsArgs {
+    const float* x;      // token row m at x + m * x_stride (NORM_MHC: stream 1 at +h)
+    int x_stride;
+    int M, K;
+    int mode;
+    const float* w;      // NORM*: (1 + w) weights [K]
+    const float* coef;   // NORM_MHC: [M][8]
+    int h;
+    const float* ssq;    // GNORM
+    float eps;
+    int perm4;           // 1: element order of the Q4 nibble dequant
+    void* frags;         // out: frags_bytes(M, K)
+    float* xs;           // out: per-token scale [roundup(M, 16)]
+};
+struct GemmArgs {
+    const void* wq;      // panel-order quants
+    const float* ws;     // panel-order scales
+    const void* frags;   // token fragments
+    const float* xs;
+    float* y;            // y[m * y_stride + n_off + n]
+    int y_stride, n_off;
+    int M, N, K;
+};
+size_t gemm_q_bytes(int quant, int N, int K);
+size_t gemm_s_floats(int N, int K);
+size_t frags_bytes(int M, int K);
+// reference layout (q [N, K] Q8 / [N, K/2] Q4, s [N, K/32]) -> panel order
+int launch_panel_pack(int quant, int N, int K, const void* q, const float* s, void* qp, float* sp, hipStream_t st);
+int launch_rows_to_frags(const RowsArgs& a, hipStream_t s);
+int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s);
+
 // ---------------------------------------------------------------- layers (layers.hip)
 // x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790)
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
@@ -131,6 +167,28 @@ int launch_deltanet(const DeltaArgs& a, int M, hipStream_t s);
 // the gated RMS norm in place on out (kernel-level entry; the engine folds it into out_proj)
 int launch_deltanet_norm(const DeltaArgs& a, int M, hipStream_t s);
 
+// ---------------------------------------------------------------- chunked prefill (prefill.hip)
+// x[m] = dequant(embed[tokens[m]]) (stream 0), stream 1 zero
+int launch_embed_tokens(const uint32_t* tokens, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
+                        hipStream_t s);
+// coef[m][8] from the router sums part[m][9] of the 2-stream rows (h: stream width)
+int launch_mhc_coef(const float* part, const float* w, int h, int iterations, float* coef, int M, hipStream_t s);
+
+struct DnPrefillArgs {
+    const float* proj;   // [M, proj_stride]: qkv[conv_dim] | z[n_v*128] | b[n_v] | a[n_v]
+    int proj_stride;
+    const float* lw;     // conv w [conv_dim*4] | A_log[n_v] | dt_bias[n_v] | norm[128]
+    float* conv_state;   // this visit's [3, conv_dim], updated in place
+    float* state;        // this visit's [n_v, 128, 128], updated in place
+    float *q, *k;        // scratch [M][n_k][128]: normalised (q also times 1/sqrt(128))
+    float *v, *gz;       // scratch [M][n_v][128]: conv output, silu(z)
+    float *beta, *decay; // scratch [M][n_v]
+    float* out;          // [M, n_v*128] (o * w) * silu(z), before the head factor of the norm
+    float* ssq;          // [M, n_v, 4] partial sums of o^2 per column group
+    int conv_dim, n_k, n_v;
+};
+int launch_deltanet_prefill(const DnPrefillArgs& a, int M, hipStream_t s);
+
 // ---------------------------------------------------------------- gated attention (attention.hip)
 struct AttnArgs {
     const float* proj;   // [M, proj_stride] q+gate | k | v
@@ -150,6 +208,12 @@ struct AttnArgs {
 // prep + attend + combine for M = 1 or 2 tokens
 int launch_attention(const AttnArgs& a, int M, hipStream_t s);
 constexpr int kAttnPart = 64;  // keys per split-K part
+
+// Gated attention over a chunk (attention_prefill.hip): rows m < M at cache positions pos0 + m
+// with rotary positions rpos[m]; q/k norm + RoPE, K/V into the f16 cache, then causal
+// attention over every earlier key and the sigmoid gate.  Same AttnArgs, with `pstep` for the
+// positions (step is unused).
+int launch_attention_prefill(const AttnArgs& a, const PrefillDev* pstep, int M, hipStream_t s);
 
 // ---------------------------------------------------------------- seeded initialiser (init.hip)
 int launch_gen_matrix(uint64_t key, int64_t rows, int64_t cols, float stdv, int quant, void* q, float* sc,

@@ -290,7 +290,7 @@ int launch_branch_norm(const NormArgs& a, hipStream_t s) {
 }
 
 int launch_mhc(const float* x, const float* w, float* part, int h, int M, hipStream_t s) {
-    if (M < 1 || M > 64 || h % 2) return -1;
+    if (M < 1 || M > SNL_PF_M || h % 2) return -1;
     hipLaunchKernelGGL(mhc_kernel, dim3(M), dim3(kMhcThreads), 0, s, x, w, part, h);
     return last_error();
 }

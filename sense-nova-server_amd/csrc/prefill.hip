@@ -1,0 +1,200 @@
+// Per-token kernels of the chunked prefill pass (up to 512 token rows per launch): the embedding
+// gather, the mHC token coefficients, and the Gated DeltaNet over a chunk.
+//
+// DeltaNet (src/shaders/linear.wgsl:38-140).  The causal conv, SiLU, q/k L2 normalisation and the
+// per-token gates do not depend on the recurrent state, so they run for every token of the chunk
+// at once (dn_conv_kernel, one block per (token, head)); the conv state then takes the chunk's
+// last three inputs (dn_conv_state_kernel).  The recurrence itself runs token by token in
+// dn_recur_kernel with the decode kernel's thread layout: 4 blocks per value head, each owning
+// 32 state columns in registers, so a column's arithmetic is exactly the decode step's.  The
+// next token's inputs are loaded while the current one is computed.  The state is updated in
+// place in the current slot (a prefill pass has no checkpoint).
+#include "common.h"
+#include "kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace snl {
+
+namespace {
+
+constexpr int DK = 128, DV = 128;
+constexpr int kCG = kDeltaGroups, kCols = DV / kCG;
+constexpr int kThreads = 512, kWaves = kThreads / 64, kRows = 8;
+
+// x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790)
+__global__ __launch_bounds__(256) void pf_embed_kernel(const uint32_t* tokens, const int8_t* eq, const float* es,
+                                                        int vocab, int h, float* x) {
+    const int m = blockIdx.x;
+    uint32_t tok = tokens[m];
+    if (tok >= (uint32_t)vocab) tok = 0;  // the host rejects out-of-range ids before launching
+    const int8_t* q = eq + (size_t)tok * h;
+    const float* s = es + (size_t)tok * (h / 32);
+    float* xr = x + (size_t)m * 2 * h;
+    for (int i = threadIdx.x; i < h; i += 256) {
+        xr[i] = (float)q[i] * s[i >> 5];
+        xr[h + i] = 0.0f;
+    }
+}
+
+// coef[m] = mhc_coefficients of the token's router sums part[m][0..8] (layers.wgsl:94-126)
+__global__ __launch_bounds__(64) void mhc_coef_kernel(const float* part, const float* w, int d, int iterations,
+                                                       float* coef, int M) {
+    const int m = blockIdx.x * 64 + threadIdx.x;
+    if (m >= M) return;
+    mhc_coefficients(part + (size_t)m * 9, w, d, iterations, coef + (size_t)m * 8);
+}
+
+// Block (token m, slot): slots [0, n_k) the q heads, [n_k, 2n_k) the k heads, then the v heads.
+// 128 threads, one channel each (linear.wgsl:38-66, :104-117).
+__global__ __launch_bounds__(128) void dn_conv_kernel(DnPrefillArgs a) {
+    __shared__ float red[2];
+    const int m = blockIdx.x, slot = blockIdx.y, tid = threadIdx.x;
+    const int n_k = a.n_k, n_v = a.n_v, cd = a.conv_dim, key_dim = n_k * DK;
+    const int kind = slot < n_k ? 0 : slot < 2 * n_k ? 1 : 2;
+    const int head = kind == 0 ? slot : kind == 1 ? slot - n_k : slot - 2 * n_k;
+    const int ch = kind == 0 ? head * DK + tid : kind == 1 ? key_dim + head * DK + tid : 2 * key_dim + head * DV + tid;
+    const float4 w = *reinterpret_cast<const float4*>(a.lw + (size_t)ch * 4);
+    // input t of the chunk: proj row t, or conv state row 3 + t for t < 0 (oldest first)
+    float in[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = m - 3 + i;
+        in[i] = t >= 0 ? a.proj[(size_t)t * a.proj_stride + ch] : a.conv_state[(size_t)(3 + t) * cd + ch];
+    }
+    const float o = ((w.x * in[0] + w.y * in[1]) + w.z * in[2]) + w.w * in[3];
+    const float v = o / (1.0f + expf(-o));
+    if (kind == 2) {
+        a.v[((size_t)m * n_v + head) * DV + tid] = v;
+        const float z = a.proj[(size_t)m * a.proj_stride + cd + head * DV + tid];
+        a.gz[((size_t)m * n_v + head) * DV + tid] = z / (1.0f + expf(-z));
+        if (tid == 0) {  // linear.wgsl:113-117
+            const float* lwp = a.lw + (size_t)cd * 4;
+            const float* prow = a.proj + (size_t)m * a.proj_stride;
+            const int b_off = cd + n_v * DV, a_off = b_off + n_v;
+            a.beta[(size_t)m * n_v + head] = 1.0f / (1.0f + expf(-prow[b_off + head]));
+            const float araw = prow[a_off + head] + lwp[n_v + head];
+            const float sp = araw <= 20.0f ? logf(1.0f + expf(araw)) : araw;
+            a.decay[(size_t)m * n_v + head] = expf(-expf(lwp[head]) * sp);
+        }
+        return;
+    }
+    // L2 normalisation over the head's 128 channels (two wave sums, added in wave order)
+    const float s = wave_sum(v * v);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    if (kind == 0) {
+        const float qs = (1.0f / sqrtf((red[0] + red[1]) + 1e-6f)) * (1.0f / sqrtf((float)DK));
+        a.q[((size_t)m * n_k + head) * DK + tid] = v * qs;
+    } else {
+        const float ks = 1.0f / sqrtf((red[0] + red[1]) + 1e-6f);
+        a.k[((size_t)m * n_k + head) * DK + tid] = v * ks;
+    }
+}
+
+// conv state := the chunk's last three inputs (from the old state when the chunk is shorter)
+__global__ __launch_bounds__(256) void dn_conv_state_kernel(DnPrefillArgs a, int M) {
+    const int ch = blockIdx.x * 256 + threadIdx.x;
+    const int cd = a.conv_dim;
+    if (ch >= cd) return;
+    float r[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int t = M - 3 + i;
+        r[i] = t >= 0 ? a.proj[(size_t)t * a.proj_stride + ch] : a.conv_state[(size_t)(3 + t) * cd + ch];
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) a.conv_state[(size_t)i * cd + ch] = r[i];
+}
+
+// The recurrence over the chunk (linear.wgsl:118-136), 4 blocks per value head.
+__global__ __launch_bounds__(kThreads) void dn_recur_kernel(DnPrefillArgs a, int M) {
+    extern __shared__ float ored[];  // [kWaves][M]
+    const int h = blockIdx.x / kCG, cg = blockIdx.x % kCG;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 3, rg = lane >> 2;
+    const int jl = 4 * wave + c, j = cg * kCols + jl;
+    const int n_k = a.n_k, n_v = a.n_v, group = n_v / n_k, kh = h / group;
+    const size_t hoff = (size_t)h * DK * DV;
+    float* S = a.state + hoff;
+    float s[kRows];
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) s[r] = S[(size_t)(kRows * rg + r) * DV + j];
+    const float norm_w = a.lw[(size_t)a.conv_dim * 4 + 2 * n_v + j];
+
+    auto load = [&](int m, float4 (&qv)[2], float4 (&kv)[2], float& vj, float& be, float& de, float& gz) {
+        const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)m * n_k + kh) * DK + kRows * rg);
+        const float4* kp = reinterpret_cast<const float4*>(a.k + ((size_t)m * n_k + kh) * DK + kRows * rg);
+        qv[0] = qp[0], qv[1] = qp[1];
+        kv[0] = kp[0], kv[1] = kp[1];
+        vj = a.v[((size_t)m * n_v + h) * DV + j];
+        be = a.beta[(size_t)m * n_v + h];
+        de = a.decay[(size_t)m * n_v + h];
+        gz = a.gz[((size_t)m * n_v + h) * DV + j];
+    };
+    float4 qn[2], kn[2];
+    float vn, ben, den, gzn;
+    load(0, qn, kn, vn, ben, den, gzn);
+    for (int m = 0; m < M; ++m) {
+        const float qf[8] = {qn[0].x, qn[0].y, qn[0].z, qn[0].w, qn[1].x, qn[1].y, qn[1].z, qn[1].w};
+        const float kf[8] = {kn[0].x, kn[0].y, kn[0].z, kn[0].w, kn[1].x, kn[1].y, kn[1].z, kn[1].w};
+        const float vj = vn, beta = ben, decay = den, gz = gzn;
+        if (m + 1 < M) load(m + 1, qn, kn, vn, ben, den, gzn);
+        float kv = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            s[r] = s[r] * decay;
+            kv = fmaf(s[r], kf[r], kv);
+        }
+#pragma unroll
+        for (int sh = 4; sh < 64; sh <<= 1) kv = kv + __shfl_xor(kv, sh, 64);
+        const float dlt = (vj - kv) * beta;
+        float o = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kRows; ++r) {
+            s[r] = fmaf(kf[r], dlt, s[r]);
+            o = fmaf(s[r], qf[r], o);
+        }
+#pragma unroll
+        for (int sh = 4; sh < 64; sh <<= 1) o = o + __shfl_xor(o, sh, 64);
+        if (rg == 0) a.out[(size_t)m * n_v * DV + h * DV + j] = (o * norm_w) * gz;
+        float q2 = o * o;
+        q2 = q2 + __shfl_xor(q2, 1, 64);
+        q2 = q2 + __shfl_xor(q2, 2, 64);
+        if (lane == 0) ored[wave * M + m] = q2;
+    }
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) S[(size_t)(kRows * rg + r) * DV + j] = s[r];
+    __syncthreads();
+    for (int m = tid; m < M; m += kThreads) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) t = t + ored[w * M + m];
+        a.ssq[((size_t)m * n_v + h) * kCG + cg] = t;
+    }
+}
+
+}  // namespace
+
+int launch_embed_tokens(const uint32_t* tokens, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
+                        hipStream_t s) {
+    if (M < 1) return -1;
+    hipLaunchKernelGGL(pf_embed_kernel, dim3(M), dim3(256), 0, s, tokens, eq, es, vocab, h, x);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_mhc_coef(const float* part, const float* w, int h, int iterations, float* coef, int M, hipStream_t s) {
+    if (M < 1) return -1;
+    hipLaunchKernelGGL(mhc_coef_kernel, dim3((M + 63) / 64), dim3(64), 0, s, part, w, 2 * h, iterations, coef, M);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+int launch_deltanet_prefill(const DnPrefillArgs& a, int M, hipStream_t s) {
+    if (M < 1 || M > SNL_PF_M || a.n_k < 1 || a.n_v % a.n_k) return -1;
+    hipLaunchKernelGGL(dn_conv_kernel, dim3(M, 2 * a.n_k + a.n_v), dim3(128), 0, s, a);
+    hipLaunchKernelGGL(dn_conv_state_kernel, dim3((a.conv_dim + 255) / 256), dim3(256), 0, s, a, M);
+    hipLaunchKernelGGL(dn_recur_kernel, dim3(a.n_v * kCG), dim3(kThreads), (size_t)kWaves * M * 4, s, a, M);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+}  // namespace snl

@@ -107,6 +107,7 @@ def lib() -> ctypes.CDLL:
         L.snl_buffer_size.restype = ctypes.c_size_t
         L.snl_buffer_size.argtypes = [vp, ctypes.c_int]
         L.snl_gemv.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
+        L.snl_gemm.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
         L.snl_deltanet.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_float] + [ctypes.c_int] * 5 + [vp]
         L.snl_attention.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int,
@@ -387,6 +388,14 @@ class kernels:
                             y_stride, kernels._stream())
         if rc != SNL_OK:
             raise SnlError(rc, "snl_gemv")
+
+    @staticmethod
+    def gemm(quant: int, wq, ws, x, y, M: int, N: int, K: int, x_stride: int, y_stride: int):
+        """The prefill GEMM (M up to 512 rows) over reference-layout weights."""
+        rc = lib().snl_gemm(quant, wq.data_ptr(), ws.data_ptr(), x.data_ptr(), y.data_ptr(), M, N, K, x_stride,
+                            y_stride, kernels._stream())
+        if rc != SNL_OK:
+            raise SnlError(rc, "snl_gemm")
 
     @staticmethod
     def deltanet(proj, proj_stride, lw, conv_state, state, out, conv_dim, n_k, n_v, eps, M, ckpt, s_in, s_out,

@@ -60,6 +60,47 @@ def test_gemv_matches_oracle(torch_cuda, K, oracle, quant, n, k, m):
 
 
 @pytest.mark.parametrize("quant", [0, 1])
+@pytest.mark.parametrize("n,k,m", [(96, 1024, 3), (4096, 4096, 512), (1544, 256, 37), (12352, 4096, 130),
+                                   (4096, 12288, 64), (24576, 4096, 17)])
+def test_gemm_matches_oracle(torch_cuda, K, oracle, quant, n, k, m):
+    """The prefill GEMM against the oracle's GEMV and float64 products of the dequantised weights."""
+    torch = torch_cuda
+    print(f"gemm quant={quant} n={n} k={k} m={m}", flush=True)
+    q, s, x = _gemv_case(oracle, quant, n, k, m, seed=7 * n + k + m + quant)
+    x[0] *= 1e3  # rows of very different magnitudes keep their own scale
+    if m > 2:
+        x[2] *= 1e-4
+    dq, ds, dx = _dev(torch, q), _dev(torch, s), _dev(torch, x)
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    K.gemm(quant, dq, ds, dx, y, m, n, k, k, n)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    deq = oracle.dequant(q, s, quant, k).astype(np.float64)
+    scale = np.abs(x.astype(np.float64)) @ np.abs(deq).T
+    exact = x.astype(np.float64) @ deq.T
+    assert np.all(np.abs(got - exact) <= 1e-5 * scale + 1e-30), np.abs(got - exact).max()
+    if m <= 64:
+        ref = oracle.gemv(quant, q, s, x, n, k)
+        assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-30)
+
+
+@pytest.mark.parametrize("quant", [0, 1])
+def test_gemm_rows_independent_of_m(torch_cuda, K, oracle, quant):
+    """A token row's result does not depend on how many rows share the call or where it sits."""
+    torch = torch_cuda
+    n, k = 1040, 1024
+    q, s, x = _gemv_case(oracle, quant, n, k, 100, seed=5)
+    dq, ds, dx = _dev(torch, q), _dev(torch, s), _dev(torch, x)
+    y = torch.zeros((100, n), dtype=torch.float32, device="cuda")
+    K.gemm(quant, dq, ds, dx, y, 100, n, k, k, n)
+    full = y.cpu().numpy()
+    for lo, hi in ((0, 3), (37, 100), (64, 65)):
+        ys = torch.zeros((hi - lo, n), dtype=torch.float32, device="cuda")
+        K.gemm(quant, dq, ds, dx[lo:hi], ys, hi - lo, n, k, k, n)
+        assert np.array_equal(ys.cpu().numpy(), full[lo:hi])
+
+
+@pytest.mark.parametrize("quant", [0, 1])
 def test_gemv_rows_independent_of_m(torch_cuda, K, oracle, quant):
     """Row r of an M-row call is bitwise the M=1 result: the verify pass reproduces plain decode."""
     torch = torch_cuda

@@ -1,9 +1,11 @@
 """The generation worker's prefix cache (src/worker.rs:115-174) on the tiny model, through the C ABI.
 
-A request served from the live state or a restored snapshot must give the same token stream and
-the same top-2 margins, bit for bit, as the same prompt run cold (reset, prefill from position
-0) on a second engine with the same weights; the cold stream is the one the engine tests hold
-against the oracle.  The worker's bookkeeping (cached tokens, live length, slot contents and
+A request served from the live state or a restored snapshot must give the token stream of the
+same prompt run cold (reset, prefill from position 0) on a second engine with the same weights,
+up to a divergence at a near-tie of the cold run (top-2 gap < 1e-3), with top-2 margins within
+1e-3; the cold stream is the one the engine tests hold against the oracle.  (Not bit for bit:
+the cold run feeds the earlier answer through the prefill GEMM, the warm one decoded it through
+the GEMV, and the two sum in different orders.)  The worker's bookkeeping (cached tokens, live length, slot contents and
 clocks) must follow the restatement in oracle/prefix_cache.py request by request, with the
 tokens fed during decoding read from the engine's position.
 """
@@ -54,8 +56,13 @@ class Checked:
         want = self.model.begin(prompt, snapshot_at)
         r = self.w.run(prompt, max_tokens, snapshot_at, spec=self.spec)
         c = self.cold.generate(prompt, max_tokens, self.spec)
-        assert r["tokens"] == c["tokens"]
-        assert np.array_equal(r["gaps"], c["gaps"])
+        n = min(len(r["tokens"]), len(c["tokens"]))
+        k = next((i for i in range(n) if r["tokens"][i] != c["tokens"][i]), n)
+        if k < n:
+            assert c["gaps"][k] < 1e-3, f"divergence at {k} with cold gap {c['gaps'][k]}"
+        else:
+            assert len(r["tokens"]) == len(c["tokens"])
+        assert np.allclose(r["gaps"][:k], c["gaps"][:k], rtol=0, atol=1e-3)
         assert r["cached_tokens"] == want["cached"]
         if expect is not None:
             assert want["action"] == expect
