@@ -223,7 +223,8 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
              int x_stride, int y_stride, void* stream);
 
 /* The prefill GEMM (src/shaders/matmul.wgsl:200-318, MatKind::Tiled): y[m*y_stride + n] =
- * sum_k x[m*x_stride + k] * W[n, k] for M in 1..SNL_PREFILL_M token rows, K % 128 == 0, W in
+ * sum_k x[m*x_stride + k] * W[n, k] for M in 1..SNL_PREFILL_M token rows, K % 128 == 0 and
+ * K <= 16384, W in
  * the reference layout as for snl_gemv.  The call packs W into the GEMM's panel order and the
  * rows into f16 hi/lo fragments in staging buffers the library keeps, and returns after the
  * product has finished on `stream`. */

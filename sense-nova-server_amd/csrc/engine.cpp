@@ -495,6 +495,8 @@ static const char* validate(const snl_config* c) {
         return "M-RoPE sections must cover the rotary dims";
     if (!(c->loop_start < c->loop_end && c->loop_end <= c->n_layers && c->loop_count >= 1)) return "invalid loop range";
     if (c->intermediate % 32 != 0 || c->vocab < 2) return "invalid intermediate size or vocab";
+    // the prefill GEMM takes rows of at most 16384 (the down projection's K)
+    if (c->intermediate > 16384) return "intermediate size must be at most 16384";
     if (c->mhc_streams != 0) {
         if (c->mhc_streams != 2) return "only 2 mHC streams are supported";
         const int s = c->mhc_start, e = c->mhc_end;
@@ -1600,7 +1602,7 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
 
 int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K, int x_stride,
              int y_stride, void* stream) {
-    if ((quant != 0 && quant != 1) || !wq || !ws || !x || !y || K % 128 || M < 1 || M > SNL_PREFILL_M || N < 1 ||
+    if ((quant != 0 && quant != 1) || !wq || !ws || !x || !y || K % 128 || K > 16384 || M < 1 || M > SNL_PREFILL_M || N < 1 ||
         x_stride < K || y_stride < N)
         return SNL_EARG;
     hipStream_t st = (hipStream_t)stream;

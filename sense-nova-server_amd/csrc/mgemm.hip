@@ -131,29 +131,20 @@ __device__ __forceinline__ float block_max256(float v, float* red) {
     return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-// value of element k of token m's branch input (the row the GEMM multiplies)
-__device__ __forceinline__ float row_value(const RowsArgs& a, const float* xr, int m, int k, float f0, float f1,
-                                           float rinv) {
-    switch (a.mode) {
-        case ROWS_PLAIN: return xr[k];
-        case ROWS_NORM: return (xr[k] * rinv) * (1.0f + a.w[k]);
-        case ROWS_NORM_MHC: return ((f0 * xr[k] + f1 * xr[a.h + k]) * rinv) * (1.0f + a.w[k]);
-        default: {  // ROWS_GNORM: head factor of the gated RMS norm of 128-wide heads
-            const float* ps = a.ssq + ((size_t)m * (a.K / 128) + k / 128) * kDeltaGroups;
-            const float var_o = (((ps[0] + ps[1]) + ps[2]) + ps[3]) / 128.0f;
-            return xr[k] * (1.0f / sqrtf(var_o + a.eps));
-        }
-    }
-}
-
+// One block per token row: the row's 8-element groups are held in registers (GPT per thread),
+// the branch input is formed (RMSNorm (1 + w) of stream 0 or of the mHC pre-mix, or the DeltaNet
+// head factor, one per group), then the row's largest magnitude sets the power of two and each
+// group is written as its hi and lo halves of the MFMA A fragments.
+template <int GPT>
 __global__ __launch_bounds__(kRowThreads) void rows_to_frags_kernel(RowsArgs a) {
     __shared__ float red[4];
-    const int m = blockIdx.x, tid = threadIdx.x, K = a.K, nb = K / 32;
+    __shared__ float rs[4];
+    const int m = blockIdx.x, tid = threadIdx.x, K = a.K, nb = K / 32, ngr = K / 8;
     const int T = m >> 4, t = m & 15;
     half8_t* xf = reinterpret_cast<half8_t*>(a.frags);
     if (m >= a.M) {  // padding rows of the last token tile
         const half8_t z = {};
-        for (int u = tid; u < nb * 4; u += kRowThreads) {
+        for (int u = tid; u < ngr; u += kRowThreads) {
             const int b = u >> 2, g = u & 3;
             xf[(((size_t)T * nb + b) * 2 + 0) * 64 + 16 * g + t] = z;
             xf[(((size_t)T * nb + b) * 2 + 1) * 64 + 16 * g + t] = z;
@@ -162,60 +153,121 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_frags_kernel(RowsArgs a) 
         return;
     }
     const float* xr = a.x + (size_t)m * a.x_stride;
-    float f0 = 1.0f, f1 = 0.0f, rinv = 1.0f;
+    float f0 = 1.0f, f1 = 0.0f;
     if (a.mode == ROWS_NORM_MHC) {
         f0 = a.coef[m * 8];
         f1 = a.coef[m * 8 + 1];
     }
+    float v[GPT][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi) {
+        const int u = tid + kRowThreads * gi;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[gi][e] = 0.0f;
+        if (u < ngr) {
+            const float4* p = reinterpret_cast<const float4*>(xr + 8 * u);
+            const float4 p0 = p[0], p1 = p[1];
+            float w8[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+            if (a.mode == ROWS_NORM_MHC) {
+                const float4* q = reinterpret_cast<const float4*>(xr + a.h + 8 * u);
+                const float4 q0 = q[0], q1 = q[1];
+                const float u8[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w8[e] = f0 * w8[e] + f1 * u8[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[gi][e] = w8[e];
+                ss = fmaf(w8[e], w8[e], ss);
+            }
+        }
+    }
     if (a.mode == ROWS_NORM || a.mode == ROWS_NORM_MHC) {
         // layers.wgsl:46-73: RMSNorm of the (pre-mixed) stream-0 row
-        float ss = 0.0f;
-        for (int k = tid; k < K; k += kRowThreads) {
-            const float v = a.mode == ROWS_NORM ? xr[k] : f0 * xr[k] + f1 * xr[a.h + k];
-            ss = fmaf(v, v, ss);
-        }
-        __shared__ float rs[4];
         const float tot = block_sum<kRowThreads>(ss, rs);
-        rinv = 1.0f / sqrtf(tot / (float)K + a.eps);
+        const float rinv = 1.0f / sqrtf(tot / (float)K + a.eps);
+#pragma unroll
+        for (int gi = 0; gi < GPT; ++gi) {
+            const int u = tid + kRowThreads * gi;
+            if (u < ngr)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[gi][e] = (v[gi][e] * rinv) * (1.0f + a.w[8 * u + e]);
+        }
+    } else if (a.mode == ROWS_GNORM) {  // head factor of the gated RMS norm of 128-wide heads
+#pragma unroll
+        for (int gi = 0; gi < GPT; ++gi) {
+            const int u = tid + kRowThreads * gi;
+            if (u < ngr) {
+                const float* ps = a.ssq + ((size_t)m * (K / 128) + u / 16) * kDeltaGroups;
+                const float var_o = (((ps[0] + ps[1]) + ps[2]) + ps[3]) / 128.0f;
+                const float f = 1.0f / sqrtf(var_o + a.eps);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[gi][e] = v[gi][e] * f;
+            }
+        }
     }
     float amax = 0.0f;
-    for (int k = tid; k < K; k += kRowThreads) amax = fmaxf(amax, fabsf(row_value(a, xr, m, k, f0, f1, rinv)));
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[gi][e]));
     amax = block_max256(amax, red);
     // hi = f16(v * 2^-e) with the largest magnitude in [2^14, 2^15)
-    int e = 0;
-    if (amax > 0.0f) e = max(ilogbf(amax) - 14, -110);
-    const float down = ldexpf(1.0f, -e);
+    int ex = 0;
+    if (amax > 0.0f) ex = max(ilogbf(amax) - 14, -110);
+    const float down = ldexpf(1.0f, -ex);
     const int q4 = a.perm4;
-    for (int u = tid; u < nb * 4; u += kRowThreads) {
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi) {
+        const int u = tid + kRowThreads * gi;
+        if (u >= ngr) continue;
         const int b = u >> 2, g = u & 3;
         half8_t hi, lo;
 #pragma unroll
         for (int pp = 0; pp < 8; ++pp) {
-            const int off = q4 ? ((pp & 1) ? 4 + (pp >> 1) : (pp >> 1)) : pp;
-            const float v = row_value(a, xr, m, 32 * b + 8 * g + off, f0, f1, rinv) * down;
-            const _Float16 hv = (_Float16)v;
+            // Q4 fragments take the element order 0, 4, 1, 5, 2, 6, 3, 7 of the nibble dequant
+            const float x = (q4 ? v[gi][(pp & 1) ? 4 + (pp >> 1) : (pp >> 1)] : v[gi][pp]) * down;
+            const _Float16 hv = (_Float16)x;
             hi[pp] = hv;
-            lo[pp] = (_Float16)(v - (float)hv);
+            lo[pp] = (_Float16)(x - (float)hv);
         }
         xf[(((size_t)T * nb + b) * 2 + 0) * 64 + 16 * g + t] = hi;
         xf[(((size_t)T * nb + b) * 2 + 1) * 64 + 16 * g + t] = lo;
     }
-    if (tid == 0) a.xs[m] = ldexpf(1.0f, e);
+    if (tid == 0) a.xs[m] = ldexpf(1.0f, ex);
 }
 
 // ---- the GEMM ----
-// Block: 4 waves over 64 tokens (4 token tiles, shared) x 4*RT row tiles (RT per wave).  The
-// token fragments of each 128-element K step go through LDS (double-buffered: the next step's
-// are loaded while this one's are multiplied), the weights and scales straight into registers
-// one step ahead.
-constexpr int kTT = 4;                         // token tiles per block (all waves)
-constexpr int kStageU4 = kTT * 4 * 2 * 64;     // uint4 per LDS stage: tiles x 4 blocks x hi/lo x lanes
+// Block: 4 waves over TT token tiles (shared by the waves) x 4*RT row tiles (RT per wave).  K runs
+// in stages of one weight piece per row tile (2 quant blocks for Q8, 4 for Q4; TT = 4 and 2
+// keep a stage's token fragments the same size).  Each stage's token fragments, weight pieces
+// and scales are copied global -> LDS by global_load_lds (16 bytes per lane, lane i at base +
+// 16i), into a ring of two buffers.  An iteration waits for its stage, reads all of it into
+// registers, issues the next stage's copies and only then runs the MFMAs, so the copies fly while
+// the matrix cores work (the compiler waits for every outstanding LDS copy before an LDS read).
+template <int QT, int RT>
+struct GemmStage {
+    static constexpr int TT = QT == 0 ? 4 : 2;     // token tiles per block
+    static constexpr int BR = 4 * RT;             // row tiles per block
+    static constexpr int NBS = QT == 0 ? 2 : 4;   // quant blocks per stage
+    static constexpr int A_U4 = TT * NBS * 2 * 64;
+    static constexpr int B_U4 = BR * 64;
+    static constexpr int S_U4 = BR * 16;
+    static constexpr int U4 = A_U4 + B_U4 + S_U4;  // uint4 per stage
+    static constexpr size_t BYTES = 2 * (size_t)U4 * 16;
+};
+
+__device__ __forceinline__ void copy16_to_lds(const void* g, uint4* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
 
 template <int QT, int RT>
-__global__ __launch_bounds__(256, 1) void mgemm_kernel(GemmArgs a, int rpanels, int tpanels) {
-    __shared__ uint4 lds_a[2 * kStageU4];  // 64 KiB
-    constexpr int BR = 4 * RT;             // row tiles per block
-    constexpr int PPQ = QT == 0 ? 2 : 1;   // weight pieces per row tile per K step
+__global__ __launch_bounds__(256, 2) void mgemm_kernel(GemmArgs a, int rpanels, int tpanels) {
+    using G = GemmStage<QT, RT>;
+    constexpr int TT = G::TT, NBS = G::NBS;
+    extern __shared__ __align__(16) uint4 lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // XCD-aware numbering: block b runs on XCD b % 8; give each XCD whole row panels
     const int bid = blockIdx.x;
@@ -224,112 +276,89 @@ __global__ __launch_bounds__(256, 1) void mgemm_kernel(GemmArgs a, int rpanels, 
     const int rp = xcd * per_xcd + idx / tpanels;
     const int tp = idx % tpanels;
     if (rp >= rpanels) return;
-    const int K = a.K, nb = K / 32, nq = K / 128;
+    const int K = a.K, nb = K / 32, nq = K / 128, nst = K / (32 * NBS);
     const int rtiles = (a.N + 15) / 16, mtiles = (a.M + 15) / 16;
     const int j = lane & 15, g = lane >> 4;
-    int R[RT];
-    bool rok[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) {
-        R[r] = rp * BR + wave * RT + r;
-        rok[r] = R[r] < rtiles;
-        if (!rok[r]) R[r] = rtiles - 1;  // a valid address; its results are not stored
-    }
-    const int T0 = tp * kTT;
+    const int R0 = rp * G::BR, T0 = tp * TT;
     const uint4* wq = reinterpret_cast<const uint4*>(a.wq);
     const float4* ws = reinterpret_cast<const float4*>(a.ws);
     const uint4* xf = reinterpret_cast<const uint4*>(a.frags);
-    const int npc = QT == 0 ? K / 64 : K / 128;
+    const int npc = QT == 0 ? K / 64 : K / 128;  // pieces per row tile (= stages)
 
-    // stage qd of the token fragments: chunk i = tid + 256k of the block's 4 runs of 8 KiB
-    // (token tile T0 + (i >> 9), blocks 4qd..4qd+3, hi/lo, lanes), kept in the same order in LDS
-    auto load_a = [&](int qd, uint4 (&r)[8]) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int i = tid + 256 * k;
-            const int T = min(T0 + (i >> 9), mtiles - 1);
-            r[k] = xf[((size_t)T * nb + 4 * qd) * 128 + (i & 511)];
-        }
-    };
-    auto store_a = [&](int buf, const uint4 (&r)[8]) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) lds_a[buf * kStageU4 + tid + 256 * k] = r[k];
-    };
-    auto load_b = [&](int qd, uint4 (&wv)[RT][PPQ], float4 (&sv)[RT]) {
-#pragma unroll
-        for (int r = 0; r < RT; ++r) {
-#pragma unroll
-            for (int pp = 0; pp < PPQ; ++pp) wv[r][pp] = wq[((size_t)R[r] * npc + qd * PPQ + pp) * 64 + lane];
-            sv[r] = ws[((size_t)R[r] * nq + qd) * 16 + j];
+    // one stage: wave instruction c of the stage's U4/64 copies moves 1 KiB
+    auto issue = [&](int st, int buf) {
+        uint4* base = lds + (size_t)buf * G::U4;
+        constexpr int NA = G::A_U4 / 64, NB = G::B_U4 / 64, NS = G::S_U4 / 64;
+        for (int c = wave; c < NA + NB + NS; c += 4) {
+            const void* src;
+            if (c < NA) {  // token tile c / (2 NBS), block c / 2 % NBS, hi/lo c % 2
+                const int t = c / (2 * NBS), bh = c % (2 * NBS);
+                const int T = min(T0 + t, mtiles - 1);
+                src = xf + (((size_t)T * nb + st * NBS) * 2 + bh) * 64 + lane;
+            } else if (c < NA + NB) {  // row tile c - NA
+                const int R = min(R0 + c - NA, rtiles - 1);
+                src = wq + ((size_t)R * npc + st) * 64 + lane;
+            } else {  // scales of 4 row tiles: lane l -> row tile 4(c - NA - NB) + l / 16, row l % 16
+                const int R = min(R0 + 4 * (c - NA - NB) + (lane >> 4), rtiles - 1);
+                src = ws + ((size_t)R * nq + st * NBS / 4) * 16 + (lane & 15);
+            }
+            copy16_to_lds(src, base + c * 64);
         }
     };
 
-    f32x4_t acc[RT][kTT];
+    f32x4_t acc[RT][TT];
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int t = 0; t < kTT; ++t) acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < TT; ++t) acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    uint4 wv[RT][PPQ], wn[RT][PPQ];
-    float4 sv[RT], sn[RT];
-    {
-        uint4 ra[8];
-        load_a(0, ra);
-        load_b(0, wv, sv);
-        store_a(0, ra);
-    }
-    __syncthreads();
-    for (int qd = 0; qd < nq; ++qd) {
-        const int buf = qd & 1;
-        const bool more = qd + 1 < nq;
-        uint4 ra[8];
-        if (more) {
-            load_a(qd + 1, ra);
-            load_b(qd + 1, wn, sn);
-        }
-        const uint4* la = lds_a + buf * kStageU4;
+    issue(0, 0);
+    for (int st = 0; st < nst; ++st) {
+        const int buf = st & 1;
+        // stage st has landed for every wave, and every wave has read stage st - 1's buffer
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        const uint4* la = lds + (size_t)buf * G::U4;
+        const uint4* lb = la + G::A_U4;
+        const float4* lsc = reinterpret_cast<const float4*>(lb + G::B_U4);
+        half8_t xh[NBS][TT], xl[NBS][TT];
+        uint4 wv[RT];
+        float4 sv[RT];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            half8_t xh[kTT], xl[kTT];
+        for (int b = 0; b < NBS; ++b)
 #pragma unroll
-            for (int t = 0; t < kTT; ++t) {
-                xh[t] = __builtin_bit_cast(half8_t, la[t * 512 + (2 * b) * 64 + lane]);
-                xl[t] = __builtin_bit_cast(half8_t, la[t * 512 + (2 * b + 1) * 64 + lane]);
+            for (int t = 0; t < TT; ++t) {
+                xh[b][t] = __builtin_bit_cast(half8_t, la[((t * NBS + b) * 2) * 64 + lane]);
+                xl[b][t] = __builtin_bit_cast(half8_t, la[((t * NBS + b) * 2 + 1) * 64 + lane]);
             }
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            wv[r] = lb[(wave * RT + r) * 64 + lane];
+            sv[r] = lsc[(wave * RT + r) * 16 + j];
+        }
+        if (st + 1 < nst) issue(st + 1, buf ^ 1);
+#pragma unroll
+        for (int b = 0; b < NBS; ++b) {
+            const int sb = (st * NBS + b) & 3;  // block inside the scales' group of 4
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 half8_t wh;
-                if constexpr (QT == 0) {
-                    const uint4 w = wv[r][b >> 1];
-                    wh = (b & 1) ? q8_to_h8(w.z, w.w) : q8_to_h8(w.x, w.y);
-                } else {
-                    const uint4 w = wv[r][0];
-                    wh = q4_to_h8(b == 0 ? w.x : b == 1 ? w.y : b == 2 ? w.z : w.w);
-                }
-                const float sc = b == 0 ? sv[r].x : b == 1 ? sv[r].y : b == 2 ? sv[r].z : sv[r].w;
+                if constexpr (QT == 0) wh = b ? q8_to_h8(wv[r].z, wv[r].w) : q8_to_h8(wv[r].x, wv[r].y);
+                else wh = q4_to_h8(b == 0 ? wv[r].x : b == 1 ? wv[r].y : b == 2 ? wv[r].z : wv[r].w);
+                const float sc = sb == 0 ? sv[r].x : sb == 1 ? sv[r].y : sb == 2 ? sv[r].z : sv[r].w;
 #pragma unroll
-                for (int t = 0; t < kTT; ++t) {
-                    f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[t], wh, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[t], wh, d, 0, 0, 0);
+                for (int t = 0; t < TT; ++t) {
+                    f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[b][t], wh, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl[b][t], wh, d, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[r][t][i] = fmaf(sc, d[i], acc[r][t][i]);
                 }
             }
         }
-        if (more) {
-            store_a(buf ^ 1, ra);
-#pragma unroll
-            for (int r = 0; r < RT; ++r) {
-#pragma unroll
-                for (int pp = 0; pp < PPQ; ++pp) wv[r][pp] = wn[r][pp];
-                sv[r] = sn[r];
-            }
-        }
-        __syncthreads();
     }
     // lane (n = j, g) holds tokens 4g..4g+3 of each token tile
 #pragma unroll
-    for (int t = 0; t < kTT; ++t) {
+    for (int t = 0; t < TT; ++t) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int m = 16 * (T0 + t) + 4 * g + i;
@@ -338,11 +367,24 @@ __global__ __launch_bounds__(256, 1) void mgemm_kernel(GemmArgs a, int rpanels, 
             float* yr = a.y + (size_t)m * a.y_stride + a.n_off;
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                const int n = 16 * R[r] + j;
-                if (rok[r] && n < a.N) yr[n] = acc[r][t][i] * xs;
+                const int R = R0 + wave * RT + r;
+                const int n = 16 * R + j;
+                if (R < rtiles && n < a.N) yr[n] = acc[r][t][i] * xs;
             }
         }
     }
+}
+
+template <int QT, int RT>
+int gemm_launch(const GemmArgs& a, int rpanels, int tpanels, hipStream_t s) {
+    using G = GemmStage<QT, RT>;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&mgemm_kernel<QT, RT>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)G::BYTES);
+    if (attr != hipSuccess) return -2;
+    const int blocks = 8 * ((rpanels + 7) / 8) * tpanels;
+    hipLaunchKernelGGL((mgemm_kernel<QT, RT>), dim3(blocks), dim3(256), G::BYTES, s, a, rpanels, tpanels);
+    return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 }  // namespace
@@ -371,26 +413,25 @@ int launch_rows_to_frags(const RowsArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.K % 128 || !a.frags || !a.xs) return -1;
     if (a.mode == ROWS_GNORM && (a.K % 128 || !a.ssq)) return -1;
     const int mpad = (a.M + 15) / 16 * 16;
-    hipLaunchKernelGGL(rows_to_frags_kernel, dim3(mpad), dim3(kRowThreads), 0, s, a);
+    const int gpt = (a.K / 8 + kRowThreads - 1) / kRowThreads;
+    if (gpt <= 2) hipLaunchKernelGGL(rows_to_frags_kernel<2>, dim3(mpad), dim3(kRowThreads), 0, s, a);
+    else if (gpt <= 4) hipLaunchKernelGGL(rows_to_frags_kernel<4>, dim3(mpad), dim3(kRowThreads), 0, s, a);
+    else if (gpt <= 6) hipLaunchKernelGGL(rows_to_frags_kernel<6>, dim3(mpad), dim3(kRowThreads), 0, s, a);
+    else if (gpt <= 8) hipLaunchKernelGGL(rows_to_frags_kernel<8>, dim3(mpad), dim3(kRowThreads), 0, s, a);
+    else return -1;  // rows longer than 16384
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
 int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0 || a.K % 128 || !a.wq || !a.ws || !a.frags || !a.xs || !a.y) return -1;
     const int rtiles = (a.N + 15) / 16, mtiles = (a.M + 15) / 16;
+    const int tt = quant == 0 ? GemmStage<0, 4>::TT : GemmStage<1, 4>::TT;
+    const int tpanels = (mtiles + tt - 1) / tt;
     // 16 row tiles per block for wide matrices, 8 when that leaves too few blocks for the CUs
-    const bool wide = (size_t)((rtiles + 15) / 16) * ((mtiles + kTT - 1) / kTT) >= 192;
-    const int br = wide ? 16 : 8;
-    const int rpanels = (rtiles + br - 1) / br, tpanels = (mtiles + kTT - 1) / kTT;
-    const int blocks = 8 * ((rpanels + 7) / 8) * tpanels;
-    if (quant == 0) {
-        if (wide) hipLaunchKernelGGL((mgemm_kernel<0, 4>), dim3(blocks), dim3(256), 0, s, a, rpanels, tpanels);
-        else hipLaunchKernelGGL((mgemm_kernel<0, 2>), dim3(blocks), dim3(256), 0, s, a, rpanels, tpanels);
-    } else {
-        if (wide) hipLaunchKernelGGL((mgemm_kernel<1, 4>), dim3(blocks), dim3(256), 0, s, a, rpanels, tpanels);
-        else hipLaunchKernelGGL((mgemm_kernel<1, 2>), dim3(blocks), dim3(256), 0, s, a, rpanels, tpanels);
-    }
-    return hipGetLastError() == hipSuccess ? 0 : -2;
+    const bool wide = (size_t)((rtiles + 15) / 16) * tpanels >= 192;
+    const int rpanels = wide ? (rtiles + 15) / 16 : (rtiles + 7) / 8;
+    if (quant == 0) return wide ? gemm_launch<0, 4>(a, rpanels, tpanels, s) : gemm_launch<0, 2>(a, rpanels, tpanels, s);
+    return wide ? gemm_launch<1, 4>(a, rpanels, tpanels, s) : gemm_launch<1, 2>(a, rpanels, tpanels, s);
 }
 
 }  // namespace snl

@@ -6,9 +6,10 @@
 // at once (dn_conv_kernel, one block per (token, head)); the conv state then takes the chunk's
 // last three inputs (dn_conv_state_kernel).  The recurrence itself runs token by token in
 // dn_recur_kernel with the decode kernel's thread layout: 4 blocks per value head, each owning
-// 32 state columns in registers, so a column's arithmetic is exactly the decode step's.  The
-// next token's inputs are loaded while the current one is computed.  The state is updated in
-// place in the current slot (a prefill pass has no checkpoint).
+// 32 state columns in registers, with the decode step's per-column arithmetic; the sums over a
+// column's 128 rows run as DPP rotations inside 16-lane rows plus two cross-row exchanges.  The
+// tokens' inputs stream through LDS in slices of 16.  The state is updated in place in the
+// current slot (a prefill pass has no checkpoint).
 #include "common.h"
 #include "kernels.h"
 
@@ -107,9 +108,28 @@ __global__ __launch_bounds__(256) void dn_conv_state_kernel(DnPrefillArgs a, int
     for (int i = 0; i < 3; ++i) a.conv_state[(size_t)i * cd + ch] = r[i];
 }
 
-// The recurrence over the chunk (linear.wgsl:118-136), 4 blocks per value head.
+// Sum over the 16 row groups (lane >> 2) of the lanes that share lane & 3: rotations by 4 and 8
+// inside each 16-lane row (DPP), then the two rows of each half and the two halves.
+__device__ __forceinline__ float rowgroup_sum(float v) {
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+    v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+    v = v + __shfl_xor(v, 16, 64);
+    v = v + __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// The recurrence over the chunk (linear.wgsl:118-136), 4 blocks per value head.  The tokens'
+// inputs pass through LDS in slices of kTok tokens, the next slice loaded while this one runs.
+constexpr int kTok = 16;
+struct RecurSlice {
+    float q[kTok][DK], k[kTok][DK];
+    float v[kTok][kCols], gz[kTok][kCols];
+    float beta[kTok], decay[kTok];
+};
+
 __global__ __launch_bounds__(kThreads) void dn_recur_kernel(DnPrefillArgs a, int M) {
     extern __shared__ float ored[];  // [kWaves][M]
+    __shared__ RecurSlice sl[2];
     const int h = blockIdx.x / kCG, cg = blockIdx.x % kCG;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = lane & 3, rg = lane >> 2;
@@ -122,50 +142,95 @@ __global__ __launch_bounds__(kThreads) void dn_recur_kernel(DnPrefillArgs a, int
     for (int r = 0; r < kRows; ++r) s[r] = S[(size_t)(kRows * rg + r) * DV + j];
     const float norm_w = a.lw[(size_t)a.conv_dim * 4 + 2 * n_v + j];
 
-    auto load = [&](int m, float4 (&qv)[2], float4 (&kv)[2], float& vj, float& be, float& de, float& gz) {
-        const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)m * n_k + kh) * DK + kRows * rg);
-        const float4* kp = reinterpret_cast<const float4*>(a.k + ((size_t)m * n_k + kh) * DK + kRows * rg);
-        qv[0] = qp[0], qv[1] = qp[1];
-        kv[0] = kp[0], kv[1] = kp[1];
-        vj = a.v[((size_t)m * n_v + h) * DV + j];
-        be = a.beta[(size_t)m * n_v + h];
-        de = a.decay[(size_t)m * n_v + h];
-        gz = a.gz[((size_t)m * n_v + h) * DV + j];
+    // slice loader: thread t takes q/k float4 t (kTok * 2 * DK / 4 = 1024 of them, two per
+    // thread), then v/gz of the group's columns and the per-token scalars
+    float4 rq[2];
+    float rv = 0.0f, rb = 0.0f;
+    auto load = [&](int m0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int f = tid + kThreads * u;  // 0..1023
+            const int which = f >> 9, rem = f & 511, tk = rem >> 5, d4 = rem & 31;
+            const int m = min(m0 + tk, M - 1);
+            const float* src = (which ? a.k : a.q) + ((size_t)m * n_k + kh) * DK;
+            rq[u] = reinterpret_cast<const float4*>(src)[d4];
+        }
+        {   // kTok * kCols = 512 values of v, one per thread
+            const int tk = tid / kCols, col = tid % kCols;
+            const int m = min(m0 + tk, M - 1);
+            rv = a.v[((size_t)m * n_v + h) * DV + cg * kCols + col];
+        }
+        {
+            const int tk = tid & (kTok - 1), m = min(m0 + tk, M - 1);
+            rb = tid < kTok ? a.beta[(size_t)m * n_v + h] : tid < 2 * kTok ? a.decay[(size_t)m * n_v + h] : 0.0f;
+        }
     };
-    float4 qn[2], kn[2];
-    float vn, ben, den, gzn;
-    load(0, qn, kn, vn, ben, den, gzn);
-    for (int m = 0; m < M; ++m) {
-        const float qf[8] = {qn[0].x, qn[0].y, qn[0].z, qn[0].w, qn[1].x, qn[1].y, qn[1].z, qn[1].w};
-        const float kf[8] = {kn[0].x, kn[0].y, kn[0].z, kn[0].w, kn[1].x, kn[1].y, kn[1].z, kn[1].w};
-        const float vj = vn, beta = ben, decay = den, gz = gzn;
-        if (m + 1 < M) load(m + 1, qn, kn, vn, ben, den, gzn);
-        float kv = 0.0f;
+    float rg2 = 0.0f;
+    auto load_gz = [&](int m0) {
+        const int tk = tid / kCols, col = tid % kCols;
+        const int m = min(m0 + tk, M - 1);
+        rg2 = a.gz[((size_t)m * n_v + h) * DV + cg * kCols + col];
+    };
+    auto store = [&](RecurSlice& d) {
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            s[r] = s[r] * decay;
-            kv = fmaf(s[r], kf[r], kv);
+        for (int u = 0; u < 2; ++u) {
+            const int f = tid + kThreads * u;
+            const int which = f >> 9, rem = f & 511, tk = rem >> 5, d4 = rem & 31;
+            reinterpret_cast<float4*>(which ? d.k[tk] : d.q[tk])[d4] = rq[u];
         }
-#pragma unroll
-        for (int sh = 4; sh < 64; sh <<= 1) kv = kv + __shfl_xor(kv, sh, 64);
-        const float dlt = (vj - kv) * beta;
-        float o = 0.0f;
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) {
-            s[r] = fmaf(kf[r], dlt, s[r]);
-            o = fmaf(s[r], qf[r], o);
+        d.v[tid / kCols][tid % kCols] = rv;
+        d.gz[tid / kCols][tid % kCols] = rg2;
+        if (tid < kTok) d.beta[tid] = rb;
+        else if (tid < 2 * kTok) d.decay[tid - kTok] = rb;
+    };
+    load(0);
+    load_gz(0);
+    store(sl[0]);
+    __syncthreads();
+    for (int m0 = 0; m0 < M; m0 += kTok) {
+        const int cur = (m0 / kTok) & 1;
+        const bool more = m0 + kTok < M;
+        if (more) {
+            load(m0 + kTok);
+            load_gz(m0 + kTok);
         }
+        const RecurSlice& d = sl[cur];
+        const int n = min(kTok, M - m0);
+        for (int tk = 0; tk < n; ++tk) {
+            const float4* qp = reinterpret_cast<const float4*>(d.q[tk] + kRows * rg);
+            const float4* kp = reinterpret_cast<const float4*>(d.k[tk] + kRows * rg);
+            const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+            const float qf[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            const float kf[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            const float decay = d.decay[tk], beta = d.beta[tk];
+            float kv = 0.0f;
 #pragma unroll
-        for (int sh = 4; sh < 64; sh <<= 1) o = o + __shfl_xor(o, sh, 64);
-        if (rg == 0) a.out[(size_t)m * n_v * DV + h * DV + j] = (o * norm_w) * gz;
-        float q2 = o * o;
-        q2 = q2 + __shfl_xor(q2, 1, 64);
-        q2 = q2 + __shfl_xor(q2, 2, 64);
-        if (lane == 0) ored[wave * M + m] = q2;
+            for (int r = 0; r < kRows; ++r) {
+                s[r] = s[r] * decay;
+                kv = fmaf(s[r], kf[r], kv);
+            }
+            kv = rowgroup_sum(kv);
+            const float dlt = (d.v[tk][jl] - kv) * beta;
+            float o = 0.0f;
+#pragma unroll
+            for (int r = 0; r < kRows; ++r) {
+                s[r] = fmaf(kf[r], dlt, s[r]);
+                o = fmaf(s[r], qf[r], o);
+            }
+            o = rowgroup_sum(o);
+            const int m = m0 + tk;
+            if (rg == 0) a.out[(size_t)m * n_v * DV + h * DV + j] = (o * norm_w) * d.gz[tk][jl];
+            float q2 = o * o;
+            q2 = q2 + __shfl_xor(q2, 1, 64);
+            q2 = q2 + __shfl_xor(q2, 2, 64);
+            if (lane == 0) ored[wave * M + m] = q2;
+        }
+        __syncthreads();  // every wave is done with sl[cur ^ 1]'s previous contents
+        if (more) store(sl[cur ^ 1]);
+        __syncthreads();
     }
 #pragma unroll
     for (int r = 0; r < kRows; ++r) S[(size_t)(kRows * rg + r) * DV + j] = s[r];
-    __syncthreads();
     for (int m = tid; m < M; m += kThreads) {
         float t = 0.0f;
 #pragma unroll
