@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_frags_kernel(RowsArgs a) 
 // the matrix cores work (the compiler waits for every outstanding LDS copy before an LDS read).
 template <int QT, int RT>
 struct GemmStage {
-    static constexpr int TT = QT == 0 ? 4 : 2;     // token tiles per block
+    static constexpr int TT = QT == 0 && RT == 4 ? 4 : 2;  // token tiles per block
     static constexpr int BR = 4 * RT;             // row tiles per block
     static constexpr int NBS = QT == 0 ? 2 : 4;   // quant blocks per stage
     static constexpr int A_U4 = TT * NBS * 2 * 64;
@@ -425,10 +425,12 @@ int launch_rows_to_frags(const RowsArgs& a, hipStream_t s) {
 int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0 || a.K % 128 || !a.wq || !a.ws || !a.frags || !a.xs || !a.y) return -1;
     const int rtiles = (a.N + 15) / 16, mtiles = (a.M + 15) / 16;
-    const int tt = quant == 0 ? GemmStage<0, 4>::TT : GemmStage<1, 4>::TT;
+    // 16 row tiles per block for wide matrices, 8 (and 2 token tiles) when that leaves too few
+    // blocks for the CUs
+    const int tt_w = quant == 0 ? GemmStage<0, 4>::TT : GemmStage<1, 4>::TT;
+    const bool wide = (size_t)((rtiles + 15) / 16) * ((mtiles + tt_w - 1) / tt_w) >= 192;
+    const int tt = wide ? tt_w : 2;
     const int tpanels = (mtiles + tt - 1) / tt;
-    // 16 row tiles per block for wide matrices, 8 when that leaves too few blocks for the CUs
-    const bool wide = (size_t)((rtiles + 15) / 16) * tpanels >= 192;
     const int rpanels = wide ? (rtiles + 15) / 16 : (rtiles + 7) / 8;
     if (quant == 0) return wide ? gemm_launch<0, 4>(a, rpanels, tpanels, s) : gemm_launch<0, 2>(a, rpanels, tpanels, s);
     return wide ? gemm_launch<1, 4>(a, rpanels, tpanels, s) : gemm_launch<1, 2>(a, rpanels, tpanels, s);
