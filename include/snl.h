@@ -200,6 +200,53 @@ int snl_worker_run(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at
 /* The cache bookkeeping: live length, and per slot the key count (-1 = empty) and last use. */
 int snl_worker_cache(const snl_worker* w, int* live_len, int* snap_len, uint64_t* snap_used);
 
+/* ---- sampling (src/sampler.rs) ------------------------------------------------------------ */
+
+/* SamplingParams (src/sampler.rs:4-29).  temperature <= 1e-5 is greedy; top_k 0 = no top-k. */
+typedef struct snl_sampling {
+    float temperature, top_p, min_p, presence_penalty, frequency_penalty, repetition_penalty;
+    int32_t top_k, _pad;
+} snl_sampling;
+
+/* The reference's StdRng (rand 0.10.3: ChaCha12 keyed by seed_from_u64) as used by Sampler:
+ * snl_rng_f32 is random::<f32>().  snl_chacha_block is the block function (rounds 12 or 20). */
+typedef struct snl_rng {
+    uint32_t key[8];
+    uint64_t counter;
+    uint32_t buf[16];
+    int32_t idx, _pad;
+} snl_rng;
+void snl_chacha_block(const uint32_t in[16], int rounds, uint32_t out[16]);
+void snl_rng_seed(snl_rng* r, uint64_t seed);
+uint32_t snl_rng_u32(snl_rng* r);
+float snl_rng_f32(snl_rng* r);
+/* Sampler::draw (src/sampler.rs:143-158) over a normalised list, excluding `exclude` (-1: none),
+ * with the uniform u; and the tail of Sampler::distribution (:111-140) over candidate logits in
+ * descending order (temperature softmax, min-p, top-p, renormalisation): probs[n] receives the
+ * probabilities, the return value is how many are kept. */
+uint32_t snl_draw(const uint32_t* tokens, const float* probs, int n, int64_t exclude, float u);
+int snl_finish_distribution(const float* logits, int n, float temperature, float min_p, float top_p, float* probs);
+
+/* Sampler (src/sampler.rs:32-96) over logits row `row` (0 or 1) of the engine's last forward: the
+ * penalties and top-k run on the device (only k candidates are read back; top_k 0 or above 1024
+ * reads the row back), the rest on the host.  accept() records a generated token for the
+ * penalties; sample() and verify() are Sampler::sample / Sampler::verify (accept the draft with
+ * probability p(draft), else draw from p without it); distribution() returns the kept list.
+ * has_seed = 0 seeds from the OS, as StdRng::from_rng does. */
+typedef struct snl_sampler snl_sampler;
+int snl_sampler_create(snl_engine* e, const snl_sampling* p, uint64_t seed, int has_seed, snl_sampler** out);
+void snl_sampler_destroy(snl_sampler* s);
+void snl_sampler_accept(snl_sampler* s, uint32_t token);
+int snl_sampler_sample(snl_sampler* s, int row, uint32_t* token);
+int snl_sampler_verify(snl_sampler* s, int row, uint32_t draft, int* accepted, uint32_t* token);
+int snl_sampler_distribution(snl_sampler* s, int row, uint32_t* tokens, float* probs, int cap, int* n_out);
+
+/* Worker::run with the request's SamplingParams (src/worker.rs:193-252): as snl_worker_run, the
+ * tokens drawn by a Sampler seeded with `seed` (has_seed = 0: from the OS).  Greedy parameters
+ * without penalties take snl_worker_run's path. gaps are not reported. */
+int snl_worker_run_sampled(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at, int max_tokens, int spec,
+                           const snl_sampling* params, uint64_t seed, int has_seed, uint32_t* out, snl_finish* fin);
+
 /* ---- inspection (tests) ------------------------------------------------------------------- */
 
 /* Shape of a generated tensor: layer -1 = embed(1)/lm_head(2)/norm(3); layer 0xFFF = MTP

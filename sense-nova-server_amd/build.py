@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libsnl.so")
 BUILD = os.path.join(os.path.dirname(HERE), "_build")
 SOURCES = ["gemv.hip", "mgemv.hip", "mgemm.hip", "gemv_ksplit.hip", "layers.hip", "deltanet.hip", "attention.hip", "attention_prefill.hip", "prefill.hip", "init.hip", "engine.cpp",
-           "snl_file.cpp", "worker.cpp"]
+           "snl_file.cpp", "worker.cpp", "sampler.hip", "sampler.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
          # packed FP32 instructions stay off (their results were unreliable on these parts)

@@ -35,6 +35,7 @@ namespace {
 
 constexpr int kSnapshots = SNL_SNAPSHOTS;
 constexpr int kLogitRows = 2;
+constexpr int kDistMax = 1024;  // largest k the device top-k serves (SNL_DIST_MAX)
 // Token rows per captured pass.  The kernels take up to SNL_MAX_M; passes use 1 or 2.
 constexpr int kMaxM = 2;
 
@@ -173,6 +174,11 @@ struct snl_engine {
 
     int cur = 0, ck_slot = -1;
     int pos = 0, hid_rows = 0;
+    int logit_rows = 0;  // logits rows the last forward left in `logits`
+    // sampler scratch: top-k keys, penalty lists, pinned readback
+    unsigned long long* topk_keys = nullptr;
+    uint32_t* pen_dev = nullptr;       // [2][vocab]: tokens, counts
+    unsigned long long* topk_host = nullptr;  // pinned, kDistMax keys
     // Counts the calls that change the caches, the recurrent state or a snapshot slot, so that a
     // holder of cache bookkeeping (the worker) can tell whether someone else has moved the engine.
     uint64_t epoch = 0;
@@ -590,6 +596,11 @@ int snl_engine::init() {
         (rc = dalloc(&pick_scratch, pick_scratch_floats(c.vocab, kLogitRows))) || (rc = dalloc(&d_picks, 2)) ||
         (rc = dalloc(&d_mpick, 1)) || (rc = dalloc(&d_step, 1)) || (rc = dalloc(&d_mstep, 1)))
         return rc;
+    // ---- sampler scratch ----
+    if ((rc = dalloc(&topk_keys, topk_scratch_keys(c.vocab, kDistMax))) || (rc = dalloc(&pen_dev, (size_t)2 * c.vocab)))
+        return rc;
+    if (hipHostMalloc((void**)&topk_host, kDistMax * sizeof(unsigned long long), hipHostMallocDefault) != hipSuccess)
+        return fail(SNL_ENOMEM, "pinned host allocation failed");
     // ---- chunked prefill rows ----
     {
         const size_t P = SNL_PF_M;
@@ -1100,6 +1111,7 @@ void snl_engine_destroy(snl_engine* e) {
     if (e->h_picks) hipHostFree(e->h_picks);
     if (e->h_step) hipHostFree(e->h_step);
     if (e->h_pstep) hipHostFree(e->h_pstep);
+    if (e->topk_host) hipHostFree(e->topk_host);
     if (e->stream) hipStreamDestroy(e->stream);
     delete e;
 }
@@ -1169,6 +1181,7 @@ int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* po
         e->pos += n;
         e->hid_rows = n;
     }
+    e->logit_rows = rows;
     if (rows > 0) {
         if (logits_out &&
             hipMemcpy(logits_out, e->logits, sizeof(float) * rows * e->cfg.vocab, hipMemcpyDeviceToHost) != hipSuccess)
@@ -1401,6 +1414,59 @@ namespace snl {
 uint64_t engine_epoch(const snl_engine* e) { return e->epoch; }
 
 int engine_fail(snl_engine* e, int code, const char* msg) { return e->fail(code, "%s", msg); }
+
+int engine_vocab(const snl_engine* e) { return e->cfg.vocab; }
+
+// Penalties on logits row `row` of the last forward (in place, as the reference mutates its logits),
+// then its k largest entries (value descending, index ascending on ties): k <= kDistMax on the
+// device; otherwise (k == 0: the whole vocabulary) the row is read back and sorted here.
+int engine_top(snl_engine* e, int row, const uint32_t* pen_tok, const uint32_t* pen_cnt, int n_pen, float rep,
+               float presence, float frequency, int k, std::vector<uint32_t>* tok, std::vector<float>* val) {
+    const int V = e->cfg.vocab;
+    if (row < 0 || row >= e->logit_rows) return e->fail(SNL_ESTATE, "no logits row %d from the last forward", row);
+    if (n_pen < 0 || n_pen > V) return e->fail(SNL_EARG, "penalty list longer than the vocabulary");
+    float* lr = e->logits + (size_t)row * V;
+    if (n_pen > 0) {
+        if (hipMemcpyAsync(e->pen_dev, pen_tok, (size_t)n_pen * 4, hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+            hipMemcpyAsync(e->pen_dev + V, pen_cnt, (size_t)n_pen * 4, hipMemcpyHostToDevice, e->stream) != hipSuccess ||
+            launch_penalties(lr, V, e->pen_dev, e->pen_dev + V, n_pen, rep, presence, frequency, e->stream))
+            return e->fail(SNL_EDEVICE, "penalty launch failed");
+    }
+    if (k <= 0 || k > V) k = V;
+    tok->resize(k);
+    val->resize(k);
+    if (k <= kDistMax) {
+        unsigned long long* res = nullptr;
+        if (launch_topk(lr, V, k, e->topk_keys, &res, e->stream) ||
+            hipMemcpyAsync(e->topk_host, res, (size_t)k * 8, hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
+            hipStreamSynchronize(e->stream) != hipSuccess)
+            return e->fail(SNL_EDEVICE, "top-k failed");
+        for (int i = 0; i < k; ++i) {
+            const unsigned long long key = e->topk_host[i];
+            const uint32_t ob = (uint32_t)(key >> 32);
+            const uint32_t bits = (ob & 0x80000000u) ? (ob & 0x7FFFFFFFu) : ~ob;
+            (*tok)[i] = 0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull);
+            float v;
+            memcpy(&v, &bits, 4);
+            (*val)[i] = v;
+        }
+        return SNL_OK;
+    }
+    std::vector<float> host(V);
+    if (hipMemcpyAsync(host.data(), lr, (size_t)V * 4, hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
+        hipStreamSynchronize(e->stream) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "logits readback failed");
+    std::vector<uint32_t> idx(V);
+    for (int i = 0; i < V; ++i) idx[i] = (uint32_t)i;
+    std::sort(idx.begin(), idx.end(), [&](uint32_t a, uint32_t b) {
+        return host[a] > host[b] || (host[a] == host[b] && a < b);
+    });
+    for (int i = 0; i < k; ++i) {
+        (*tok)[i] = idx[i];
+        (*val)[i] = host[idx[i]];
+    }
+    return SNL_OK;
+}
 
 }  // namespace snl
 

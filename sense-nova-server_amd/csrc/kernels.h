@@ -189,6 +189,16 @@ struct DnPrefillArgs {
 };
 int launch_deltanet_prefill(const DnPrefillArgs& a, int M, hipStream_t s);
 
+// ---------------------------------------------------------------- sampler (sampler.hip)
+// src/sampler.rs:99-106: repetition, presence and frequency penalties on logits[tok[i]] in place
+int launch_penalties(float* logits, int V, const uint32_t* tok, const uint32_t* cnt, int n, float rep, float presence,
+                     float frequency, hipStream_t s);
+// the k (<= 2048) largest entries as keys (order bits of the value << 32 | ~index), descending;
+// *result points into scratch (topk_scratch_keys(V, k) keys)
+size_t topk_scratch_keys(int V, int k);
+int launch_topk(const float* logits, int V, int k, unsigned long long* scratch, unsigned long long** result,
+                hipStream_t s);
+
 // ---------------------------------------------------------------- gated attention (attention.hip)
 struct AttnArgs {
     const float* proj;   // [M, proj_stride] q+gate | k | v

@@ -9,7 +9,8 @@
 //     continuing live, restoring the snapshot with the longest strict prefix, or resetting, and
 //     the optional snapshot taken part-way through a prompt;
 //   * the speculation self-pause (src/worker.rs:222-234) and the error reset of the request
-//     loop (src/worker.rs:94-101).
+//     loop (src/worker.rs:94-101);
+//   * the same loop with a Sampler (sampler.cpp) for non-greedy SamplingParams.
 //
 // Only text prompts are fed, so a token's prefix-cache key is its id and token i of a prompt
 // sits at rotary position (i, i, i).
@@ -164,9 +165,13 @@ size_t shared_prefix(const std::vector<uint32_t>& cached, const uint32_t* prompt
     return cached.size() < n && std::equal(cached.begin(), cached.end(), prompt) ? cached.size() : 0;
 }
 
-// Worker::run for one text prompt with greedy sampling (src/worker.rs:123-272).
+int decode_sampled(snl_worker* w, snl_sampler* smp, int n, bool spec, const std::vector<uint32_t>& eos,
+                   int max_tokens, uint32_t* out, int* n_gen, bool* stopped, snl_gen_stats* st);
+
+// Worker::run for one text prompt (src/worker.rs:123-272), greedy on the device picks, or with a
+// Sampler when smp is given.
 int run(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at, int max_tokens, int spec, uint32_t* out,
-        float* gaps, snl_finish* fin) {
+        float* gaps, snl_finish* fin, snl_sampler* smp = nullptr) {
     snl_engine* e = w->e;
     const int ctx = snl_ctx(e);
     if (n <= 0) return snl::engine_fail(e, SNL_EARG, "empty prompt");
@@ -238,23 +243,121 @@ int run(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at, int max_t
     w->live.assign(prompt, prompt + n);
     const auto t1 = clk::now();
 
-    snl_decoder* d = begin(e, n, draft, pick);
     int generated = 0;
     bool stopped = false;
-    rc = decode(d, eos_ids(e), max_tokens, out, gaps, &generated, &stopped, &w->live,
-                w->self_pause ? &w->spec_pause : nullptr);
+    snl_gen_stats st{};
+    if (smp) {
+        rc = decode_sampled(w, smp, n, draft, eos_ids(e), max_tokens, out, &generated, &stopped, &st);
+    } else {
+        snl_decoder* d = begin(e, n, draft, pick);
+        rc = decode(d, eos_ids(e), max_tokens, out, gaps, &generated, &stopped, &w->live,
+                    w->self_pause ? &w->spec_pause : nullptr);
+        st = d->st;
+        snl_decoder_destroy(d);
+    }
     if (!rc && fin) {
         fin->reason = stopped ? 1 : 0;
         fin->prompt_tokens = n;
         fin->completion_tokens = generated;
         fin->cached_tokens = (int32_t)cached;
-        fin->drafted = d->st.drafted;
-        fin->accepted = d->st.accepted;
+        fin->drafted = st.drafted;
+        fin->accepted = st.accepted;
         fin->prefill_s = secs(t0, t1);
         fin->decode_s = secs(t1, clk::now());
     }
-    snl_decoder_destroy(d);
     return rc;
+}
+
+// The loop of src/worker.rs:193-252 with a Sampler: the first token is sampled from the prompt's
+// last logits row; each step emits the pending token, records it for the penalties, drafts with
+// the MTP head (greedy), verifies [token, draft] in one 2-row pass with Sampler::verify on row 0,
+// and on acceptance samples the next token from row 1, else rolls back and keeps verify's draw.
+int decode_sampled(snl_worker* w, snl_sampler* smp, int n, bool spec, const std::vector<uint32_t>& eos,
+                   int max_tokens, uint32_t* out, int* n_gen, bool* stopped, snl_gen_stats* st) {
+    snl_engine* e = w->e;
+    auto is_eos = [&](uint32_t t) { return std::find(eos.begin(), eos.end(), t) != eos.end(); };
+    int rc;
+    uint32_t tok = 0;
+    if ((rc = snl_sampler_sample(smp, 0, &tok))) return rc;
+    int mr0 = snl_hid_rows(e), mn = 1, mslot = n - 1;
+    uint32_t mtok[2] = {tok, 0}, mpos[6] = {(uint32_t)(n - 1), (uint32_t)(n - 1), (uint32_t)(n - 1), 0, 0, 0};
+    uint32_t rope = (uint32_t)n;
+    int generated = 0;
+    *stopped = false;
+    double draft_s = 0.0, verify_s = 0.0;
+    for (;;) {
+        // Emit::push (src/worker.rs:347-381): the token that ends generation is not fed
+        out[generated++] = tok;
+        if (is_eos(tok)) {
+            *stopped = true;
+            break;
+        }
+        if (generated >= max_tokens) break;
+        snl_sampler_accept(smp, tok);
+        const auto ts = clk::now();
+        uint32_t d = 0;
+        if (spec && (rc = snl_mtp(e, mr0, mtok, mn, mpos, mslot, 1, &d, nullptr, nullptr))) return rc;
+        const auto tb = clk::now();
+        draft_s += secs(ts, tb);
+        if (!spec) {
+            uint32_t p1[3] = {rope, rope, rope};
+            if ((rc = snl_forward(e, &tok, 1, p1, 1, 0, nullptr, nullptr))) return rc;
+            w->live.push_back(tok);
+            rope += 1;
+            if ((rc = snl_sampler_sample(smp, 0, &tok))) return rc;
+            continue;
+        }
+        const int slot = snl_pos(e);
+        uint32_t pair[2] = {tok, d};
+        uint32_t p2[6] = {rope, rope, rope, rope + 1, rope + 1, rope + 1};
+        if ((rc = snl_forward(e, pair, 2, p2, 2, 1, nullptr, nullptr))) return rc;
+        verify_s += secs(tb, clk::now());
+        st->drafted++;
+        const int accepted_before = st->accepted;
+        if (w->self_pause && st->drafted == kSpecTrial && draft_s > verify_s * accepted_before / st->drafted) {
+            spec = false;  // src/worker.rs:222-234
+            w->spec_pause = kSpecPause;
+        }
+        int ok = 0;
+        uint32_t next = 0;
+        if ((rc = snl_sampler_verify(smp, 0, d, &ok, &next))) return rc;
+        w->live.push_back(tok);
+        if (ok) {
+            st->accepted++;
+            w->live.push_back(d);
+            out[generated++] = d;
+            if (is_eos(d)) {
+                *stopped = true;
+                break;
+            }
+            if (generated >= max_tokens) break;
+            snl_sampler_accept(smp, d);
+            if ((rc = snl_sampler_sample(smp, 1, &tok))) return rc;
+            mr0 = 1;
+            mn = 2;
+            mtok[0] = d;
+            mtok[1] = tok;
+            for (int k = 0; k < 3; ++k) {
+                mpos[k] = rope;
+                mpos[3 + k] = rope + 1;
+            }
+            rope += 2;
+        } else {
+            if ((rc = snl_rollback(e))) return rc;
+            tok = next;
+            mr0 = 1;
+            mn = 1;
+            mtok[0] = tok;
+            for (int k = 0; k < 3; ++k) mpos[k] = rope;
+            rope += 1;
+        }
+        mslot = slot;
+    }
+    st->draft_s = draft_s;
+    st->verify_s = verify_s;
+    st->generated = generated;
+    *n_gen = generated;
+    return SNL_OK;
 }
 
 }  // namespace
@@ -396,6 +499,28 @@ int snl_worker_run(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at
     int rc = run(w, prompt, n, snapshot_at, max_tokens, spec, out, gaps, fin);
     if (rc) {
         // Leave the caches in a known state after a failure (src/worker.rs:94-101).
+        const std::string msg = snl_last_error(w->e);
+        snl_reset(w->e);
+        w->live.clear();
+        for (auto& s : w->snaps) s = snl_worker::Snap();
+        snl::engine_fail(w->e, rc, msg.c_str());
+    }
+    w->epoch = snl::engine_epoch(w->e);
+    return rc;
+}
+
+int snl_worker_run_sampled(snl_worker* w, const uint32_t* prompt, int n, int snapshot_at, int max_tokens, int spec,
+                           const snl_sampling* params, uint64_t seed, int has_seed, uint32_t* out, snl_finish* fin) {
+    if (!w || (!prompt && n > 0) || !out || !params) return SNL_EARG;
+    const bool greedy = params->temperature <= 1e-5f && params->repetition_penalty == 1.0f &&
+                        params->presence_penalty == 0.0f && params->frequency_penalty == 0.0f;
+    if (greedy) return snl_worker_run(w, prompt, n, snapshot_at, max_tokens, spec, out, nullptr, fin);
+    if (fin) *fin = snl_finish{};
+    snl_sampler* smp = nullptr;
+    int rc = snl_sampler_create(w->e, params, seed, has_seed, &smp);
+    if (!rc) rc = run(w, prompt, n, snapshot_at, max_tokens, spec, out, nullptr, fin, smp);
+    snl_sampler_destroy(smp);
+    if (rc) {
         const std::string msg = snl_last_error(w->e);
         snl_reset(w->e);
         w->live.clear();

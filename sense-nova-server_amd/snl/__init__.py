@@ -6,4 +6,4 @@ prefix cache (src/worker.rs:115-174).  Nothing here computes on the CPU:
 every call goes to the HIP library, and loading fails loudly when it is missing.
 """
 from .config import ModelConfig, SnlConfig, nine_b_config, tiny_config  # noqa: F401
-from .engine import Engine, SnlError, Worker, lib, kernels  # noqa: F401
+from .engine import Engine, Rng, Sampler, Sampling, SnlError, Worker, lib, kernels  # noqa: F401

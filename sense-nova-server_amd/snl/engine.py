@@ -50,6 +50,33 @@ class Finish(ctypes.Structure):
 SNAPSHOTS = 4
 
 
+class Sampling(ctypes.Structure):
+    """SamplingParams (src/sampler.rs:4-29); the reference's defaults."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_p", ctypes.c_float), ("min_p", ctypes.c_float),
+                ("presence_penalty", ctypes.c_float), ("frequency_penalty", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float), ("top_k", ctypes.c_int32), ("_pad", ctypes.c_int32)]
+
+    def __init__(self, temperature=1.0, top_p=0.95, top_k=20, min_p=0.0, presence_penalty=0.0,
+                 frequency_penalty=0.0, repetition_penalty=1.0):
+        super().__init__(temperature, top_p, min_p, presence_penalty, frequency_penalty, repetition_penalty, top_k, 0)
+
+
+class Rng(ctypes.Structure):
+    """The reference's StdRng (ChaCha12, seed_from_u64) inside the library."""
+    _fields_ = [("key", ctypes.c_uint32 * 8), ("counter", ctypes.c_uint64), ("buf", ctypes.c_uint32 * 16),
+                ("idx", ctypes.c_int32), ("_pad", ctypes.c_int32)]
+
+    def __init__(self, seed: int):
+        super().__init__()
+        lib().snl_rng_seed(ctypes.byref(self), ctypes.c_uint64(seed))
+
+    def u32(self) -> int:
+        return int(lib().snl_rng_u32(ctypes.byref(self)))
+
+    def f32(self) -> float:
+        return float(lib().snl_rng_f32(ctypes.byref(self)))
+
+
 class OpTime(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 24), ("bytes", ctypes.c_double), ("ms", ctypes.c_double)]
 
@@ -101,6 +128,29 @@ def lib() -> ctypes.CDLL:
         L.snl_worker_run.argtypes = [vp, u32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, u32p, f32p,
                                      ctypes.POINTER(Finish)]
         L.snl_worker_cache.argtypes = [vp, i32p, i32p, ctypes.POINTER(ctypes.c_uint64)]
+        L.snl_worker_run_sampled.argtypes = [vp, u32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.POINTER(Sampling), ctypes.c_uint64, ctypes.c_int, u32p,
+                                             ctypes.POINTER(Finish)]
+        L.snl_chacha_block.argtypes = [u32p, ctypes.c_int, u32p]
+        L.snl_chacha_block.restype = None
+        L.snl_rng_seed.argtypes = [ctypes.POINTER(Rng), ctypes.c_uint64]
+        L.snl_rng_seed.restype = None
+        L.snl_rng_u32.argtypes = [ctypes.POINTER(Rng)]
+        L.snl_rng_u32.restype = ctypes.c_uint32
+        L.snl_rng_f32.argtypes = [ctypes.POINTER(Rng)]
+        L.snl_rng_f32.restype = ctypes.c_float
+        L.snl_draw.argtypes = [u32p, f32p, ctypes.c_int, ctypes.c_int64, ctypes.c_float]
+        L.snl_draw.restype = ctypes.c_uint32
+        L.snl_finish_distribution.argtypes = [f32p, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_float, f32p]
+        L.snl_sampler_create.argtypes = [vp, ctypes.POINTER(Sampling), ctypes.c_uint64, ctypes.c_int,
+                                         ctypes.POINTER(vp)]
+        L.snl_sampler_destroy.argtypes = [vp]
+        L.snl_sampler_destroy.restype = None
+        L.snl_sampler_accept.argtypes = [vp, ctypes.c_uint32]
+        L.snl_sampler_accept.restype = None
+        L.snl_sampler_sample.argtypes = [vp, ctypes.c_int, u32p]
+        L.snl_sampler_verify.argtypes = [vp, ctypes.c_int, ctypes.c_uint32, i32p, u32p]
+        L.snl_sampler_distribution.argtypes = [vp, ctypes.c_int, u32p, f32p, ctypes.c_int, i32p]
         L.snl_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.c_int, i32p, i32p]
         L.snl_tensor_read.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, f32p]
         L.snl_buffer_read.argtypes = [vp, ctypes.c_int, vp, ctypes.c_size_t]
@@ -353,6 +403,22 @@ class Worker:
         res.update(tokens=out[:n].tolist(), gaps=gaps[:n])
         return res
 
+    def run_sampled(self, prompt: Sequence[int], max_tokens: int, params: "Sampling", seed: Optional[int] = None,
+                    snapshot_at: Optional[int] = None, spec: bool = True):
+        """One request with SamplingParams (Worker::run with a Sampler); returns tokens and Finish fields."""
+        p = _u32(prompt)
+        out = np.zeros(max(1, max_tokens), np.uint32)
+        fin = Finish()
+        rc = lib().snl_worker_run_sampled(self.h, _ptr(p, u32p), len(p), -1 if snapshot_at is None else snapshot_at,
+                                          max_tokens, int(spec), ctypes.byref(params),
+                                          ctypes.c_uint64(seed or 0), int(seed is not None), _ptr(out, u32p),
+                                          ctypes.byref(fin))
+        self.engine._check(rc)
+        res = {f: getattr(fin, f) for f, _ in Finish._fields_}
+        res["reason"] = "stop" if fin.reason == 1 else "length"
+        res["tokens"] = out[:fin.completion_tokens].tolist()
+        return res
+
     def cache(self):
         """(live length, per-slot key counts with -1 for empty, per-slot last use)."""
         live = ctypes.c_int32()
@@ -364,6 +430,50 @@ class Worker:
     def close(self):
         if getattr(self, "h", None):
             lib().snl_worker_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Sampler:
+    """Sampler (src/sampler.rs:32-96) over the engine's logits rows of its last forward."""
+
+    def __init__(self, engine: "Engine", params: "Sampling", seed: Optional[int] = None):
+        self.engine = engine
+        h = vp()
+        engine._check(lib().snl_sampler_create(engine.h, ctypes.byref(params), ctypes.c_uint64(seed or 0),
+                                               int(seed is not None), ctypes.byref(h)))
+        self.h = h
+
+    def accept(self, token: int):
+        lib().snl_sampler_accept(self.h, token)
+
+    def sample(self, row: int = 0) -> int:
+        t = ctypes.c_uint32()
+        self.engine._check(lib().snl_sampler_sample(self.h, row, ctypes.byref(t)))
+        return int(t.value)
+
+    def verify(self, row: int, draft: int):
+        ok = ctypes.c_int32()
+        t = ctypes.c_uint32()
+        self.engine._check(lib().snl_sampler_verify(self.h, row, draft, ctypes.byref(ok), ctypes.byref(t)))
+        return bool(ok.value), int(t.value)
+
+    def distribution(self, row: int = 0, cap: int = 1 << 18):
+        toks = np.zeros(cap, np.uint32)
+        probs = np.zeros(cap, np.float32)
+        n = ctypes.c_int32()
+        self.engine._check(lib().snl_sampler_distribution(self.h, row, _ptr(toks, u32p), _ptr(probs, f32p), cap,
+                                                          ctypes.byref(n)))
+        return toks[:n.value], probs[:n.value]
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().snl_sampler_destroy(self.h)
             self.h = None
 
     def __del__(self):
