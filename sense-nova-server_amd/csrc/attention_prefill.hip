@@ -5,9 +5,10 @@
 // rotate-half RoPE at the token's rotary position, q rows to qbuf (f32), k / v rows into the f16
 // cache at the token's cache position.
 //
-// attend: block (kv head, 16 queries), wave w = query head 4*kv + w of the GQA group; the block
-// streams the keys [0, last query's position] in steps of 32 through LDS (K rows, and V
-// transposed so that each MFMA A fragment is two 8-byte reads), shared by the group's 4 heads.
+// attend: block (kv head, 16 queries, key part), wave w = query head 4*kv + w of the GQA group;
+// the block streams its part of the keys [0, last query's position] (4096 keys per part) in steps
+// of 32 through LDS (K rows, and V transposed so that each MFMA A fragment is two 8-byte reads),
+// shared by the group's 4 heads.
 //   scores  S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (exact f16),
 //           B = the query's dims split into f16 hi + lo under a per-query power of two, so the
 //           f32 score carries the decode kernel's precision; lane (query j, group g) ends with
@@ -16,7 +17,9 @@
 //           position weigh 0;
 //   values  O^T += V^T P^T: B = the lane's own 8 probabilities as f16 hi + lo (keys 4g..4g+3 and
 //           16+4g..16+4g+3, the same order in the V^T fragment), A = 16 dims x those keys.
-// The output is divided by the softmax sum and multiplied by the sigmoid gate, as in combine.
+// With one part the output is divided by the softmax sum and multiplied by the sigmoid gate, as in
+// combine; with several, each part leaves (unnormalised output, running max, sum) and
+// pf_combine_kernel merges the parts in order.
 #include <float.h>
 #include <hip/hip_fp16.h>
 
@@ -31,6 +34,7 @@ namespace {
 
 constexpr int HD = 256, G = 4;
 constexpr int QTILE = 16, KB = 32;
+constexpr int KPART = 4096;  // keys per part when a long context splits the key range
 constexpr int KROW = HD + 8;  // K tile row (halfs): 528 bytes keeps the 16 rows of a read on distinct banks
 constexpr int VROW = KB + 4;  // V^T row (halfs): 72 bytes
 
@@ -77,7 +81,8 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(AttnArgs a, const PrefillD
     }
 }
 
-__global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const PrefillDev* st, int M) {
+__global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const PrefillDev* st, int M, float* part,
+                                                        int parts_max) {
     __shared__ __align__(16) _Float16 ks[KB * KROW];
     __shared__ __align__(16) _Float16 vt[HD * VROW];
     const int kh = blockIdx.x, q0 = blockIdx.y * QTILE;
@@ -86,6 +91,9 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
     const int pos0 = st->pos0;
     const int qn = min(QTILE, M - q0);
     const int kend = pos0 + q0 + qn;  // keys of the block's last query
+    const int p = blockIdx.z, nparts = (kend + KPART - 1) / KPART;
+    if (p >= nparts) return;
+    const int kfirst = p * KPART, kstop = min(kend, kfirst + KPART);
     const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
     const int j = lane & 15, g = lane >> 4;
     const int mq = q0 + j;
@@ -129,20 +137,20 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
     const uint16_t* kc = a.kcache + kh * HD;
     const uint16_t* vc = a.vcache + kh * HD;
 
-    for (int kb = 0; kb < kend; kb += KB) {
+    for (int kb = kfirst; kb < kstop; kb += KB) {
         __syncthreads();  // the previous step's tiles are consumed
         {   // K rows: thread (key t >> 3, 32 dims)
-            const int key = tid >> 3, part = tid & 7;
+            const int key = tid >> 3, seg = tid & 7;
             const int kk = kb + key;
             uint4 r[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) r[i] = make_uint4(0u, 0u, 0u, 0u);
-            if (kk < kend) {
-                const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)kk * kv_dim + part * 32);
+            if (kk < kstop) {
+                const uint4* src = reinterpret_cast<const uint4*>(kc + (size_t)kk * kv_dim + seg * 32);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) r[i] = src[i];
             }
-            uint4* dst = reinterpret_cast<uint4*>(ks + key * KROW + part * 32);
+            uint4* dst = reinterpret_cast<uint4*>(ks + key * KROW + seg * 32);
 #pragma unroll
             for (int i = 0; i < 4; ++i) dst[i] = r[i];
         }
@@ -152,8 +160,8 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
             const int kp = item >> 5, dg = item & 31;
             const int k0 = kb + 2 * kp;
             uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = make_uint4(0u, 0u, 0u, 0u);
-            if (k0 < kend) v0 = *reinterpret_cast<const uint4*>(vc + (size_t)k0 * kv_dim + dg * 8);
-            if (k0 + 1 < kend) v1 = *reinterpret_cast<const uint4*>(vc + (size_t)(k0 + 1) * kv_dim + dg * 8);
+            if (k0 < kstop) v0 = *reinterpret_cast<const uint4*>(vc + (size_t)k0 * kv_dim + dg * 8);
+            if (k0 + 1 < kstop) v1 = *reinterpret_cast<const uint4*>(vc + (size_t)(k0 + 1) * kv_dim + dg * 8);
             const uint32_t a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -187,7 +195,7 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
             for (int r = 0; r < 4; ++r) {
                 const int kk = kb + 16 * kt + 4 * g + r;
                 const int i = 4 * kt + r;
-                ok[i] = qvalid && kk <= qlim;
+                ok[i] = qvalid && kk <= qlim && kk < kstop;
                 val[i] = sc[kt][r] * up;
                 if (ok[i]) bmax = fmaxf(bmax, val[i]);
             }
@@ -223,6 +231,18 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
     float l = lpart + __shfl_xor(lpart, 16, 64);
     l = l + __shfl_xor(l, 32, 64);
     if (!qvalid) return;
+    if (parts_max > 1) {  // this part's unnormalised output, running max and sum for the combine
+        float* pp = part + (((size_t)mq * a.n_heads + hh) * parts_max + p) * (HD + 2);
+#pragma unroll
+        for (int dt = 0; dt < 16; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pp[16 * dt + 4 * g + r] = o[dt][r];
+        if (g == 0) {
+            pp[HD] = mrun;
+            pp[HD + 1] = l;
+        }
+        return;
+    }
     const float* grow = a.proj + (size_t)mq * a.proj_stride + hh * 2 * HD + HD;
     float* orow = a.out + (size_t)mq * q_dim + hh * HD;
 #pragma unroll
@@ -234,12 +254,41 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
         }
 }
 
+// Merge the key parts of one (query, head): block (head, query), thread = dim.  Parts are added
+// in order with weights e^(m_p - max); then the division by the softmax sum and the sigmoid gate.
+__global__ __launch_bounds__(HD) void pf_combine_kernel(AttnArgs a, const PrefillDev* st, int M, const float* part,
+                                                        int parts_max) {
+    const int hh = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+    const int q0 = m / QTILE * QTILE, qn = min(QTILE, M - q0);
+    const int nparts = (st->pos0 + q0 + qn + KPART - 1) / KPART;
+    const float* pp = part + ((size_t)m * a.n_heads + hh) * parts_max * (HD + 2);
+    float mx = -1e30f;
+    for (int p = 0; p < nparts; ++p) mx = fmaxf(mx, pp[(size_t)p * (HD + 2) + HD]);
+    float acc = 0.0f, l = 0.0f;
+    for (int p = 0; p < nparts; ++p) {
+        const float* q = pp + (size_t)p * (HD + 2);
+        const float f = expf(q[HD] - mx);
+        acc = acc + q[d] * f;
+        l = l + q[HD + 1] * f;
+    }
+    const float gate = a.proj[(size_t)m * a.proj_stride + hh * 2 * HD + HD + d];
+    a.out[(size_t)m * a.n_heads * HD + hh * HD + d] = acc / l / (1.0f + expf(-gate));
+}
+
 }  // namespace
 
-int launch_attention_prefill(const AttnArgs& a, const PrefillDev* pstep, int M, hipStream_t s) {
+int attention_prefill_parts(int ctx) { return (ctx + KPART - 1) / KPART; }
+
+int launch_attention_prefill(const AttnArgs& a, const PrefillDev* pstep, int M, int keys, float* part, int parts_max,
+                             hipStream_t s) {
     if (M < 1 || M > SNL_PF_M || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2 || !pstep) return -1;
+    const int parts = (keys + KPART - 1) / KPART;  // parts of the pass's longest key range
+    if (parts > 1 && (!part || parts > parts_max)) return -1;
     hipLaunchKernelGGL(pf_prep_kernel, dim3(a.n_heads + 2 * a.n_kv, M), dim3(256), 0, s, a, pstep);
-    hipLaunchKernelGGL(pf_attend_kernel, dim3(a.n_kv, (M + QTILE - 1) / QTILE), dim3(256), 0, s, a, pstep, M);
+    hipLaunchKernelGGL(pf_attend_kernel, dim3(a.n_kv, (M + QTILE - 1) / QTILE, parts), dim3(256), 0, s, a, pstep, M,
+                       part, parts > 1 ? parts_max : 1);
+    if (parts > 1)
+        hipLaunchKernelGGL(pf_combine_kernel, dim3(a.n_heads, M), dim3(HD), 0, s, a, pstep, M, part, parts_max);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

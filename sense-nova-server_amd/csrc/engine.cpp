@@ -162,6 +162,9 @@ struct snl_engine {
     float *pf_dq = nullptr, *pf_dk = nullptr, *pf_dv = nullptr, *pf_gz = nullptr, *pf_beta = nullptr,
           *pf_decay = nullptr;
     void* pf_frags = nullptr;
+    float* pf_apart = nullptr;  // attention key-part partials (contexts past one part)
+    int pf_parts = 1;
+    int pf_pos0 = 0;            // cache position of the current prefill pass's row 0
     PrefillDev *d_pstep = nullptr, *h_pstep = nullptr;  // h_pstep: pinned
     uint16_t *kcache = nullptr, *vcache = nullptr, *m_kc = nullptr, *m_vc = nullptr;
     float *lin_state = nullptr, *conv_state = nullptr;
@@ -617,6 +620,8 @@ int snl_engine::init() {
             (rc = dalloc(&pf_decay, P * nv)) || (rc = dalloc((uint8_t**)&pf_frags, frags_bytes(SNL_PF_M, kmax))) ||
             (rc = dalloc(&d_pstep, 1)))
             return rc;
+        pf_parts = attention_prefill_parts(ctx);
+        if (pf_parts > 1 && (rc = dalloc(&pf_apart, P * c.n_heads * pf_parts * (c.head_dim + 2)))) return rc;
         if (hipHostMalloc((void**)&h_pstep, sizeof(PrefillDev), hipHostMallocDefault) != hipSuccess)
             return fail(SNL_ENOMEM, "pinned host allocation failed");
     }
@@ -798,7 +803,7 @@ int snl_engine::record_prefill(int M, int rows) {
             a.proj = pf_proj;
             a.qbuf = pf_qbuf;
             a.out = pf_attn;
-            if (op("attention", 0.0)) rc |= launch_attention_prefill(a, d_pstep, M, stream);
+            if (op("attention", 0.0)) rc |= launch_attention_prefill(a, d_pstep, M, pf_pos0 + M, pf_apart, pf_parts, stream);
             rc |= pf_mat("gemm_o", L.mix_out, pf_attn, q_dim, M, ROWS_PLAIN, nullptr, pf_br, h);
             ++fslot;
         } else {
@@ -858,7 +863,7 @@ int snl_engine::record_mtp_prefill(int M, int r0) {
     a.proj = pf_proj;
     a.qbuf = pf_qbuf;
     a.out = pf_attn;
-    if (op("attention", 0.0)) rc |= launch_attention_prefill(a, d_pstep, M, stream);
+    if (op("attention", 0.0)) rc |= launch_attention_prefill(a, d_pstep, M, pf_pos0 + M, pf_apart, pf_parts, stream);
     rc |= pf_mat("gemm_mtp_o", m_o, pf_attn, q_dim, M, ROWS_PLAIN, nullptr, pf_br, h);
     if (op("merge", 0.0)) rc |= launch_merge(pf_x, pf_coef, pf_br, h, M, 0, stream);
     rc |= pf_mat("gemm_mtp_gate_up", m_gate_up, pf_x, X2, M, ROWS_NORM, m_post_ln.p, pf_proj, 2 * c.intermediate);
@@ -875,6 +880,7 @@ int snl_engine::prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int 
                               bool mtp, int r0) {
     PrefillDev& st = *h_pstep;
     st.pos0 = cache_pos0;
+    pf_pos0 = cache_pos0;
     st.m = m;
     for (int i = 0; i < m; ++i) {
         st.tokens[i] = tokens[i];

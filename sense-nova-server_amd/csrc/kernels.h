@@ -222,8 +222,11 @@ constexpr int kAttnPart = 64;  // keys per split-K part
 // Gated attention over a chunk (attention_prefill.hip): rows m < M at cache positions pos0 + m
 // with rotary positions rpos[m]; q/k norm + RoPE, K/V into the f16 cache, then causal
 // attention over every earlier key and the sigmoid gate.  Same AttnArgs, with `pstep` for the
-// positions (step is unused).
-int launch_attention_prefill(const AttnArgs& a, const PrefillDev* pstep, int M, hipStream_t s);
+// positions (step is unused).  keys = pos0 + M (host-side); past 4096 keys the key range splits
+// into parts whose partials go to part [M][n_heads][parts_max][258].
+int attention_prefill_parts(int ctx);
+int launch_attention_prefill(const AttnArgs& a, const PrefillDev* pstep, int M, int keys, float* part, int parts_max,
+                             hipStream_t s);
 
 // ---------------------------------------------------------------- seeded initialiser (init.hip)
 int launch_gen_matrix(uint64_t key, int64_t rows, int64_t cols, float stdv, int quant, void* q, float* sc,

@@ -218,3 +218,59 @@ def test_error_paths(pair):
     assert ei.value.code == snl.engine.SNL_EARG
     g.reset()
     assert g.pos == 0
+
+
+@pytest.mark.parametrize("quant", [0, 1], ids=["q8", "q4"])
+def test_prompt_across_prefill_chunks(snl_mod, oracle, quant):
+    """1100 prompt tokens run as prefill passes of 512, 512 and 76 rows (and the MTP catch-up
+    after each): logits, greedy streams and acceptance decisions against the oracle."""
+    cfg = snl_mod.tiny_config()
+    print(f"long prompt quant={quant}", flush=True)
+    g = snl_mod.Engine(cfg, seed=21, quant=quant, ctx=1400)
+    o = oracle.Engine(cfg, seed=21, quant=quant, ctx=1400, max_m=g.prefill_chunk)
+    try:
+        prompt = _prompt(1100, cfg.vocab, seed=31)
+        pos = [[i] * 3 for i in range(1100)]
+        lg_g, _ = g.forward(prompt, pos, logit_rows=2)
+        lg_o = o.forward(prompt, pos, logit_rows=2)
+        assert np.abs(lg_g - lg_o).max() / np.abs(lg_o).max() < 1e-3
+        st_g = g.buffer(3)
+        st_o = o.buf(3, st_g.size)
+        assert np.abs(st_g - st_o).max() / np.abs(st_o).max() < 1e-2
+        for spec in (True, False):
+            g.reset()
+            o.reset()
+            rg = g.generate(prompt, 32, spec)
+            ro = o.generate(prompt, 32, spec)
+            matched = _compare_streams(rg["tokens"], ro["tokens"], ro["gaps"])
+            print(f"spec={spec} matched {matched}/32 drafted {rg['drafted']}/{ro['drafted']} "
+                  f"accepted {rg['accepted']}/{ro['accepted']}", flush=True)
+            if matched == 32 and spec:
+                assert (rg["drafted"], rg["accepted"]) == (ro["drafted"], ro["accepted"])
+    finally:
+        g.close()
+        o.close()
+
+
+def test_long_prefill_matches_decode_feed(snl_mod):
+    """4600 prompt tokens: the prefill passes past 4096 keys split attention into key parts and
+    merge them; the same prompt fed two tokens at a time through the decode kernels (held against
+    the oracle above) must give the same logits and DeltaNet state within the tolerances."""
+    cfg = snl_mod.tiny_config()
+    e = snl_mod.Engine(cfg, seed=23, quant=0, ctx=4700)
+    try:
+        n = 4600
+        prompt = _prompt(n, cfg.vocab, seed=41)
+        pos = [[i] * 3 for i in range(n)]
+        print("long prefill: one call", flush=True)
+        lg_a, _ = e.forward(prompt, pos, logit_rows=2)
+        st_a = e.buffer(3)
+        e.reset()
+        print("long prefill: two tokens per pass", flush=True)
+        for i in range(0, n, 2):
+            lg_b, _ = e.forward(prompt[i:i + 2], pos[i:i + 2], logit_rows=2 if i + 2 >= n else 0)
+        st_b = e.buffer(3)
+        assert np.abs(lg_a - lg_b).max() / np.abs(lg_b).max() < 1e-3
+        assert np.abs(st_a - st_b).max() / np.abs(st_b).max() < 1e-2
+    finally:
+        e.close()
