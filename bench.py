@@ -156,6 +156,13 @@ def long_context(snl, np) -> int:
     log(f"turn 2: cached {r2['cached_tokens']}, prefill {r2['prefill_s']:.3f}s, decode {r2['decode_s']:.2f}s")
     w.close()
     eng.close()
+    # roofline of the pass's dominant kernel: the prefill GEMM on the gate_up shape (Q4_0, 512 rows,
+    # N = 24576, K = 4096), timed alone between HIP events; useful flops 2*M*N*K per launch (the f16
+    # hi/lo split of the token rows issues twice that on the matrix cores)
+    gm, gn, gk = 512, 2 * cfg.intermediate, cfg.hidden
+    g_ms = snl.kernels.gemm_time(1, gn, gk, gm, reps=20)
+    g_tflops = 2.0 * gm * gn * gk / (g_ms * 1e-3) / 1e12
+    log(f"prefill GEMM Q4_0 {gm}x{gn}x{gk}: {g_ms * 1e3:.1f} us -> {g_tflops:.1f} TFLOP/s")
     print(json.dumps({
         "metric": "9B Q4_0 32K-context prefill tok/s and prefix-cache turn (1 GPU)",
         "value": round(n / r1["prefill_s"], 1),
@@ -173,6 +180,15 @@ def long_context(snl, np) -> int:
             "turn2_prefill_s": round(r2["prefill_s"], 3),
             "turn2_decode_tok_s": round(r2["completion_tokens"] / r2["decode_s"], 2),
             "acceptance": round((r1["accepted"] + r2["accepted"]) / max(r1["drafted"] + r2["drafted"], 1), 4),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "mgemm_kernel<Q4_0> (gate_up shape, M=512, N=24576, K=4096)",
+            "achieved": round(g_tflops, 1),
+            "peak": 2500.0,
+            "unit": "TFLOP/s",
+            "frac": round(g_tflops / 2500.0, 4),
+            "traffic": None,
         },
     }), flush=True)
     return 0

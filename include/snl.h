@@ -278,6 +278,10 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
 #define SNL_PREFILL_M 512
 int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K,
              int x_stride, int y_stride, void* stream);
+/* Times the prefill GEMM alone (measurement): seeded N x K weights in panel order and M random
+ * token rows, `reps` launches back to back between two HIP events on a stream of its own;
+ * *ms_per_launch receives the mean. */
+int snl_gemm_time(int quant, int N, int K, int M, int reps, double* ms_per_launch);
 
 /* One Gated DeltaNet step over M = 1..4 tokens (linear.wgsl conv + delta).  conv_state and
  * state hold three slots each ([3][3, conv_dim] and [3][n_v, 128, 128]); the call reads

@@ -1728,6 +1728,66 @@ int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* 
     return SNL_OK;
 }
 
+int snl_gemm_time(int quant, int N, int K, int M, int reps, double* ms_per_launch) {
+    if ((quant != 0 && quant != 1) || K % 128 || K > 16384 || M < 1 || M > SNL_PREFILL_M || N < 1 || reps < 1 ||
+        !ms_per_launch)
+        return SNL_EARG;
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return SNL_EDEVICE;
+    const size_t n = (size_t)N * K;
+    uint8_t *q = nullptr, *pq = nullptr;
+    float *s = nullptr, *ps = nullptr, *x = nullptr, *y = nullptr, *xs = nullptr;
+    void* fr = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = SNL_OK;
+    if (hipMalloc((void**)&q, quant == 0 ? n : n / 2) != hipSuccess || hipMalloc((void**)&s, n / 32 * 4) != hipSuccess ||
+        hipMalloc((void**)&pq, gemm_q_bytes(quant, N, K)) != hipSuccess ||
+        hipMalloc((void**)&ps, gemm_s_floats(N, K) * 4) != hipSuccess ||
+        hipMalloc((void**)&x, (size_t)M * K * 4) != hipSuccess || hipMalloc((void**)&y, (size_t)M * N * 4) != hipSuccess ||
+        hipMalloc(&fr, frags_bytes(M, K)) != hipSuccess || hipMalloc((void**)&xs, (size_t)(M + 15) / 16 * 64) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        rc = SNL_ENOMEM;
+    } else {
+        RowsArgs r{};
+        r.x = x;
+        r.x_stride = K;
+        r.M = M;
+        r.K = K;
+        r.mode = ROWS_PLAIN;
+        r.perm4 = quant;
+        r.frags = fr;
+        r.xs = xs;
+        GemmArgs g{};
+        g.wq = pq;
+        g.ws = ps;
+        g.frags = fr;
+        g.xs = xs;
+        g.y = y;
+        g.y_stride = N;
+        g.M = M;
+        g.N = N;
+        g.K = K;
+        float ms = 0.0f;
+        if (launch_gen_matrix(0x5EEDull, N, K, 0.02f, quant, q, s, st) ||
+            launch_gen_vector(0x5EEEull, (int64_t)M * K, 0, 1.0f, 0, 0, x, st) ||
+            launch_panel_pack(quant, N, K, q, s, pq, ps, st) || launch_rows_to_frags(r, st) ||
+            launch_mgemm(g, quant, st) || hipEventRecord(e0, st) != hipSuccess)
+            rc = SNL_EDEVICE;
+        for (int i = 0; !rc && i < reps; ++i)
+            if (launch_mgemm(g, quant, st)) rc = SNL_EDEVICE;
+        if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                    hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+            rc = SNL_EDEVICE;
+        if (!rc) *ms_per_launch = (double)ms / reps;
+    }
+    (void)hipStreamSynchronize(st);
+    for (void* p : {(void*)q, (void*)s, (void*)pq, (void*)ps, (void*)x, (void*)y, fr, (void*)xs}) (void)hipFree(p);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(st);
+    return rc;
+}
+
 int snl_deltanet(const float* proj, int proj_stride, const float* lw, float* conv_state, float* state, float* out,
                  int conv_dim, int n_k, int n_v, float eps, int M, int ckpt, int s_in, int s_out, int s_ck,
                  void* stream) {

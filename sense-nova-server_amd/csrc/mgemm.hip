@@ -24,10 +24,13 @@
 // elements 32b + 8g + (0..7) (Q4: in the order 0, 4, 1, 5, 2, 6, 3, 7 that the nibble dequant
 // produces), scaled by 2^-e(token); xs[m] = 2^e(m) restores the scale.
 //
-// Work split: a block of 4 waves computes 64 tokens x 256 rows (128 rows when the matrix is too
-// short to give every CU a block); every wave takes all 4 token tiles and its own 4 (2) row tiles.
-// Blocks that share a row panel are numbered so that the 8 XCDs each take whole row panels: the
-// panel is read from HBM once into one XCD's L2 and the token panels reuse it.
+// Work split: a block of 8 waves computes 128 tokens x 256 rows for Q8 (64 x 256 for Q4), and
+// 64 tokens x 128 rows when the matrix is too short to give every CU a block.  The block tile
+// sets how often operands are re-read from L2: the token fragments once per row panel, the
+// weights once per token panel, which is what bounds this kernel (halving the MFMA work or
+// dropping the scale FMAs each changes its time by under 10%).  Blocks that share a row panel are
+// numbered so that the 8 XCDs each take whole row panels: the panel is read from HBM once into
+// one XCD's L2 and the token panels reuse it.
 // Each output element's arithmetic is fixed by its row and column, whatever M or the tile it
 // falls in, so a token's result does not depend on the chunk that carries it.
 #include "common.h"
@@ -239,23 +242,29 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_frags_kernel(RowsArgs a) 
 }
 
 // ---- the GEMM ----
-// Block: 4 waves over TT token tiles (shared by the waves) x 4*RT row tiles (RT per wave).  K runs
-// in stages of one weight piece per row tile (2 quant blocks for Q8, 4 for Q4; TT = 4 and 2
-// keep a stage's token fragments the same size).  Each stage's token fragments, weight pieces
+// Block: 8 waves, 2 along the tokens x 4 along the rows; wave (wt, wr) takes TTW token tiles x RT
+// row tiles, so a block covers 2*TTW token tiles x 4*RT row tiles.  K runs in stages of one weight
+// piece per row tile (2 quant blocks for Q8, 4 for Q4; TTW = 4 and 2 keep a wave's token
+// fragments the same size).  Each stage's token fragments, weight pieces
 // and scales are copied global -> LDS by global_load_lds (16 bytes per lane, lane i at base +
 // 16i), into a ring of two buffers.  An iteration waits for its stage, reads all of it into
 // registers, issues the next stage's copies and only then runs the MFMAs, so the copies fly while
 // the matrix cores work (the compiler waits for every outstanding LDS copy before an LDS read).
+constexpr int kGemmThreads = 512;  // 8 waves
+
 template <int QT, int RT>
 struct GemmStage {
-    static constexpr int TT = QT == 0 && RT == 4 ? 4 : 2;  // token tiles per block
-    static constexpr int BR = 4 * RT;             // row tiles per block
+    static constexpr int TTW = QT == 0 && RT == 4 ? 4 : 2;  // token tiles per wave
+    static constexpr int WT = 2, WR = 4, NW = WT * WR;      // waves along tokens, along rows
+    static constexpr int TT = WT * TTW;                     // token tiles per block
+    static constexpr int BR = WR * RT;                      // row tiles per block
     static constexpr int NBS = QT == 0 ? 2 : 4;   // quant blocks per stage
     static constexpr int A_U4 = TT * NBS * 2 * 64;
     static constexpr int B_U4 = BR * 64;
     static constexpr int S_U4 = BR * 16;
     static constexpr int U4 = A_U4 + B_U4 + S_U4;  // uint4 per stage
     static constexpr size_t BYTES = 2 * (size_t)U4 * 16;
+    static_assert(NW * 64 == kGemmThreads, "block size");
 };
 
 __device__ __forceinline__ void copy16_to_lds(const void* g, uint4* lds_wave_base) {
@@ -264,11 +273,12 @@ __device__ __forceinline__ void copy16_to_lds(const void* g, uint4* lds_wave_bas
 }
 
 template <int QT, int RT>
-__global__ __launch_bounds__(256, 2) void mgemm_kernel(GemmArgs a, int rpanels, int tpanels) {
+__global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpanels, int tpanels) {
     using G = GemmStage<QT, RT>;
-    constexpr int TT = G::TT, NBS = G::NBS;
+    constexpr int TT = G::TTW, NBS = G::NBS;  // TT: this wave's token tiles
     extern __shared__ __align__(16) uint4 lds[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wt = wave / G::WR, wr = wave % G::WR;
     // XCD-aware numbering: block b runs on XCD b % 8; give each XCD whole row panels
     const int bid = blockIdx.x;
     const int xcd = bid & 7, idx = bid >> 3;
@@ -279,7 +289,7 @@ __global__ __launch_bounds__(256, 2) void mgemm_kernel(GemmArgs a, int rpanels, 
     const int K = a.K, nb = K / 32, nq = K / 128, nst = K / (32 * NBS);
     const int rtiles = (a.N + 15) / 16, mtiles = (a.M + 15) / 16;
     const int j = lane & 15, g = lane >> 4;
-    const int R0 = rp * G::BR, T0 = tp * TT;
+    const int R0 = rp * G::BR, T0 = tp * G::TT;
     const uint4* wq = reinterpret_cast<const uint4*>(a.wq);
     const float4* ws = reinterpret_cast<const float4*>(a.ws);
     const uint4* xf = reinterpret_cast<const uint4*>(a.frags);
@@ -289,7 +299,7 @@ __global__ __launch_bounds__(256, 2) void mgemm_kernel(GemmArgs a, int rpanels, 
     auto issue = [&](int st, int buf) {
         uint4* base = lds + (size_t)buf * G::U4;
         constexpr int NA = G::A_U4 / 64, NB = G::B_U4 / 64, NS = G::S_U4 / 64;
-        for (int c = wave; c < NA + NB + NS; c += 4) {
+        for (int c = wave; c < NA + NB + NS; c += G::NW) {
             const void* src;
             if (c < NA) {  // token tile c / (2 NBS), block c / 2 % NBS, hi/lo c % 2
                 const int t = c / (2 * NBS), bh = c % (2 * NBS);
@@ -328,13 +338,14 @@ __global__ __launch_bounds__(256, 2) void mgemm_kernel(GemmArgs a, int rpanels, 
         for (int b = 0; b < NBS; ++b)
 #pragma unroll
             for (int t = 0; t < TT; ++t) {
-                xh[b][t] = __builtin_bit_cast(half8_t, la[((t * NBS + b) * 2) * 64 + lane]);
-                xl[b][t] = __builtin_bit_cast(half8_t, la[((t * NBS + b) * 2 + 1) * 64 + lane]);
+                const int tb = wt * TT + t;  // token tile in the block
+                xh[b][t] = __builtin_bit_cast(half8_t, la[((tb * NBS + b) * 2) * 64 + lane]);
+                xl[b][t] = __builtin_bit_cast(half8_t, la[((tb * NBS + b) * 2 + 1) * 64 + lane]);
             }
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
-            wv[r] = lb[(wave * RT + r) * 64 + lane];
-            sv[r] = lsc[(wave * RT + r) * 16 + j];
+            wv[r] = lb[(wr * RT + r) * 64 + lane];
+            sv[r] = lsc[(wr * RT + r) * 16 + j];
         }
         if (st + 1 < nst) issue(st + 1, buf ^ 1);
 #pragma unroll
@@ -361,13 +372,13 @@ __global__ __launch_bounds__(256, 2) void mgemm_kernel(GemmArgs a, int rpanels, 
     for (int t = 0; t < TT; ++t) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int m = 16 * (T0 + t) + 4 * g + i;
+            const int m = 16 * (T0 + wt * TT + t) + 4 * g + i;
             if (m >= a.M) continue;
             const float xs = a.xs[m];
             float* yr = a.y + (size_t)m * a.y_stride + a.n_off;
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
-                const int R = R0 + wave * RT + r;
+                const int R = R0 + wr * RT + r;
                 const int n = 16 * R + j;
                 if (R < rtiles && n < a.N) yr[n] = acc[r][t][i] * xs;
             }
@@ -383,7 +394,7 @@ int gemm_launch(const GemmArgs& a, int rpanels, int tpanels, hipStream_t s) {
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)G::BYTES);
     if (attr != hipSuccess) return -2;
     const int blocks = 8 * ((rpanels + 7) / 8) * tpanels;
-    hipLaunchKernelGGL((mgemm_kernel<QT, RT>), dim3(blocks), dim3(256), G::BYTES, s, a, rpanels, tpanels);
+    hipLaunchKernelGGL((mgemm_kernel<QT, RT>), dim3(blocks), dim3(G::NW * 64), G::BYTES, s, a, rpanels, tpanels);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
@@ -428,8 +439,9 @@ int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s) {
     // 16 row tiles per block for wide matrices, 8 (and 2 token tiles) when that leaves too few
     // blocks for the CUs
     const int tt_w = quant == 0 ? GemmStage<0, 4>::TT : GemmStage<1, 4>::TT;
+    const int tt_n = quant == 0 ? GemmStage<0, 2>::TT : GemmStage<1, 2>::TT;
     const bool wide = (size_t)((rtiles + 15) / 16) * ((mtiles + tt_w - 1) / tt_w) >= 192;
-    const int tt = wide ? tt_w : 2;
+    const int tt = wide ? tt_w : tt_n;
     const int tpanels = (mtiles + tt - 1) / tt;
     const int rpanels = wide ? (rtiles + 15) / 16 : (rtiles + 7) / 8;
     if (quant == 0) return wide ? gemm_launch<0, 4>(a, rpanels, tpanels, s) : gemm_launch<0, 2>(a, rpanels, tpanels, s);

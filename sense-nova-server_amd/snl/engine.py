@@ -158,6 +158,7 @@ def lib() -> ctypes.CDLL:
         L.snl_buffer_size.argtypes = [vp, ctypes.c_int]
         L.snl_gemv.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
         L.snl_gemm.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
+        L.snl_gemm_time.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_double)]
         L.snl_deltanet.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_float] + [ctypes.c_int] * 5 + [vp]
         L.snl_attention.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int,
@@ -506,6 +507,15 @@ class kernels:
                             y_stride, kernels._stream())
         if rc != SNL_OK:
             raise SnlError(rc, "snl_gemm")
+
+    @staticmethod
+    def gemm_time(quant: int, N: int, K: int, M: int, reps: int = 20) -> float:
+        """Mean ms per launch of the prefill GEMM alone (seeded weights, random rows)."""
+        ms = ctypes.c_double()
+        rc = lib().snl_gemm_time(quant, N, K, M, reps, ctypes.byref(ms))
+        if rc != SNL_OK:
+            raise SnlError(rc, "snl_gemm_time")
+        return ms.value
 
     @staticmethod
     def deltanet(proj, proj_stride, lw, conv_state, state, out, conv_dim, n_k, n_v, eps, M, ckpt, s_in, s_out,

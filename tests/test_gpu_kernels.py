@@ -100,6 +100,13 @@ def test_gemm_rows_independent_of_m(torch_cuda, K, oracle, quant):
         assert np.array_equal(ys.cpu().numpy(), full[lo:hi])
 
 
+def test_gemm_time_runs(torch_cuda, K):
+    """The isolated GEMM timing used for the long-context roofline returns a positive mean."""
+    for quant in (0, 1):
+        ms = K.gemm_time(quant, 2048, 1024, 512, reps=3)
+        assert 0.0 < ms < 100.0
+
+
 @pytest.mark.parametrize("quant", [0, 1])
 def test_gemv_rows_independent_of_m(torch_cuda, K, oracle, quant):
     """Row r of an M-row call is bitwise the M=1 result: the verify pass reproduces plain decode."""
