@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     if (kstart >= total_max) return;
     const int nkeys = min(kPart, total_max - kstart);
     const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane >> 4, j = lane & 15;
     int valid[M];
 #pragma unroll

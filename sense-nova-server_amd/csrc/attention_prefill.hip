@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
     __shared__ __align__(16) _Float16 ks[KB * KROW];
     __shared__ __align__(16) _Float16 vt[HD * VROW];
     const int kh = blockIdx.x, q0 = blockIdx.y * QTILE;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hh = kh * G + w;
     const int pos0 = st->pos0;
     const int qn = min(QTILE, M - q0);

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     const StepDev* st = a.step;
     const int s_in = st->s_in, s_out = st->s_out, s_ck = st->s_ck, ckpt = st->ckpt;
     const int h = blockIdx.x / kCG, cg = blockIdx.x - (blockIdx.x / kCG) * kCG;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 3, rg = lane >> 2;
     const int jl = 4 * wave + c, j = cg * kCols + jl;  // column in the group, in the head
     const int group = a.n_v / a.n_k, kh = h / group;

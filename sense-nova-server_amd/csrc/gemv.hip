@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a, int G) {
     const int K4p = nchunks * (kChunk / 4);                         // staged row length, whole chunks
     float4* xs4 = lds4;                                             // [M][K4p] staged rows (permuted)
     float* sxs = reinterpret_cast<float*>(lds4 + (size_t)M * K4p);  // [M][K/16] 16-element sums
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int blk = blockIdx.x;
     const int steps = G * nchunks;
 

@@ -69,7 +69,7 @@ __device__ __forceinline__ void dot16(const uint32_t (&w)[4], const float (&x)[1
 
 template <int QT, int M>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int blk = blockIdx.x;
     const int K = a.K, nb = K >> 5;
     const int nchunks = (K + kChunk - 1) / kChunk;

@@ -211,7 +211,7 @@ __device__ __forceinline__ Top2 top2_block(Top2 t) {
     __shared__ float s1[4], s2[4];
     __shared__ uint32_t si[4];
     t = top2_wave(t);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     __syncthreads();
     if (lane == 0) {
         s1[w] = t.v1;

@@ -277,7 +277,9 @@ __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpa
     using G = GemmStage<QT, RT>;
     constexpr int TT = G::TTW, NBS = G::NBS;  // TT: this wave's token tiles
     extern __shared__ __align__(16) uint4 lds[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index in a scalar register: the copy loop below then branches and forms its
+    // addresses in scalar code instead of exec-masked vector code
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wt = wave / G::WR, wr = wave % G::WR;
     // XCD-aware numbering: block b runs on XCD b % 8; give each XCD whole row panels
     const int bid = blockIdx.x;

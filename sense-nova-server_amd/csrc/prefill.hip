@@ -131,7 +131,7 @@ __global__ __launch_bounds__(kThreads) void dn_recur_kernel(DnPrefillArgs a, int
     extern __shared__ float ored[];  // [kWaves][M]
     __shared__ RecurSlice sl[2];
     const int h = blockIdx.x / kCG, cg = blockIdx.x % kCG;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 3, rg = lane >> 2;
     const int jl = 4 * wave + c, j = cg * kCols + jl;
     const int n_k = a.n_k, n_v = a.n_v, group = n_v / n_k, kh = h / group;
