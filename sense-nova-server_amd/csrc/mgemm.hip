@@ -245,11 +245,12 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_frags_kernel(RowsArgs a) 
 // Block: 8 waves, 2 along the tokens x 4 along the rows; wave (wt, wr) takes TTW token tiles x RT
 // row tiles, so a block covers 2*TTW token tiles x 4*RT row tiles.  K runs in stages of one weight
 // piece per row tile (2 quant blocks for Q8, 4 for Q4; TTW = 4 and 2 keep a wave's token
-// fragments the same size).  Each stage's token fragments, weight pieces
-// and scales are copied global -> LDS by global_load_lds (16 bytes per lane, lane i at base +
-// 16i), into a ring of two buffers.  An iteration waits for its stage, reads all of it into
-// registers, issues the next stage's copies and only then runs the MFMAs, so the copies fly while
-// the matrix cores work (the compiler waits for every outstanding LDS copy before an LDS read).
+// fragments the same size).  Each stage's token fragments, weight pieces and scales are copied
+// global -> LDS by global_load_lds (16 bytes per lane, lane i at base + 16i) into a ring of three
+// buffers, two stages ahead of the one computed.  A step waits for its own stage only (the vector
+// memory count may keep one stage of copies outstanding), passes a barrier, reads the stage into
+// registers, issues the copies of the stage two ahead into the buffer read one step before, and
+// runs the MFMAs while both later stages are in flight.
 constexpr int kGemmThreads = 512;  // 8 waves
 
 template <int QT, int RT>
@@ -263,20 +264,32 @@ struct GemmStage {
     static constexpr int B_U4 = BR * 64;
     static constexpr int S_U4 = BR * 16;
     static constexpr int U4 = A_U4 + B_U4 + S_U4;  // uint4 per stage
-    static constexpr size_t BYTES = 2 * (size_t)U4 * 16;
+    static constexpr int NC = U4 / 64;             // 1 KiB copies per stage
+    static constexpr int NC_MIN = NC / NW;         // copies per stage of the waves with the fewest
     static_assert(NW * 64 == kGemmThreads, "block size");
+    static constexpr size_t BYTES = 3 * (size_t)U4 * 16;  // three stage buffers
+    static_assert(BYTES <= 160 * 1024, "three stages fit the LDS");
 };
 
-__device__ __forceinline__ void copy16_to_lds(const void* g, uint4* lds_wave_base) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+// s_waitcnt immediate (gfx9 layout): vector memory count vm, LDS count 0, export count untouched
+constexpr int wait_vm_lgkm0(int vm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4); }
+
+// 1 KiB global -> LDS copy of one wave: lane i moves 16 bytes from base + voff(i) to LDS
+// dst + 16 i.  Issued as inline assembly, so the compiler's wait insertion does not see it and
+// does not hold every LDS read until all copies in flight have landed; the kernel orders the
+// copies itself (s_waitcnt on the vector memory count before the barrier that publishes a stage).
+// The compiler's own waits stay correct: loads it does not know about can only make them wait
+// longer.
+__device__ __forceinline__ void copy16_to_lds(const char* base, unsigned voff, unsigned dst) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(base)
+                 : "memory", "m0");
 }
 
 template <int QT, int RT>
 __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpanels, int tpanels) {
     using G = GemmStage<QT, RT>;
     constexpr int TT = G::TTW, NBS = G::NBS;  // TT: this wave's token tiles
-    extern __shared__ __align__(16) uint4 lds[];
+    extern __shared__ __align__(16) uint4 lds[];  // three stage buffers of G::U4
     // the wave index in a scalar register: the copy loop below then branches and forms its
     // addresses in scalar code instead of exec-masked vector code
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -292,29 +305,39 @@ __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpa
     const int rtiles = (a.N + 15) / 16, mtiles = (a.M + 15) / 16;
     const int j = lane & 15, g = lane >> 4;
     const int R0 = rp * G::BR, T0 = tp * G::TT;
-    const uint4* wq = reinterpret_cast<const uint4*>(a.wq);
-    const float4* ws = reinterpret_cast<const float4*>(a.ws);
-    const uint4* xf = reinterpret_cast<const uint4*>(a.frags);
     const int npc = QT == 0 ? K / 64 : K / 128;  // pieces per row tile (= stages)
 
-    // one stage: wave instruction c of the stage's U4/64 copies moves 1 KiB
+    // One stage: wave instruction c of the stage's U4/64 copies moves 1 KiB.  The panel copies and
+    // the token fragments are allocated in whole block panels (gemm_q_bytes, gemm_s_floats,
+    // frags_bytes), so no copy needs a clamp: each source is a scalar offset plus one of two
+    // per-lane offsets.  Rows and tokens past the matrix only feed outputs that are not stored.
+    const char* xf_b = reinterpret_cast<const char*>(a.frags);
+    const char* wq_b = reinterpret_cast<const char*>(a.wq);
+    const char* ws_b = reinterpret_cast<const char*>(a.ws);
+    const unsigned lane16 = (unsigned)lane * 16u;
+    // scales: lane l -> row tile + l / 16 of the copy's 4, row l % 16
+    const unsigned lane_s = (unsigned)(lane >> 4) * (unsigned)nq * 256u + (unsigned)(lane & 15) * 16u;
+    const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
     auto issue = [&](int st, int buf) {
-        uint4* base = lds + (size_t)buf * G::U4;
+        const unsigned dst0 = lds_base + (unsigned)(buf * G::U4) * 16u;
         constexpr int NA = G::A_U4 / 64, NB = G::B_U4 / 64, NS = G::S_U4 / 64;
         for (int c = wave; c < NA + NB + NS; c += G::NW) {
-            const void* src;
+            const char* src;
+            unsigned lo = lane16;
             if (c < NA) {  // token tile c / (2 NBS), block c / 2 % NBS, hi/lo c % 2
                 const int t = c / (2 * NBS), bh = c % (2 * NBS);
-                const int T = min(T0 + t, mtiles - 1);
-                src = xf + (((size_t)T * nb + st * NBS) * 2 + bh) * 64 + lane;
+                src = xf_b + ((((size_t)(T0 + t) * nb + st * NBS) * 2 + bh) << 10);
             } else if (c < NA + NB) {  // row tile c - NA
-                const int R = min(R0 + c - NA, rtiles - 1);
-                src = wq + ((size_t)R * npc + st) * 64 + lane;
-            } else {  // scales of 4 row tiles: lane l -> row tile 4(c - NA - NB) + l / 16, row l % 16
-                const int R = min(R0 + 4 * (c - NA - NB) + (lane >> 4), rtiles - 1);
-                src = ws + ((size_t)R * nq + st * NBS / 4) * 16 + (lane & 15);
+                src = wq_b + (((size_t)(R0 + c - NA) * npc + st) << 10);
+            } else {  // scales of row tiles R0 + 4(c - NA - NB) .. + 3
+                // Q8 stages take 2 of a row's 4 scales: an odd stage starts 8 bytes into the float4,
+                // so the stage's scales are always .x and .y (the last 8 bytes read belong to the
+                // next row, or to the padding after the last)
+                src = ws_b + (((size_t)(R0 + 4 * (c - NA - NB)) * nq + st * NBS / 4) << 8) +
+                      (NBS == 2 ? (st & 1) * 8 : 0);
+                lo = lane_s;
             }
-            copy16_to_lds(src, base + c * 64);
+            copy16_to_lds(src, lo, dst0 + (unsigned)c * 1024u);
         }
     };
 
@@ -324,13 +347,21 @@ __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpa
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    issue(0, 0);
-    for (int st = 0; st < nst; ++st) {
-        const int buf = st & 1;
-        // stage st has landed for every wave, and every wave has read stage st - 1's buffer
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        const uint4* la = lds + (size_t)buf * G::U4;
+    // Stage st lives in buffer st % 3; two stages of copies are in flight while one is computed.
+    auto step = [&](int st) {
+        const uint4* la = lds + (size_t)(st % 3) * G::U4;
+        // This wave's copies of stage st have landed when at most one stage's worth (the copies
+        // of stage st + 1) is outstanding; every read of this wave is complete.  After the
+        // barrier every wave's copies of stage st have landed and every wave has read stage
+        // st - 1, whose buffer `next` then takes stage st + 2.
+        // no instruction of the previous step moves past this point, no LDS access across the
+        // barrier
+        __builtin_amdgcn_sched_barrier(0);
+        if (st + 1 < nst) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(G::NC_MIN));
+        else __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         const uint4* lb = la + G::A_U4;
         const float4* lsc = reinterpret_cast<const float4*>(lb + G::B_U4);
         half8_t xh[NBS][TT], xl[NBS][TT];
@@ -349,16 +380,15 @@ __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpa
             wv[r] = lb[(wr * RT + r) * 64 + lane];
             sv[r] = lsc[(wr * RT + r) * 16 + j];
         }
-        if (st + 1 < nst) issue(st + 1, buf ^ 1);
+        if (st + 2 < nst) issue(st + 2, (st + 2) % 3);
 #pragma unroll
         for (int b = 0; b < NBS; ++b) {
-            const int sb = (st * NBS + b) & 3;  // block inside the scales' group of 4
 #pragma unroll
             for (int r = 0; r < RT; ++r) {
                 half8_t wh;
                 if constexpr (QT == 0) wh = b ? q8_to_h8(wv[r].z, wv[r].w) : q8_to_h8(wv[r].x, wv[r].y);
                 else wh = q4_to_h8(b == 0 ? wv[r].x : b == 1 ? wv[r].y : b == 2 ? wv[r].z : wv[r].w);
-                const float sc = sb == 0 ? sv[r].x : sb == 1 ? sv[r].y : sb == 2 ? sv[r].z : sv[r].w;
+                const float sc = b == 0 ? sv[r].x : b == 1 ? sv[r].y : b == 2 ? sv[r].z : sv[r].w;
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
                     f32x4_t d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh[b][t], wh, f32x4_t{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
@@ -368,7 +398,10 @@ __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpa
                 }
             }
         }
-    }
+    };
+    issue(0, 0);
+    if (nst > 1) issue(1, 1);
+    for (int st = 0; st < nst; ++st) step(st);
     // lane (n = j, g) holds tokens 4g..4g+3 of each token tile
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
@@ -402,12 +435,16 @@ int gemm_launch(const GemmArgs& a, int rpanels, int tpanels, hipStream_t s) {
 
 }  // namespace
 
+// Row tiles of a panel copy: whole 256-row block panels, so a block's copies never run past it.
+static size_t panel_tiles(int N) { return ((size_t)(N + 15) / 16 + 15) / 16 * 16; }
+
 size_t gemm_q_bytes(int quant, int N, int K) {
-    const size_t rt = (size_t)(N + 15) / 16;
+    const size_t rt = panel_tiles(N);
     return quant == 0 ? rt * 16 * K : rt * 8 * K;
 }
 
-size_t gemm_s_floats(int N, int K) { return (size_t)(N + 15) / 16 * 16 * (K / 32); }
+// (+ 4: the shifted scale copy of an odd Q8 stage reads 8 bytes past the last float4)
+size_t gemm_s_floats(int N, int K) { return panel_tiles(N) * 16 * (K / 32) + 4; }
 
 int launch_panel_pack(int quant, int N, int K, const void* q, const float* s, void* qp, float* sp, hipStream_t st) {
     if (K % 128 || N <= 0 || (quant != 0 && quant != 1)) return -1;
@@ -420,7 +457,8 @@ int launch_panel_pack(int quant, int N, int K, const void* q, const float* s, vo
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
-size_t frags_bytes(int M, int K) { return (size_t)((M + 15) / 16) * 16 * K * 4; }
+// token fragments in whole 128-token panels (8 tiles), the widest token panel of a block
+size_t frags_bytes(int M, int K) { return (size_t)((M + 127) / 128) * 128 * K * 4; }
 
 int launch_rows_to_frags(const RowsArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.K % 128 || !a.frags || !a.xs) return -1;
