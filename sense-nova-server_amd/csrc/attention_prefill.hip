@@ -115,8 +115,7 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
             amax = fmaxf(amax, fabsf(qv[s][i]));
         }
     }
-    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    amax = xor_max<32>(xor_max<16>(amax));
     const int e = amax > 0.0f ? max(ilogbf(amax) - 14, -110) : 0;
     const float down = ldexpf(1.0f, -e), up = ldexpf(1.0f, e) * a.scale;
     half8_t qh[8], ql[8];
@@ -199,8 +198,7 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
                 val[i] = sc[kt][r] * up;
                 if (ok[i]) bmax = fmaxf(bmax, val[i]);
             }
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-        bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+        bmax = xor_max<32>(xor_max<16>(bmax));
         const float mnew = fmaxf(mrun, bmax);
         const float factor = expf(mrun - mnew);
         half8_t ph, pl;
@@ -228,8 +226,7 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
         }
     }
     // ---- normalise, gate, store: lane (query j) holds dims 16dt + 4g + r ----
-    float l = lpart + __shfl_xor(lpart, 16, 64);
-    l = l + __shfl_xor(l, 32, 64);
+    const float l = xor_sum<32>(xor_sum<16>(lpart));
     if (!qvalid) return;
     if (parts_max > 1) {  // this part's unnormalised output, running max and sum for the combine
         float* pp = part + (((size_t)mq * a.n_heads + hh) * parts_max + p) * (HD + 2);

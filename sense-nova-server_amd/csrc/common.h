@@ -44,10 +44,60 @@ struct PrefillDev {
     uint32_t rpos[SNL_PF_M][4];  // rotary (t, h, w, 0) position of each row
 };
 
+// ---- butterfly exchanges in vector registers ----
+// lane_xor<O>(v), O = 1, 2, 4, 8: the v of lane l ^ O, by DPP inside each 16-lane row (quad
+// permutes for 1 and 2; row shifts by 4 under bank masks, banks 0 and 2 reading l + 4 and banks 1
+// and 3 reading l - 4; a row rotation by 8).  xor_sum<O> / xor_max<O> add / take the max of v and
+// lane l ^ O's v; for O = 16 and 32 the gfx950 permlane swaps bring the pair together, and both
+// lanes combine (lower lane's value, upper lane's value), the same result as v + __shfl_xor(v, O)
+// since the operation commutes.  None of them goes through the LDS as ds_bpermute does.
+template <int O>
+__device__ __forceinline__ float lane_xor(float v) {
+    static_assert(O == 1 || O == 2 || O == 4 || O == 8, "DPP exchange inside a row");
+    const int x = __float_as_int(v);
+    if constexpr (O == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (O == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+    else if constexpr (O == 4) {
+        const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xF, 0x5, false);  // row_shl:4, banks 0, 2
+        return __int_as_float(__builtin_amdgcn_update_dpp(t, x, 0x114, 0xF, 0xA, false));  // row_shr:4, 1, 3
+    } else {
+        return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));  // row_ror:8
+    }
+}
+
+template <int O>
+__device__ __forceinline__ float xor_sum(float v) {
+    if constexpr (O == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+        return v + lane_xor<O>(v);
+    }
+}
+
+template <int O>
+__device__ __forceinline__ float xor_max(float v) {
+    if constexpr (O == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    } else {
+        return fmaxf(v, lane_xor<O>(v));
+    }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SNL_WAVE);
-    return v;
+    v = xor_sum<32>(v);
+    v = xor_sum<16>(v);
+    v = xor_sum<8>(v);
+    v = xor_sum<4>(v);
+    v = xor_sum<2>(v);
+    return xor_sum<1>(v);
 }
 
 // N independent wave sums, level by level so the N exchanges of a level overlap; each value gets
@@ -55,23 +105,42 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int N>
 __device__ __forceinline__ void wave_sum_n(float (&v)[N]) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
+    for (int i = 0; i < N; ++i) v[i] = xor_sum<32>(v[i]);
 #pragma unroll
-        for (int i = 0; i < N; ++i) v[i] += __shfl_xor(v[i], o, SNL_WAVE);
+    for (int i = 0; i < N; ++i) v[i] = xor_sum<16>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_sum<8>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_sum<4>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_sum<2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_sum<1>(v[i]);
 }
 
 template <int N>
 __device__ __forceinline__ void wave_max_n(float (&v)[N]) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1)
+    for (int i = 0; i < N; ++i) v[i] = xor_max<32>(v[i]);
 #pragma unroll
-        for (int i = 0; i < N; ++i) v[i] = fmaxf(v[i], __shfl_xor(v[i], o, SNL_WAVE));
+    for (int i = 0; i < N; ++i) v[i] = xor_max<16>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_max<8>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_max<4>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_max<2>(v[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = xor_max<1>(v[i]);
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SNL_WAVE));
-    return v;
+    v = xor_max<32>(v);
+    v = xor_max<16>(v);
+    v = xor_max<8>(v);
+    v = xor_max<4>(v);
+    v = xor_max<2>(v);
+    return xor_max<1>(v);
 }
 
 // Sum over a block of NT threads (NT a multiple of 64, at most 1024); every thread gets the total.

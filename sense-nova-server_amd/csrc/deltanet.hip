@@ -142,8 +142,7 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
             s[r] = s[r] * decay[m];
             kv = fmaf(s[r], ck[m][kRows * rg + r] * kscale[m], kv);
         }
-#pragma unroll
-        for (int sh = 4; sh < 64; sh <<= 1) kv = kv + __shfl_xor(kv, sh, 64);
+        kv = xor_sum<32>(xor_sum<16>(xor_sum<8>(xor_sum<4>(kv))));
         const float dlt = (cv[m][jl] - kv) * beta[m];
         float o = 0.0f;
 #pragma unroll
@@ -151,13 +150,12 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
             s[r] = fmaf(ck[m][kRows * rg + r] * kscale[m], dlt, s[r]);
             o = fmaf(s[r], cq[m][kRows * rg + r] * qscale[m], o);
         }
-#pragma unroll
-        for (int sh = 4; sh < 64; sh <<= 1) o = o + __shfl_xor(o, sh, 64);
+        o = xor_sum<32>(xor_sum<16>(xor_sum<8>(xor_sum<4>(o))));
         if (rg == 0) a.out[(size_t)m * a.n_v * DV + h * DV + j] = (o * norm_w) * gz[m];
         // this wave's 4 columns: o^2 added over lanes 0-3
         float q2 = o * o;
-        q2 = q2 + __shfl_xor(q2, 1, 64);
-        q2 = q2 + __shfl_xor(q2, 2, 64);
+        q2 = xor_sum<1>(q2);
+        q2 = xor_sum<2>(q2);
         osq[m] = q2;
         if (m + 1 == ckpt) {
             float* SC = a.state + (size_t)s_ck * a.state_slot + hoff;

@@ -122,12 +122,7 @@ __global__ __launch_bounds__(256) void panel_pack_s_kernel(int N, int K, const f
 constexpr int kRowThreads = 256;
 
 __device__ __forceinline__ float block_max256(float v, float* red) {
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 8, 64));
-    v = fmaxf(v, __shfl_xor(v, 4, 64));
-    v = fmaxf(v, __shfl_xor(v, 2, 64));
-    v = fmaxf(v, __shfl_xor(v, 1, 64));
+    v = wave_max(v);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();

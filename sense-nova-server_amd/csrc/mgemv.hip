@@ -520,10 +520,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
 #pragma unroll
     for (int p = 0; p < P; ++p) {
         float t0 = acc[p][0] + acc[p][1], t1 = acc[p][2] + acc[p][3];
-        t0 = t0 + __shfl_xor(t0, 16, 64);
-        t1 = t1 + __shfl_xor(t1, 16, 64);
-        t0 = t0 + __shfl_xor(t0, 32, 64);
-        t1 = t1 + __shfl_xor(t1, 32, 64);
+        t0 = xor_sum<16>(t0);
+        t1 = xor_sum<16>(t1);
+        t0 = xor_sum<32>(t0);
+        t1 = xor_sum<32>(t1);
         if (g == 0) {
             red_s[(wave * 16 + j) * 2 * P + 2 * p] = t0;
             red_s[(wave * 16 + j) * 2 * P + 2 * p + 1] = t1;

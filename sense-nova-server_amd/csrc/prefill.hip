@@ -109,13 +109,13 @@ __global__ __launch_bounds__(256) void dn_conv_state_kernel(DnPrefillArgs a, int
 }
 
 // Sum over the 16 row groups (lane >> 2) of the lanes that share lane & 3: rotations by 4 and 8
-// inside each 16-lane row (DPP), then the two rows of each half and the two halves.
+// inside each 16-lane row (DPP), then the two rows of each half and the two halves (permlane
+// swaps).
 __device__ __forceinline__ float rowgroup_sum(float v) {
     v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
     v = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
-    v = v + __shfl_xor(v, 16, 64);
-    v = v + __shfl_xor(v, 32, 64);
-    return v;
+    v = xor_sum<16>(v);
+    return xor_sum<32>(v);
 }
 
 // The recurrence over the chunk (linear.wgsl:118-136), 4 blocks per value head.  The tokens'
@@ -221,8 +221,8 @@ __global__ __launch_bounds__(kThreads) void dn_recur_kernel(DnPrefillArgs a, int
             const int m = m0 + tk;
             if (rg == 0) a.out[(size_t)m * n_v * DV + h * DV + j] = (o * norm_w) * d.gz[tk][jl];
             float q2 = o * o;
-            q2 = q2 + __shfl_xor(q2, 1, 64);
-            q2 = q2 + __shfl_xor(q2, 2, 64);
+            q2 = xor_sum<1>(q2);
+            q2 = xor_sum<2>(q2);
             if (lane == 0) ored[wave * M + m] = q2;
         }
         __syncthreads();  // every wave is done with sl[cur ^ 1]'s previous contents
