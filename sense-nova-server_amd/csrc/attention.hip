@@ -181,14 +181,14 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
             for (int e = 0; e < NC / 2; ++e) {
                 if (e < hn) {
                     const float send = up ? d[e] : d[hn + e], keep = up ? d[hn + e] : d[e];
-                    d[e] = keep + __shfl_xor(send, mask, 64);
+                    d[e] = keep + lane_xor_n(send, mask);
                 }
             }
             n = hn;
         }
         float tot = d[0];
 #pragma unroll
-        for (int mask = 8 / NC; mask > 0; mask >>= 1) tot = tot + __shfl_xor(tot, mask, 64);
+        for (int mask = 8 / NC; mask > 0; mask >>= 1) tot = tot + lane_xor_n(tot, mask);
         // lane j of the row holds combination j / (16 / NC)
         if ((j & (16 / NC - 1)) == 0) sc[j / (16 / NC)][t] = tot * a.scale;
     }
@@ -200,14 +200,12 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
         const int vk = valid[c / G];
         const float s0 = l < vk ? sc[c][l] : -FLT_MAX, s1 = l + 32 < vk ? sc[c][l + 32] : -FLT_MAX;
         float mx = fmaxf(s0, s1);
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+        mx = xor_max<1>(xor_max<2>(xor_max<4>(xor_max<8>(xor_max<16>(mx)))));  // inside each 32-lane half
         const float e0 = l < vk ? expf(s0 - mx) : 0.0f, e1 = l + 32 < vk ? expf(s1 - mx) : 0.0f;
         sc[c][l] = e0;
         sc[c][l + 32] = e1;
         float sum = e0 + e1;
-#pragma unroll
-        for (int o = 16; o > 0; o >>= 1) sum = sum + __shfl_xor(sum, o, 32);
+        sum = xor_sum<1>(xor_sum<2>(xor_sum<4>(xor_sum<8>(xor_sum<16>(sum)))));
         if (l == 0) {
             smax[c] = vk > 0 ? mx : -1e30f;
             ssum[c] = sum;

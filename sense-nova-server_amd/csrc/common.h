@@ -65,6 +65,17 @@ __device__ __forceinline__ float lane_xor(float v) {
     }
 }
 
+// lane_xor for an exchange distance known once the caller's loop is unrolled (1, 2, 4, 8)
+__device__ __forceinline__ float lane_xor_n(float v, int o) {
+    switch (o) {
+        case 1: return lane_xor<1>(v);
+        case 2: return lane_xor<2>(v);
+        case 4: return lane_xor<4>(v);
+        case 8: return lane_xor<8>(v);
+        default: return __shfl_xor(v, o, SNL_WAVE);
+    }
+}
+
 template <int O>
 __device__ __forceinline__ float xor_sum(float v) {
     if constexpr (O == 32) {
