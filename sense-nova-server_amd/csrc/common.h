@@ -65,6 +65,21 @@ __device__ __forceinline__ float lane_xor(float v) {
     }
 }
 
+// the 32-bit word of lane l ^ O, any O from 1 to 32 (permlane swaps for 16 and 32: of the swapped
+// pair, a lane takes the half that came from its partner)
+template <int O>
+__device__ __forceinline__ uint32_t lane_xor_bits(uint32_t x) {
+    if constexpr (O == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return (threadIdx.x & 32) ? r[0] : r[1];
+    } else if constexpr (O == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return (threadIdx.x & 16) ? r[0] : r[1];
+    } else {
+        return __float_as_uint(lane_xor<O>(__uint_as_float(x)));
+    }
+}
+
 // lane_xor for an exchange distance known once the caller's loop is unrolled (1, 2, 4, 8)
 __device__ __forceinline__ float lane_xor_n(float v, int o) {
     switch (o) {

@@ -195,16 +195,20 @@ __device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
     return r;
 }
 
+template <int O>
+__device__ __forceinline__ Top2 top2_xor(Top2 t) {
+    const Top2 u = {__uint_as_float(lane_xor_bits<O>(__float_as_uint(t.v1))), lane_xor_bits<O>(t.i1),
+                    __uint_as_float(lane_xor_bits<O>(__float_as_uint(t.v2)))};
+    return top2_merge(t, u);
+}
+
 __device__ __forceinline__ Top2 top2_wave(Top2 t) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        Top2 u;
-        u.v1 = __shfl_xor(t.v1, o, 64);
-        u.i1 = __shfl_xor(t.i1, o, 64);
-        u.v2 = __shfl_xor(t.v2, o, 64);
-        t = top2_merge(t, u);
-    }
-    return t;
+    t = top2_xor<32>(t);
+    t = top2_xor<16>(t);
+    t = top2_xor<8>(t);
+    t = top2_xor<4>(t);
+    t = top2_xor<2>(t);
+    return top2_xor<1>(t);
 }
 
 __device__ __forceinline__ Top2 top2_block(Top2 t) {
@@ -224,15 +228,24 @@ __device__ __forceinline__ Top2 top2_block(Top2 t) {
     return r;
 }
 
-constexpr int kPickChunk = 8192;
+// 2048 logits per block, 8 per thread, all loaded before the first comparison: the row is read in
+// one round trip by ~120 blocks per row instead of a chain of dependent loads
+constexpr int kPickPer = 8;
+constexpr int kPickChunk = 256 * kPickPer;
 
 __global__ __launch_bounds__(256) void pick_partial_kernel(const float* logits, int V, float* scratch, int nblk) {
     const int row = blockIdx.y, b = blockIdx.x;
     const float* lg = logits + (size_t)row * V;
     Top2 t = {-FLT_MAX, 0xFFFFFFFFu, -FLT_MAX};
-    const int end = min(V, (b + 1) * kPickChunk);
-    for (int i = b * kPickChunk + threadIdx.x; i < end; i += 256) {
-        const float v = lg[i];
+    float vals[kPickPer];
+    const int i0 = b * kPickChunk + threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < kPickPer; ++u) vals[u] = i0 + 256 * u < V ? lg[i0 + 256 * u] : -FLT_MAX;
+#pragma unroll
+    for (int u = 0; u < kPickPer; ++u) {
+        const int i = i0 + 256 * u;
+        const float v = vals[u];
+        if (i >= V) break;
         // strict > keeps the first index; elements arrive in ascending order per thread
         if (v > t.v1) {
             t.v2 = t.v1;
