@@ -254,28 +254,26 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     }
 }
 
-// attention.wgsl:248-269: merge the token's parts, then the sigmoid gate.  Block (head, token) of
-// 1024 threads: every part's scale e^(max_p - max) goes to LDS once, then thread (d, q) adds the
-// parts q, q+4, ... of dim d and the four groups are added in order.
-constexpr int kCombThreads = 1024, kMaxParts = 1024;
+// attention.wgsl:248-269: merge the token's parts, then the sigmoid gate.  Block (head, token, 64
+// dims) of 1024 threads: every part's scale e^(max_p - max) goes to LDS once, then thread (d, q)
+// adds the parts q, q+16, ... of dim d and the 16 groups are added in order.  Many short chains
+// keep a long context's partials (512 parts at 32K keys) in flight at once.
+constexpr int kCombThreads = 1024, kCombDims = 64, kCombGroups = kCombThreads / kCombDims, kMaxParts = 1024;
 
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
     __shared__ float fs[kMaxParts];
     __shared__ float red[kCombThreads / 64];
-    __shared__ float accq[4][HD];
+    __shared__ float accq[kCombGroups][kCombDims];
     const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
-    const int d = tid & (HD - 1), q = tid >> 8;
+    const int dl = tid & (kCombDims - 1), q = tid / kCombDims;
+    const int d = blockIdx.z * kCombDims + dl;
     const int total = a.step->pos0 + m + 1;
     const int np = (total + kPart - 1) / kPart;
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     const float* base = a.partial + ((size_t)m * a.n_heads + h) * parts_max * (HD + 2);
-    const float gate = a.proj[(size_t)m * a.proj_stride + h * 2 * HD + HD + d];
-    // global max of the part maxima
-    float mp = -1e30f, lp = 0.0f;
-    if (tid < np) {
-        mp = base[(size_t)tid * (HD + 2) + HD];
-        lp = base[(size_t)tid * (HD + 2) + HD + 1];
-    }
+    // global max of the part maxima (np <= kMaxParts = kCombThreads: one part per thread)
+    const float mp = tid < np ? base[(size_t)tid * (HD + 2) + HD] : -1e30f;
+    const float lp = tid < np ? base[(size_t)tid * (HD + 2) + HD + 1] : 0.0f;
     float mx = wave_max(mp);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
@@ -288,11 +286,14 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
     const float l = block_sum<kCombThreads>(lp * f, red);  // the sum of the parts' weights
     float acc = 0.0f;
 #pragma unroll 8
-    for (int p = q; p < np; p += 4) acc = acc + base[(size_t)p * (HD + 2) + d] * fs[p];
-    accq[q][d] = acc;
+    for (int p = q; p < np; p += kCombGroups) acc = acc + base[(size_t)p * (HD + 2) + d] * fs[p];
+    accq[q][dl] = acc;
     __syncthreads();
     if (q == 0) {
-        const float v = ((accq[0][d] + accq[1][d]) + accq[2][d]) + accq[3][d];
+        float v = accq[0][dl];
+#pragma unroll
+        for (int g = 1; g < kCombGroups; ++g) v = v + accq[g][dl];
+        const float gate = a.proj[(size_t)m * a.proj_stride + h * 2 * HD + HD + d];
         a.out[(size_t)m * a.n_heads * HD + h * HD + d] = v / l / (1.0f + expf(-gate));
     }
 }
@@ -310,7 +311,7 @@ int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
         case 2: hipLaunchKernelGGL(attend_kernel<2>, grid, dim3(256), 0, s, a); break;
         default: return -1;
     }
-    hipLaunchKernelGGL(combine_kernel, dim3(a.n_heads, M), dim3(kCombThreads), 0, s, a);
+    hipLaunchKernelGGL(combine_kernel, dim3(a.n_heads, M, HD / kCombDims), dim3(kCombThreads), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 
