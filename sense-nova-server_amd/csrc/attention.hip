@@ -80,27 +80,31 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, un
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-// Block (kv head, part of kPart keys) for all M tokens and the 4 query heads of the GQA group
-// (NC = 4M head-token combinations).  256 threads = 4 waves.
-//  loads:   the queries, then every key of the part, then every value, all in flight at once;
-//           rows past the part's last key read zero through the buffer range check;
-//  scores:  wave w takes keys [16w, 16w+16) of the part, 4 at a time: 16-lane row r of the wave
-//           holds key 4i+r, lane j of the row dims [16j, 16j+16); the 16 lanes of a row are reduced
-//           by a transposed butterfly (every combination takes the same shuffle sequence);
-//  softmax: exact within the part, 32 threads per combination; keys a token may not see get
-//           weight 0;
-//  values:  thread (dim pair, key half) accumulates its 32 keys (weight 0 adds nothing).
-// Each combination's arithmetic only depends on its own token's keys, so a token's result does
-// not depend on M or on its row index.
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Block (kv head, part of kPart keys) for all M tokens and the 4 query heads of the GQA group,
+// 256 threads = 4 waves, on v_mfma_f32_16x16x32_f16.  The 16 MFMA columns hold the head-token
+// combinations: token m's 4 heads take columns 4 * ((pos0 + m) & 1) + head, so a token sits in the
+// same columns whether it is decoded alone or in a pair, and its arithmetic never depends on M
+// (the other columns are zero).
+//  scores:  S^T = K Q^T: wave w takes keys [16w, 16w+16) of the part as the A operand (16 keys x
+//           32 dims, exact f16 straight from the cache; rows past the part's last key read zero
+//           through the buffer range check); B = the queries as f16 hi + lo under a per-column
+//           power of two, so a score keeps the query's f32 precision;
+//  softmax: exact within the part per combination (32 threads each); keys a token may not see
+//           get weight 0;
+//  values:  O^T = V^T P^T: the part's values pass through LDS (64 keys x 256 dims, f16, rows past
+//           the last key zero) and each lane gathers the 8 keys of its A fragment for one dim;
+//           B = the probabilities as f16 hi + lo; wave w takes dims [64w, 64w+64).
 template <int M>
 __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     constexpr int NC = G * M;
     static_assert(NC == 4 || NC == 8, "M = 1 or 2");
-    constexpr int KI = kPart / 16;  // keys per 16-lane row
-    constexpr int KH = kPart / 2;   // keys per value thread
-    __shared__ __align__(16) float sc[NC][kPart];
-    __shared__ float smax[NC], ssum[NC];
-    __shared__ float2 vred[NC][128];
+    constexpr int VROW = HD + 8;  // V tile row in halfs (528 bytes)
+    __shared__ __align__(16) _Float16 vt[kPart * VROW];
+    __shared__ __align__(16) float sc[16][kPart];  // by MFMA column
+    __shared__ float smax[16], ssum[16];
     const int kh = blockIdx.x, p = blockIdx.y;
     const StepDev* st = a.step;
     const int pos0 = st->pos0;
@@ -110,146 +114,125 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     const int nkeys = min(kPart, total_max - kstart);
     const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r = lane >> 4, j = lane & 15;
-    int valid[M];
+    const int n = lane & 15, g = lane >> 4;  // MFMA column (combination) and k-group of this lane
+    int cm = -1;                             // the token of column n, if any
 #pragma unroll
-    for (int m = 0; m < M; ++m) valid[m] = min(nkeys, pos0 + m + 1 - kstart);
+    for (int m = 0; m < M; ++m)
+        if ((n >> 2) == ((pos0 + m) & 1)) cm = m;
+    const int chh = n & 3;  // its head in the group
 
-    // ---- loads: queries, keys, values ----
-    float q[NC][16];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        const float4* qp = reinterpret_cast<const float4*>(a.qbuf + (size_t)(c / G) * q_dim + (kh * G + c % G) * HD + 16 * j);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const float4 t = qp[v];
-            q[c][4 * v] = t.x, q[c][4 * v + 1] = t.y, q[c][4 * v + 2] = t.z, q[c][4 * v + 3] = t.w;
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    // the part's rows of the cache (all kv heads), nkeys of them in range
+    // ---- loads: the part's values (for the LDS tile), this wave's keys, the queries ----
     const unsigned row_bytes = (unsigned)kv_dim * 2;
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.kcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.vcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
-    u32x4_t kraw[KI][2];
+    u32x4_t vv[kPart / 8];
 #pragma unroll
-    for (int i = 0; i < KI; ++i) {
-        const int t = 16 * w + 4 * i + r;  // key of this 16-lane row
-        const int off = t * (int)row_bytes + (kh * HD + 16 * j) * 2;
-        kraw[i][0] = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0);
-        kraw[i][1] = __builtin_amdgcn_raw_buffer_load_b128(kr, off + 16, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    const int dp = tid & 127, kh2 = tid >> 7;
-    uint32_t vw[KH];
+    for (int i = 0; i < kPart / 8; ++i)  // thread: keys tid / 32 + 8i, 16-byte segment tid % 32
+        vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((tid >> 5) + 8 * i) * (int)row_bytes + kh * HD * 2 + (tid & 31) * 16, 0, 0);
+    u32x4_t kf[HD / 32];
 #pragma unroll
-    for (int i = 0; i < KH; ++i) {
-        const int t = kh2 * KH + i;
-        vw[i] = __builtin_amdgcn_raw_buffer_load_b32(vr, t * (int)row_bytes + (kh * HD + 2 * dp) * 2, 0, 0);
+    for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
+        kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
+    float qv[HD / 32][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s) {
+        float4 u0 = make_float4(0.f, 0.f, 0.f, 0.f), u1 = u0;
+        if (cm >= 0) {
+            const float4* qp = reinterpret_cast<const float4*>(a.qbuf + (size_t)cm * q_dim + (kh * G + chh) * HD + 32 * s + 8 * g);
+            u0 = qp[0];
+            u1 = qp[1];
+        }
+        qv[s][0] = u0.x, qv[s][1] = u0.y, qv[s][2] = u0.z, qv[s][3] = u0.w;
+        qv[s][4] = u1.x, qv[s][5] = u1.y, qv[s][6] = u1.z, qv[s][7] = u1.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[s][e]));
     }
-    __builtin_amdgcn_sched_barrier(0);
+    amax = xor_max<32>(xor_max<16>(amax));  // the 4 lanes of column n
+    const int ex = amax > 0.0f ? max(ilogbf(amax) - 14, -110) : 0;
+    const float down = ldexpf(1.0f, -ex), up = ldexpf(1.0f, ex) * a.scale;
+    half8_t qh[HD / 32], ql[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = qv[s][e] * down;
+            const _Float16 hv = (_Float16)v;
+            qh[s][e] = hv;
+            ql[s][e] = (_Float16)(v - (float)hv);
+        }
+#pragma unroll
+    for (int i = 0; i < kPart / 8; ++i)
+        *reinterpret_cast<u32x4_t*>(vt + ((tid >> 5) + 8 * i) * VROW + (tid & 31) * 8) = vv[i];
 
-    // ---- scores ----
+    // ---- scores: lane (column n, k-group g) ends with keys 16w + 4g + r ----
+    f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < KI; ++i) {
-        const int t = 16 * w + 4 * i + r;
-        float kf[16];
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const u32x4_t raw = kraw[i][v];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                kf[8 * v + 2 * e] = h2f(raw[e] & 0xFFFF);
-                kf[8 * v + 2 * e + 1] = h2f(raw[e] >> 16);
-            }
-        }
-        float d[NC];
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            float s = q[c][0] * kf[0];
-#pragma unroll
-            for (int e = 1; e < 16; ++e) s = fmaf(q[c][e], kf[e], s);
-            d[c] = s;
-        }
-        // transposed butterfly over the 16 lanes of the row
-        int n = NC;
-#pragma unroll
-        for (int mask = 8; mask >= 16 / NC && n > 1; mask >>= 1) {
-            const bool up = j & mask;
-            const int hn = n / 2;
-#pragma unroll
-            for (int e = 0; e < NC / 2; ++e) {
-                if (e < hn) {
-                    const float send = up ? d[e] : d[hn + e], keep = up ? d[hn + e] : d[e];
-                    d[e] = keep + lane_xor_n(send, mask);
-                }
-            }
-            n = hn;
-        }
-        float tot = d[0];
-#pragma unroll
-        for (int mask = 8 / NC; mask > 0; mask >>= 1) tot = tot + lane_xor_n(tot, mask);
-        // lane j of the row holds combination j / (16 / NC)
-        if ((j & (16 / NC - 1)) == 0) sc[j / (16 / NC)][t] = tot * a.scale;
+    for (int s = 0; s < HD / 32; ++s) {
+        const half8_t kfr = __builtin_bit_cast(half8_t, kf[s]);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr, qh[s], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kfr, ql[s], c, 0, 0, 0);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[n][16 * w + 4 * g + r] = c[r] * up;
     lds_barrier();
 
     // ---- exact softmax over the part, 32 threads per combination ----
     if (tid < 32 * NC) {
-        const int c = tid >> 5, l = tid & 31;
-        const int vk = valid[c / G];
-        const float s0 = l < vk ? sc[c][l] : -FLT_MAX, s1 = l + 32 < vk ? sc[c][l + 32] : -FLT_MAX;
+        const int cc = tid >> 5, l = tid & 31;
+        const int m = cc / G, col = 4 * ((pos0 + m) & 1) + cc % G;
+        const int vk = min(nkeys, pos0 + m + 1 - kstart);
+        const float s0 = l < vk ? sc[col][l] : -FLT_MAX, s1 = l + 32 < vk ? sc[col][l + 32] : -FLT_MAX;
         float mx = fmaxf(s0, s1);
         mx = xor_max<1>(xor_max<2>(xor_max<4>(xor_max<8>(xor_max<16>(mx)))));  // inside each 32-lane half
         const float e0 = l < vk ? expf(s0 - mx) : 0.0f, e1 = l + 32 < vk ? expf(s1 - mx) : 0.0f;
-        sc[c][l] = e0;
-        sc[c][l + 32] = e1;
+        sc[col][l] = e0;
+        sc[col][l + 32] = e1;
         float sum = e0 + e1;
         sum = xor_sum<1>(xor_sum<2>(xor_sum<4>(xor_sum<8>(xor_sum<16>(sum)))));
         if (l == 0) {
-            smax[c] = vk > 0 ? mx : -1e30f;
-            ssum[c] = sum;
+            smax[col] = vk > 0 ? mx : -1e30f;
+            ssum[col] = sum;
         }
     }
     lds_barrier();
 
-    // ---- values: thread (dim pair dp, key half kh2) ----
-    float2 acc[NC];
+    // ---- values: lane (column n, k-group g) ends with dims 64w + 16dt + 4g + r ----
+    f32x4_t o[4];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) acc[c] = make_float2(0.0f, 0.0f);
+    for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i4 = 0; i4 < KH; i4 += 4) {
-        float4 wt[NC];
+    for (int ks = 0; ks < kPart / 32; ++ks) {
+        half8_t ph, pl;
+        const float4 pa = *reinterpret_cast<const float4*>(&sc[n][32 * ks + 8 * g]);
+        const float4 pb = *reinterpret_cast<const float4*>(&sc[n][32 * ks + 8 * g + 4]);
+        const float pv[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) wt[c] = *reinterpret_cast<const float4*>(&sc[c][kh2 * KH + i4]);
+        for (int e = 0; e < 8; ++e) {
+            const _Float16 hv = (_Float16)pv[e];
+            ph[e] = hv;
+            pl[e] = (_Float16)(pv[e] - (float)hv);
+        }
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            const float v0 = h2f(vw[i4 + ii] & 0xFFFF), v1 = h2f(vw[i4 + ii] >> 16);
+        for (int dt = 0; dt < 4; ++dt) {
+            half8_t va;
+            const _Float16* vp = vt + (32 * ks + 8 * g) * VROW + 64 * w + 16 * dt + n;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                const float wv = ii == 0 ? wt[c].x : ii == 1 ? wt[c].y : ii == 2 ? wt[c].z : wt[c].w;
-                acc[c].x = fmaf(wv, v0, acc[c].x);
-                acc[c].y = fmaf(wv, v1, acc[c].y);
-            }
+            for (int e = 0; e < 8; ++e) va[e] = vp[e * VROW];
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
         }
     }
-    if (kh2 == 1)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) vred[c][dp] = acc[c];
-    __syncthreads();
-    if (kh2 == 0) {
+    if (cm >= 0) {
         const int parts_max = (a.ctx + kPart - 1) / kPart;
+        float* out = a.partial + (((size_t)cm * a.n_heads + kh * G + chh) * parts_max + p) * (HD + 2);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) {
-            const int m = c / G, hh = kh * G + c % G;
-            float* o = a.partial + (((size_t)m * a.n_heads + hh) * parts_max + p) * (HD + 2);
-            const float2 u = vred[c][dp];
-            o[2 * dp] = acc[c].x + u.x;
-            o[2 * dp + 1] = acc[c].y + u.y;
-            if (dp == 0) {
-                o[HD] = smax[c];
-                o[HD + 1] = ssum[c];
-            }
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) out[64 * w + 16 * dt + 4 * g + r] = o[dt][r];
+        if (w == 0 && g == 0) {
+            out[HD] = smax[n];
+            out[HD + 1] = ssum[n];
         }
     }
 }
