@@ -349,8 +349,10 @@ __global__ __launch_bounds__(kGemmThreads) void mgemm_kernel(GemmArgs a, int rpa
         // of stage st + 1) is outstanding; every read of this wave is complete.  After the
         // barrier every wave's copies of stage st have landed and every wave has read stage
         // st - 1, whose buffer `next` then takes stage st + 2.
-        // no instruction of the previous step moves past this point, no LDS access across the
-        // barrier
+        // no instruction of the previous step moves past this point (its LDS reads stay ahead of
+        // the wait, so they are complete before the barrier lets another wave overwrite their
+        // buffer), and no LDS access of this step moves above the barrier
+        asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
         if (st + 1 < nst) __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(G::NC_MIN));
         else __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(0));
