@@ -159,6 +159,7 @@ struct snl_engine {
     // attention_prefill.hip)
     float *pf_x = nullptr, *pf_proj = nullptr, *pf_act = nullptr, *pf_attn = nullptr, *pf_qbuf = nullptr,
           *pf_br = nullptr, *pf_xs = nullptr, *pf_part = nullptr, *pf_coef = nullptr, *pf_ssq = nullptr;
+    float* pf_pairs = nullptr;  // prefill DeltaNet: k.k / k.q inside blocks of 4 tokens
     float *pf_dq = nullptr, *pf_dk = nullptr, *pf_dv = nullptr, *pf_gz = nullptr, *pf_beta = nullptr,
           *pf_decay = nullptr;
     void* pf_frags = nullptr;
@@ -614,7 +615,8 @@ int snl_engine::init() {
             (rc = dalloc(&pf_act, P * c.intermediate)) || (rc = dalloc(&pf_attn, P * attn_w)) ||
             (rc = dalloc(&pf_qbuf, P * q_dim)) || (rc = dalloc(&pf_br, P * h)) || (rc = dalloc(&pf_xs, P)) ||
             (rc = dalloc(&pf_part, P * 9)) || (rc = dalloc(&pf_coef, P * 8)) ||
-            (rc = dalloc(&pf_ssq, P * nv * kDeltaGroups)) || (rc = dalloc(&pf_dq, P * std::max<size_t>(key_dim, 1))) ||
+            (rc = dalloc(&pf_ssq, P * nv * kDeltaPrefillGroups)) ||
+            (rc = dalloc(&pf_pairs, dn_pairs_floats((int)P, std::max(c.lin_k_heads, 1)))) || (rc = dalloc(&pf_dq, P * std::max<size_t>(key_dim, 1))) ||
             (rc = dalloc(&pf_dk, P * std::max<size_t>(key_dim, 1))) || (rc = dalloc(&pf_dv, P * lin_value_dim + 1)) ||
             (rc = dalloc(&pf_gz, P * lin_value_dim + 1)) || (rc = dalloc(&pf_beta, P * nv)) ||
             (rc = dalloc(&pf_decay, P * nv)) || (rc = dalloc((uint8_t**)&pf_frags, frags_bytes(SNL_PF_M, kmax))) ||
@@ -819,6 +821,7 @@ int snl_engine::record_prefill(int M, int rows) {
             d.gz = pf_gz;
             d.beta = pf_beta;
             d.decay = pf_decay;
+            d.pairs = pf_pairs;
             d.out = pf_attn;
             d.ssq = pf_ssq;
             d.conv_dim = conv_dim;

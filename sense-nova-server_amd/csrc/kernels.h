@@ -66,7 +66,7 @@ int gemv_init();
 // ---------------------------------------------------------------- prefill GEMM (mgemm.hip)
 // Token rows -> the GEMM's f16 hi/lo A fragments, with the branch input computed on the way:
 // the rows as they are, RMSNorm(x0) * (1 + w), the mHC pre-mix then that norm (coef[m][0..1]),
-// or the head factor of the DeltaNet gated norm (ssq partials [M][K/128][4]).
+// or the head factor of the DeltaNet gated norm (ssq partials [M][K/128][kDeltaPrefillGroups]).
 enum RowsMode { ROWS_PLAIN = 0, ROWS_NORM = 1, ROWS_NORM_MHC = 2, ROWS_GNORM = 3 };
 struct RowsArgs {
     const float* x;      // token row m at x + m * x_stride (NORM_MHC: stream 1 at +h)
@@ -163,6 +163,8 @@ struct DeltaArgs {
     const StepDev* step;  // s_in / s_out / s_ck / ckpt
 };
 constexpr int kDeltaGroups = 4;  // column groups per value head (partials per head in ssq)
+// column groups per value head of the prefill recurrence (partials per head in its ssq)
+constexpr int kDeltaPrefillGroups = 8;
 int launch_deltanet(const DeltaArgs& a, int M, hipStream_t s);
 // the gated RMS norm in place on out (kernel-level entry; the engine folds it into out_proj)
 int launch_deltanet_norm(const DeltaArgs& a, int M, hipStream_t s);
@@ -184,10 +186,12 @@ struct DnPrefillArgs {
     float *v, *gz;       // scratch [M][n_v][128]: conv output, silu(z)
     float *beta, *decay; // scratch [M][n_v]
     float* out;          // [M, n_v*128] (o * w) * silu(z), before the head factor of the norm
-    float* ssq;          // [M, n_v, 4] partial sums of o^2 per column group
+    float* ssq;          // [M, n_v, kDeltaPrefillGroups] partial sums of o^2 per column group
+    float* pairs;        // scratch of dn_pairs_floats(M, n_k): k.k and k.q inside blocks of tokens
     int conv_dim, n_k, n_v;
 };
 int launch_deltanet_prefill(const DnPrefillArgs& a, int M, hipStream_t s);
+size_t dn_pairs_floats(int M, int n_k);
 
 // ---------------------------------------------------------------- sampler (sampler.hip)
 // src/sampler.rs:99-106: repetition, presence and frequency penalties on logits[tok[i]] in place

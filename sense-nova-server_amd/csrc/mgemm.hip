@@ -197,8 +197,11 @@ __global__ __launch_bounds__(kRowThreads) void rows_to_frags_kernel(RowsArgs a) 
         for (int gi = 0; gi < GPT; ++gi) {
             const int u = tid + kRowThreads * gi;
             if (u < ngr) {
-                const float* ps = a.ssq + ((size_t)m * (K / 128) + u / 16) * kDeltaGroups;
-                const float var_o = (((ps[0] + ps[1]) + ps[2]) + ps[3]) / 128.0f;
+                const float* ps = a.ssq + ((size_t)m * (K / 128) + u / 16) * kDeltaPrefillGroups;
+                float t = ps[0];
+#pragma unroll
+                for (int gi = 1; gi < kDeltaPrefillGroups; ++gi) t = t + ps[gi];
+                const float var_o = t / 128.0f;
                 const float f = 1.0f / sqrtf(var_o + a.eps);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[gi][e] = v[gi][e] * f;
