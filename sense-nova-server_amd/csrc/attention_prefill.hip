@@ -7,7 +7,8 @@
 //
 // attend: block (kv head, 16 queries, key part), wave w = query head 4*kv + w of the GQA group;
 // the block streams its part of the keys [0, last query's position] (4096 keys per part) in steps
-// of 32 through LDS (K rows, and V transposed so that each MFMA A fragment is two 8-byte reads),
+// of 32 through LDS (K rows and V rows, each staged with 16-byte copies; the V^T fragments come
+// back from the V rows through the transposing LDS read, two 8-byte reads per fragment),
 // shared by the group's 4 heads.
 //   scores  S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims of K (exact f16),
 //           B = the query's dims split into f16 hi + lo under a per-query power of two, so the
@@ -36,10 +37,11 @@ constexpr int HD = 256, G = 4;
 constexpr int QTILE = 16, KB = 32;
 constexpr int KPART = 4096;  // keys per part when a long context splits the key range
 constexpr int KROW = HD + 8;  // K tile row (halfs): 528 bytes keeps the 16 rows of a read on distinct banks
-constexpr int VROW = KB + 4;  // V^T row (halfs): 72 bytes
+constexpr int VROW = HD + 16;  // V row (halfs): 544 bytes, so the 4 rows of a transposed read hit distinct banks
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void pf_prep_kernel(AttnArgs a, const PrefillDev* st) {
@@ -84,7 +86,7 @@ __global__ __launch_bounds__(256) void pf_prep_kernel(AttnArgs a, const PrefillD
 __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const PrefillDev* st, int M, float* part,
                                                         int parts_max) {
     __shared__ __align__(16) _Float16 ks[KB * KROW];
-    __shared__ __align__(16) _Float16 vt[HD * VROW];
+    __shared__ __align__(16) _Float16 vs[KB * VROW];
     const int kh = blockIdx.x, q0 = blockIdx.y * QTILE;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hh = kh * G + w;
@@ -153,21 +155,20 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
 #pragma unroll
             for (int i = 0; i < 4; ++i) dst[i] = r[i];
         }
+        {   // V rows, as the K rows: thread (key t >> 3, 32 dims)
+            const int key = tid >> 3, seg = tid & 7;
+            const int kk = kb + key;
+            uint4 r[4];
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {  // V transposed: item (key pair, 8 dims)
-            const int item = tid + 256 * it;
-            const int kp = item >> 5, dg = item & 31;
-            const int k0 = kb + 2 * kp;
-            uint4 v0 = make_uint4(0u, 0u, 0u, 0u), v1 = make_uint4(0u, 0u, 0u, 0u);
-            if (k0 < kstop) v0 = *reinterpret_cast<const uint4*>(vc + (size_t)k0 * kv_dim + dg * 8);
-            if (k0 + 1 < kstop) v1 = *reinterpret_cast<const uint4*>(vc + (size_t)(k0 + 1) * kv_dim + dg * 8);
-            const uint32_t a0[4] = {v0.x, v0.y, v0.z, v0.w}, a1[4] = {v1.x, v1.y, v1.z, v1.w};
+            for (int i = 0; i < 4; ++i) r[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (kk < kstop) {
+                const uint4* src = reinterpret_cast<const uint4*>(vc + (size_t)kk * kv_dim + seg * 32);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t lo = (a0[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-                const uint32_t hi = (a1[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
-                *reinterpret_cast<uint32_t*>(vt + (dg * 8 + i) * VROW + 2 * kp) = lo | (hi << 16);
+                for (int i = 0; i < 4; ++i) r[i] = src[i];
             }
+            uint4* dst = reinterpret_cast<uint4*>(vs + key * VROW + seg * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = r[i];
         }
         __syncthreads();
 
@@ -217,9 +218,15 @@ __global__ __launch_bounds__(256) void pf_attend_kernel(AttnArgs a, const Prefil
 #pragma unroll
         for (int dt = 0; dt < 16; ++dt) {
             o[dt] = o[dt] * factor;
-            const _Float16* vr = vt + (16 * dt + j) * VROW;
-            const half4_t va = *reinterpret_cast<const half4_t*>(vr + 4 * g);
-            const half4_t vb = *reinterpret_cast<const half4_t*>(vr + 16 + 4 * g);
+            // transposed reads (ds_read_b64_tr_b16): in each 16-lane group, lane 4a + b receives
+            // element b of the 8 bytes addressed by lanes a, a + 4, a + 8, a + 12; lane s
+            // addresses key 4g + s / 4 (then 16 + 4g + s / 4), dims 16 dt + 4 (s % 4), so lane j
+            // receives dim 16 dt + j of keys 4g .. 4g + 3 (then 16 + 4g ..)
+            const _Float16* pa = vs + (4 * g + (j >> 2)) * VROW + 16 * dt + 4 * (j & 3);
+            const half4_t va = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4_t*)(pa)));
+            const half4_t vb = __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4_t*)(pa + 16 * VROW)));
             const half8_t vf = half8_t{va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, ph, o[dt], 0, 0, 0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pl, o[dt], 0, 0, 0);
