@@ -82,6 +82,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, un
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // Block (kv head, part of kPart keys) for all M tokens and the 4 query heads of the GQA group,
 // 256 threads = 4 waves, on v_mfma_f32_16x16x32_f16.  The 16 MFMA columns hold the head-token
@@ -101,7 +102,7 @@ template <int M>
 __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     constexpr int NC = G * M;
     static_assert(NC == 4 || NC == 8, "M = 1 or 2");
-    constexpr int VROW = HD + 8;  // V tile row in halfs (528 bytes)
+    constexpr int VROW = HD + 16;  // V tile row in halfs (544 bytes: a transposed read's 4 rows on distinct banks)
     __shared__ __align__(16) _Float16 vt[kPart * VROW];
     __shared__ __align__(16) float sc[16][kPart];  // by MFMA column
     __shared__ float smax[16], ssum[16];
@@ -215,10 +216,14 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
         }
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-            half8_t va;
-            const _Float16* vp = vt + (32 * ks + 8 * g) * VROW + 64 * w + 16 * dt + n;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) va[e] = vp[e * VROW];
+            // transposed reads (ds_read_b64_tr_b16): in each 16-lane group, lane 4a + b receives
+            // element b of the 8 bytes addressed by lanes a, a + 4, a + 8, a + 12; lane s
+            // addresses key 32ks + 8g + s / 4 (then + 4), dims 64w + 16dt + 4 (s % 4), so lane n
+            // receives dim 64w + 16dt + n of its 8 keys
+            const _Float16* vp = vt + (32 * ks + 8 * g + (n >> 2)) * VROW + 64 * w + 16 * dt + 4 * (n & 3);
+            const short4_t v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(vp));
+            const short4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t*)(vp + 4 * VROW));
+            const half8_t va = __builtin_bit_cast(half8_t, __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7));
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph, o[dt], 0, 0, 0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[dt], 0, 0, 0);
         }
