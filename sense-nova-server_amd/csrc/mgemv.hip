@@ -183,19 +183,21 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const int wv = lane * 16, sv = lane * CS * 4;
     // The scales first, then the quants; the scheduling barrier keeps chunks in issue order.  The
     // whole offset goes in the per-lane operand: the range check covers that operand and the
-    // instruction offset.
+    // instruction offset.  Both carry the non-temporal hint (cache-policy argument 2): a decode
+    // pass reads every weight once, and at normal priority that stream would evict the token
+    // rows, recurrent state and key/value cache that the following kernels read again.
     auto issue = [&](uint4 (&w)[CL], float (&sc)[CS], int q) {
         const int so = sv + q * (int)cstride * 64 * CS * 4;
         if constexpr (CS == 2) {
-            const snl_f32x2_t t = snl_raw_buffer_load_f32x2(sr, so, 0, 0);
+            const snl_f32x2_t t = snl_raw_buffer_load_f32x2(sr, so, 0, 2);
             sc[0] = t.x, sc[1] = t.y;
         } else {
-            sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 0));
+            sc[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, so, 0, 2));
         }
         const int wo = wv + q * (int)cstride * CL * 1024;
 #pragma unroll
         for (int v = 0; v < CL; ++v)
-            w[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo + v * 1024, 0, 0));
+            w[v] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(wr, wo + v * 1024, 0, 2));
         __builtin_amdgcn_sched_barrier(0);
     };
     // ---- prologue, part 1: every load of the token rows comes before the first weight load ----
