@@ -282,7 +282,7 @@ def main() -> int:
             d[2] += ms
     if args.op_times:
         for name in sorted(per_op):
-            if name in ("copy", "end"):
+            if name in ("copy", "norm", "end"):
                 continue
             ms, b, n = eng.time_op(name, args.roofline_reps)
             gbs = b / (ms * 1e-3) / 1e9 if b > 0 else 0.0

@@ -112,7 +112,7 @@ int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uin
  * events on the engine stream, and reports the mean time per launch, the algorithmic HBM bytes
  * per launch (0 where not counted) and the launches per pass.  Skipped ops leave the inputs as
  * they are; nothing is committed (position, state slot and carried hidden row are unchanged).
- * "copy" is refused. */
+ * "copy" and "norm" (the final norm, which also writes the carried hidden row) are refused. */
 int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch, double* bytes_per_launch,
                 int* launches_per_pass);
 

@@ -449,8 +449,9 @@ struct snl_engine {
     }
     int consumed_n = 0;  // partial count a NORM_MHC launch adds up
     int norm(const float* xin, int x_stride, const int32_t* row_base, int mode, const float* w, float* out,
-             int first, int count) {
+             int first, int count, float* last_copy = nullptr) {
         NormArgs a{};
+        a.last_copy = last_copy;
         a.x = xin;
         a.x_stride = x_stride;
         a.row_base = row_base;
@@ -666,8 +667,9 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
     // the checkpoint request itself travels in the step record
     const snl_config& c = cfg;
     int rc = 0;
-    if (op("embed", 0.0)) rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream);
-    if (op("copy", 0.0)) rc |= launch_copy(hid, hlast, h, stream);  // row 0 = hidden of the token before this step
+    // the same launch copies hlast into hid row 0 (the hidden of the token before this step)
+    if (op("embed", 0.0))
+        rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream, hlast, hid);
     int fslot = 0, lslot = 0;
     const size_t kvn = (size_t)ctx * kv_dim;
     const size_t nl = std::max(n_lin, 1);
@@ -740,12 +742,12 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
                    GEMV_PLAIN, nullptr, nullptr,
                    MhcRole{mhc ? L.mhc_ffn.p : nullptr, leave ? layers[ln].mhc_attn.p : nullptr, next_start ? 1 : 0});
     }
-    rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M);
+    // the last row's output also lands in hlast (the hidden carried to the next pass)
+    rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M, hlast);
     if (rows > 0) {
         rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
         if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
     }
-    if (op("copy", 0.0)) rc |= launch_copy(hlast, hid + (size_t)M * h, h, stream);
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
 }
@@ -1260,7 +1262,8 @@ int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch
     if (!e || !name || reps < 1 || !ms_per_launch) return SNL_EARG;
     e->err.clear();
     ++e->epoch;
-    if (!strcmp(name, "copy")) return e->fail(SNL_EARG, "time_op: 'copy' moves the carried hidden row");
+    if (!strcmp(name, "copy") || !strcmp(name, "norm"))
+        return e->fail(SNL_EARG, "time_op: '%s' writes the carried hidden row", name);
     if (e->pos + 2 > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + 2, e->ctx);
     // a verify pass (2 rows, checkpoint) at the current position; nothing is committed
     StepDev& st = e->h_step[0];

@@ -100,9 +100,10 @@ int launch_rows_to_frags(const RowsArgs& a, hipStream_t s);
 int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s);
 
 // ---------------------------------------------------------------- layers (layers.hip)
-// x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790)
+// x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790); with carry_src, one
+// more block copies h floats from carry_src to carry_dst in the same launch
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
-                 hipStream_t s);
+                 hipStream_t s, const float* carry_src = nullptr, float* carry_dst = nullptr);
 
 // out[r] = rmsnorm(branch input of row first+r) * (one + w) for r < count (layers.wgsl:46-73).
 // mode 1 mixes the two streams with coef[row][0..1].  Row `row` of x starts at
@@ -121,6 +122,7 @@ struct NormArgs {
     int count;
     float eps;
     float one;
+    float* last_copy;  // nullable: the last row's output is also written here
 };
 int launch_branch_norm(const NormArgs& a, hipStream_t s);
 

@@ -11,17 +11,36 @@ namespace snl {
 
 namespace {
 
-__global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const int8_t* eq, const float* es, int vocab,
-                                                     int h, float* x) {
+__global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const int8_t* __restrict__ eq,
+                                                     const float* __restrict__ es, int vocab, int h,
+                                                     float* __restrict__ x, int M, const float* carry_src,
+                                                     float* carry_dst) {
     const int m = blockIdx.x;
+    if (m == M) {  // the carried row (launched only with carry_src)
+        for (int i = threadIdx.x; i * 4 < h; i += 256)
+            reinterpret_cast<float4*>(carry_dst)[i] = reinterpret_cast<const float4*>(carry_src)[i];
+        return;
+    }
     uint32_t tok = step->tokens[m];
     if (tok >= (uint32_t)vocab) tok = 0;  // the host rejects out-of-range ids before launching
     const int8_t* q = eq + (size_t)tok * h;
     const float* s = es + (size_t)tok * (h / 32);
     float* xr = x + (size_t)m * 2 * h;
-    for (int i = threadIdx.x; i < h; i += 256) {
-        xr[i] = (float)q[i] * s[i >> 5];
-        xr[h + i] = 0.0f;
+    // piece p: 16 consecutive quants (half of quant block p / 2), one 16-byte load and its scale,
+    // both issued before any store
+    for (int p = threadIdx.x; p * 16 < h; p += 256) {
+        const uint4 w = *reinterpret_cast<const uint4*>(q + 16 * p);
+        const float sc = s[p >> 1];
+        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+        float4* o = reinterpret_cast<float4*>(xr + 16 * p);
+        float4* z = reinterpret_cast<float4*>(xr + h + 16 * p);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t v = wd[k];
+            o[k] = make_float4((float)(int8_t)(v & 0xffu) * sc, (float)(int8_t)((v >> 8) & 0xffu) * sc,
+                               (float)(int8_t)((v >> 16) & 0xffu) * sc, (float)(int8_t)(v >> 24) * sc);
+            z[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
     }
 }
 
@@ -75,6 +94,7 @@ __global__ __launch_bounds__(256) void branch_norm_kernel(NormArgs a) {
             o.z = (v[j].z * rinv) * (a.one + w.z);
             o.w = (v[j].w * rinv) * (a.one + w.w);
             ob[i] = o;
+            if (a.last_copy && r == a.count - 1) reinterpret_cast<float4*>(a.last_copy)[i] = o;
         }
     }
 }
@@ -290,14 +310,20 @@ inline int last_error() { return hipGetLastError() == hipSuccess ? 0 : -2; }
 }  // namespace
 
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
-                 hipStream_t s) {
-    if (M < 1 || M > SNL_MAX_M || h % 32) return -1;
-    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, s, step, eq, es, vocab, h, x);
+                 hipStream_t s, const float* carry_src, float* carry_dst) {
+    if (M < 1 || M > SNL_MAX_M || h % 32 || (reinterpret_cast<uintptr_t>(eq) & 15) ||
+        (reinterpret_cast<uintptr_t>(x) & 15) || (carry_src && !carry_dst) ||
+        (reinterpret_cast<uintptr_t>(carry_src) & 15) || (reinterpret_cast<uintptr_t>(carry_dst) & 15))
+        return -1;
+    hipLaunchKernelGGL(embed_kernel, dim3(M + (carry_src ? 1 : 0)), dim3(256), 0, s, step, eq, es, vocab, h, x, M,
+                       carry_src, carry_dst);
     return last_error();
 }
 
 int launch_branch_norm(const NormArgs& a, hipStream_t s) {
-    if (a.count < 1 || a.h > 8192 || a.h < 4 || a.h % 4 || a.x_stride % 4 || a.out_stride % 4) return -1;
+    if (a.count < 1 || a.h > 8192 || a.h < 4 || a.h % 4 || a.x_stride % 4 || a.out_stride % 4 ||
+        (reinterpret_cast<uintptr_t>(a.last_copy) & 15))
+        return -1;
     hipLaunchKernelGGL(branch_norm_kernel, dim3(a.count), dim3(256), 0, s, a);
     return last_error();
 }
