@@ -173,6 +173,25 @@ def test_rollback_equals_never_run(pair):
     assert pk1[0].token == pk2[0].token and pk1[0].top1 == pk2[0].top1
 
 
+def test_carried_hidden_row(pair):
+    """forward_mm (src/engine.rs:801-936) starts a pass with hlast in hid row 0 and ends it with the
+    last token's normalized hidden in hlast; both copies ride in the embed and final-norm launches."""
+    cfg, g, o = pair
+    h = cfg.hidden
+    n = 6
+    g.reset()
+    g.forward(_prompt(n, cfg.vocab, seed=11), [[i] * 3 for i in range(n)], logit_rows=1)
+    g.forward([5, 6], [[n] * 3, [n + 1] * 3], logit_rows=2)
+    hid = g.buffer(1)[: 3 * h].reshape(3, h)
+    carried = g.buffer(2)[:h]
+    assert np.array_equal(carried, hid[2])
+    g.forward([7], [[n + 2] * 3], logit_rows=1)
+    hid2 = g.buffer(1)[: 2 * h].reshape(2, h)
+    assert np.array_equal(hid2[0], carried)
+    assert np.array_equal(g.buffer(2)[:h], hid2[1])
+    assert not np.array_equal(hid2[1], carried)
+
+
 def test_snapshot_restore(pair):
     cfg, g, o = pair
     prompt = _prompt(20, cfg.vocab, seed=9)
