@@ -39,18 +39,25 @@ __global__ __launch_bounds__(256) void prep_kernel(AttnArgs a) {
     }
     const bool is_q = slot < a.n_heads;
     float v = is_q ? row[slot * 2 * HD + d] : row[2 * q_dim + (slot - a.n_heads) * HD + d];
+    // the norm weight and the rotary position go out with the row: a global load placed after a
+    // barrier waits for it, and each such wait is one more memory round trip
+    const float nw = a.norms[(is_q ? 0 : HD) + d];
+    const int half = a.rot_dim / 2;
+    uint32_t rot_pos = 0;
+    if (d < a.rot_dim) {
+        const int fi = d % half;
+        const uint32_t* rp = st->rpos[m];
+        rot_pos = rp[0];
+        if (fi % 3 == 1 && (uint32_t)fi < (a.mrope >> 16)) rot_pos = rp[1];
+        else if (fi % 3 == 2 && (uint32_t)fi < (a.mrope & 0xFFFFu)) rot_pos = rp[2];
+    }
     const float total = block_sum<256>(v * v, red);
-    v = (v * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + a.norms[(is_q ? 0 : HD) + d]);
+    v = (v * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nw);
     sh[d] = v;
     __syncthreads();
-    const int half = a.rot_dim / 2;
     if (d < a.rot_dim) {
         const int fi = d % half;
         const float inv_freq = powf(a.rope_theta, -(float)(2 * fi) / (float)a.rot_dim);
-        const uint32_t* rp = st->rpos[m];
-        uint32_t rot_pos = rp[0];
-        if (fi % 3 == 1 && (uint32_t)fi < (a.mrope >> 16)) rot_pos = rp[1];
-        else if (fi % 3 == 2 && (uint32_t)fi < (a.mrope & 0xFFFFu)) rot_pos = rp[2];
         const float ang = (float)rot_pos * inv_freq;
         const float cs = cosf(ang), sn = sinf(ang);
         v = d < half ? sh[d] * cs - sh[d + half] * sn : sh[d] * cs + sh[d - half] * sn;
@@ -255,13 +262,20 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
     const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
     const int dl = tid & (kCombDims - 1), q = tid / kCombDims;
     const int d = blockIdx.z * kCombDims + dl;
-    const int total = a.step->pos0 + m + 1;
-    const int np = (total + kPart - 1) / kPart;
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     const float* base = a.partial + ((size_t)m * a.n_heads + h) * parts_max * (HD + 2);
+    // Every load that does not need the key count goes out first, in one round trip: the part
+    // maxima and weights and this thread's first partial value (all inside the parts_max rows of
+    // the buffer; parts past the count are masked below) and the output gate.
+    const float mp0 = tid < parts_max ? base[(size_t)tid * (HD + 2) + HD] : -1e30f;
+    const float lp0 = tid < parts_max ? base[(size_t)tid * (HD + 2) + HD + 1] : 0.0f;
+    const float pv0 = q < parts_max ? base[(size_t)q * (HD + 2) + d] : 0.0f;
+    const float gate = q == 0 ? a.proj[(size_t)m * a.proj_stride + h * 2 * HD + HD + d] : 0.0f;
+    const int total = a.step->pos0 + m + 1;
+    const int np = (total + kPart - 1) / kPart;
     // global max of the part maxima (np <= kMaxParts = kCombThreads: one part per thread)
-    const float mp = tid < np ? base[(size_t)tid * (HD + 2) + HD] : -1e30f;
-    const float lp = tid < np ? base[(size_t)tid * (HD + 2) + HD + 1] : 0.0f;
+    const float mp = tid < np ? mp0 : -1e30f;
+    const float lp = tid < np ? lp0 : 0.0f;
     float mx = wave_max(mp);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
@@ -273,15 +287,15 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
     if (tid < np) fs[tid] = f;
     const float l = block_sum<kCombThreads>(lp * f, red);  // the sum of the parts' weights
     float acc = 0.0f;
+    if (q < np) acc = acc + pv0 * fs[q];
 #pragma unroll 8
-    for (int p = q; p < np; p += kCombGroups) acc = acc + base[(size_t)p * (HD + 2) + d] * fs[p];
+    for (int p = q + kCombGroups; p < np; p += kCombGroups) acc = acc + base[(size_t)p * (HD + 2) + d] * fs[p];
     accq[q][dl] = acc;
     __syncthreads();
     if (q == 0) {
         float v = accq[0][dl];
 #pragma unroll
         for (int g = 1; g < kCombGroups; ++g) v = v + accq[g][dl];
-        const float gate = a.proj[(size_t)m * a.proj_stride + h * 2 * HD + HD + d];
         a.out[(size_t)m * a.n_heads * HD + h * HD + d] = v / l / (1.0f + expf(-gate));
     }
 }
