@@ -62,13 +62,15 @@ typedef struct snl_engine snl_engine;
 /* Engine::load (src/engine.rs:230-644) with weights drawn on the device from `seed`
  * (quant 0 = Q8_0, 1 = Q4_0 for the matrices a Q4_0 file quantises; embedding, LM head,
  * DeltaNet in_proj and the MTP head stay Q8_0 as in src/convert.rs:228-311).
- * ctx = KV positions per attention layer.  Returns SNL_OK and *out, or an error. */
+ * ctx = KV positions per attention layer, 2..262144 (the reference's default max_position;
+ * larger values return SNL_ECTX).  Returns SNL_OK and *out, or an error. */
 int snl_engine_create(const snl_config* cfg, uint64_t seed, int quant, int ctx, snl_engine** out);
 /* Engine::load (src/engine.rs:230-644) from the reference's `.snl` weight files
  * (src/weights.rs:1-121): `path` the text model, `mtp_path` (nullable) the MTP head, as written
  * by the converter (src/convert.rs:316-427).  Matrices keep each tensor's dtype (q8_0 / q4_0);
- * ctx is clamped to the model's max_position.  The vision tower is not loaded.  Errors (missing
- * or misshapen tensors, bad header) return SNL_EARG with the message in snl_create_error(). */
+ * ctx is clamped to the model's max_position, and above 262144 returns SNL_ECTX.  The vision
+ * tower is not loaded.  Errors (missing or misshapen tensors, bad header) return SNL_EARG with
+ * the message in snl_create_error(). */
 int snl_engine_load(const char* path, const char* mtp_path, int ctx, snl_engine** out);
 /* The converter's output (src/convert.rs:316-427) for the engine's current weights: the text model
  * to `path` and, when mtp_path is not NULL, the MTP head to mtp_path, so that snl_engine_load
@@ -112,7 +114,8 @@ int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uin
  * events on the engine stream, and reports the mean time per launch, the algorithmic HBM bytes
  * per launch (0 where not counted) and the launches per pass.  Skipped ops leave the inputs as
  * they are; nothing is committed (position, state slot and carried hidden row are unchanged).
- * "copy" and "norm" (the final norm, which also writes the carried hidden row) are refused. */
+ * "copy" and "norm" (the final norm, which also writes the carried hidden row) are refused, and
+ * so is any op while a checkpointed verify awaits its rollback (SNL_ESTATE). */
 int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch, double* bytes_per_launch,
                 int* launches_per_pass);
 

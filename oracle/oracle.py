@@ -361,6 +361,37 @@ class Engine:
         sa = np.ctypeslib.as_array(s, shape=(r * c // 32,)).copy()
         return qt, qa.reshape(r, -1), sa.reshape(r, -1)
 
+    def set_vector(self, layer: int, kind: int, values) -> None:
+        """Overwrite an f32 parameter vector of the engine in place (tests that need chosen values,
+        such as a zero mHC router with given biases)."""
+        q = vp()
+        s = f32p()
+        rows = ctypes.c_int32()
+        cols = ctypes.c_int32()
+        qt = lib().orc_engine_tensor(self.h, layer, kind, ctypes.byref(q), ctypes.byref(s), ctypes.byref(rows),
+                                     ctypes.byref(cols))
+        if qt != 2:
+            raise KeyError((layer, kind))
+        v = f32(values).reshape(-1)
+        if v.size != cols.value:
+            raise ValueError(f"expected {cols.value} values, got {v.size}")
+        ctypes.memmove(q.value, v.ctypes.data, v.nbytes)
+
+    def zero_rows(self, layer: int, kind: int, first: int) -> None:
+        """Set the block scales of rows first.. of a quantised matrix to zero, so those rows dequantise
+        to exactly 0 (a head whose argmax is confined to the first rows)."""
+        q = vp()
+        s = f32p()
+        rows = ctypes.c_int32()
+        cols = ctypes.c_int32()
+        qt = lib().orc_engine_tensor(self.h, layer, kind, ctypes.byref(q), ctypes.byref(s), ctypes.byref(rows),
+                                     ctypes.byref(cols))
+        if qt not in (0, 1):
+            raise KeyError((layer, kind))
+        nb = cols.value // 32
+        sa = np.ctypeslib.as_array(s, shape=(rows.value * nb,))
+        sa[first * nb:] = 0.0
+
     def generate(self, prompt: Sequence[int], max_tokens: int, spec: bool):
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         out = np.zeros(max_tokens, np.uint32)

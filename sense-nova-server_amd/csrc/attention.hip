@@ -252,11 +252,13 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 // attention.wgsl:248-269: merge the token's parts, then the sigmoid gate.  Block (head, token, 64
 // dims) of 1024 threads: every part's scale e^(max_p - max) goes to LDS once, then thread (d, q)
 // adds the parts q, q+16, ... of dim d and the 16 groups are added in order.  Many short chains
-// keep a long context's partials (512 parts at 32K keys) in flight at once.
-constexpr int kCombThreads = 1024, kCombDims = 64, kCombGroups = kCombThreads / kCombDims, kMaxParts = 1024;
+// keep a long context's partials (512 parts at 32K keys) in flight at once.  Past 1024 parts
+// (64K keys) thread t also takes the parts t + 1024, t + 2048, ... for the maximum and the weights;
+// the order of every sum depends on the token's part count alone.
+constexpr int kCombThreads = 1024, kCombDims = 64, kCombGroups = kCombThreads / kCombDims;
 
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
-    __shared__ float fs[kMaxParts];
+    __shared__ float fs[kAttnMaxParts];
     __shared__ float red[kCombThreads / 64];
     __shared__ float accq[kCombGroups][kCombDims];
     const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
@@ -273,19 +275,28 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
     const float gate = q == 0 ? a.proj[(size_t)m * a.proj_stride + h * 2 * HD + HD + d] : 0.0f;
     const int total = a.step->pos0 + m + 1;
     const int np = (total + kPart - 1) / kPart;
-    // global max of the part maxima (np <= kMaxParts = kCombThreads: one part per thread)
-    const float mp = tid < np ? mp0 : -1e30f;
-    const float lp = tid < np ? lp0 : 0.0f;
-    float mx = wave_max(mp);
+    // global max of the part maxima
+    float mx = tid < np ? mp0 : -1e30f;
+    for (int p = tid + kCombThreads; p < np; p += kCombThreads) mx = fmaxf(mx, base[(size_t)p * (HD + 2) + HD]);
+    mx = wave_max(mx);
     if ((tid & 63) == 0) red[tid >> 6] = mx;
     __syncthreads();
     mx = red[0];
 #pragma unroll
     for (int w = 1; w < kCombThreads / 64; ++w) mx = fmaxf(mx, red[w]);
     __syncthreads();
-    const float f = tid < np ? expf(mp - mx) : 0.0f;
-    if (tid < np) fs[tid] = f;
-    const float l = block_sum<kCombThreads>(lp * f, red);  // the sum of the parts' weights
+    float lsum = 0.0f;
+    if (tid < np) {
+        const float f = expf(mp0 - mx);
+        fs[tid] = f;
+        lsum = lp0 * f;
+    }
+    for (int p = tid + kCombThreads; p < np; p += kCombThreads) {
+        const float f = expf(base[(size_t)p * (HD + 2) + HD] - mx);
+        fs[p] = f;
+        lsum = lsum + base[(size_t)p * (HD + 2) + HD + 1] * f;
+    }
+    const float l = block_sum<kCombThreads>(lsum, red);  // the sum of the parts' weights
     float acc = 0.0f;
     if (q < np) acc = acc + pv0 * fs[q];
 #pragma unroll 8
@@ -304,7 +315,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
 
 int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
     if (M < 1 || M > 2 || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2) return -1;
-    if ((a.ctx + kPart - 1) / kPart > kMaxParts) return -1;
+    if (a.ctx > kMaxCtx) return -1;
     hipLaunchKernelGGL(prep_kernel, dim3(a.n_heads + 2 * a.n_kv, M), dim3(256), 0, s, a);
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     dim3 grid(a.n_kv, parts_max);

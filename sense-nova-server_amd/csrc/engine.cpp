@@ -944,9 +944,14 @@ int snl_engine_create(const snl_config* cfg, uint64_t seed, int quant, int ctx, 
         g_create_error = std::string("unsupported model configuration: ") + why;
         return SNL_EARG;
     }
-    if ((quant != 0 && quant != 1) || ctx < 2 || ctx > (1 << 22)) {
+    if ((quant != 0 && quant != 1) || ctx < 2) {
         g_create_error = "bad quant or ctx";
         return SNL_EARG;
+    }
+    if (ctx > kMaxCtx) {
+        g_create_error = "ctx " + std::to_string(ctx) + " exceeds the largest supported context (" +
+                         std::to_string(kMaxCtx) + " positions)";
+        return SNL_ECTX;
     }
     snl_engine* e = new snl_engine();
     e->cfg = *cfg;
@@ -992,9 +997,14 @@ int snl_engine_load(const char* path, const char* mtp_path, int ctx, snl_engine*
         return SNL_EARG;
     }
     if (fc.max_position < ctx) ctx = (int)fc.max_position;
-    if (ctx < 2 || ctx > (1 << 22)) {
+    if (ctx < 2) {
         g_create_error = "bad ctx";
         return SNL_EARG;
+    }
+    if (ctx > kMaxCtx) {
+        g_create_error = "ctx " + std::to_string(ctx) + " exceeds the largest supported context (" +
+                         std::to_string(kMaxCtx) + " positions)";
+        return SNL_ECTX;
     }
     snl_engine* e = new snl_engine();
     e->cfg = cfg;
@@ -1265,6 +1275,10 @@ int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch
     if (!strcmp(name, "copy") || !strcmp(name, "norm"))
         return e->fail(SNL_EARG, "time_op: '%s' writes the carried hidden row", name);
     if (e->pos + 2 > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + 2, e->ctx);
+    // the timed passes write both state slots other than `cur`, one of which holds a pending
+    // checkpoint after a checkpointed verify
+    if (e->ck_slot >= 0)
+        return e->fail(SNL_ESTATE, "time_op: a checkpoint is pending (roll back or run another pass first)");
     // a verify pass (2 rows, checkpoint) at the current position; nothing is committed
     StepDev& st = e->h_step[0];
     memset(&st, 0, sizeof st);

@@ -224,6 +224,10 @@ struct AttnArgs {
 // prep + attend + combine for M = 1 or 2 tokens
 int launch_attention(const AttnArgs& a, int M, hipStream_t s);
 constexpr int kAttnPart = 64;  // keys per split-K part
+// Largest context (KV positions per attention layer): the reference's default max_position
+// (src/config.rs), 4096 decode parts of 64 keys.
+constexpr int kMaxCtx = 262144;
+constexpr int kAttnMaxParts = kMaxCtx / kAttnPart;
 
 // Gated attention over a chunk (attention_prefill.hip): rows m < M at cache positions pos0 + m
 // with rotary positions rpos[m]; q/k norm + RoPE, K/V into the f16 cache, then causal

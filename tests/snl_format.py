@@ -98,3 +98,40 @@ def read(path: str):
         s = np.frombuffer(data, np.float32, sb // 4, t["scales_offset"]) if sb else None
         out[name] = (t["dtype"], t["shape"], q, s)
     return header, out, data
+
+
+def tensor_kinds(cfg, mtp: bool, mtp_layer: int = 0xFFF):
+    """(layer, kind, name) of each tensor of the main or MTP file in the converter's order
+    (src/convert.rs:203-311); layer -1 for the globals, `mtp_layer` for the MTP head."""
+    if mtp:
+        ks = [(20, "fc_e"), (21, "fc_h"), (22, "norm_e"), (23, "norm_h"), (24, "norm"), (1, "in_ln"), (2, "post_ln"),
+              (3, "qk_norm"), (5, "qkv"), (6, "o_proj"), (9, "gate_up"), (10, "down")]
+        return [(mtp_layer, k, "mtp." + n) for k, n in ks]
+    out = [(-1, 1, "embed"), (-1, 2, "lm_head"), (-1, 3, "norm")]
+    for i in range(cfg.n_layers):
+        out += [(i, 1, f"l{i}.in_ln"), (i, 2, f"l{i}.post_ln")]
+        out += [(i, 3, f"l{i}.qk_norm")] if cfg.full_attention[i] else [(i, 4, f"l{i}.lin")]
+        if cfg.is_mhc(i):
+            out += [(i, 11, f"l{i}.mhc_attn"), (i, 12, f"l{i}.mhc_ffn")]
+    for i in range(cfg.n_layers):
+        if cfg.full_attention[i]:
+            out += [(i, 5, f"l{i}.qkv"), (i, 6, f"l{i}.o_proj")]
+        else:
+            out += [(i, 7, f"l{i}.in_proj"), (i, 8, f"l{i}.out_proj")]
+        out += [(i, 9, f"l{i}.gate_up"), (i, 10, f"l{i}.down")]
+    return out
+
+
+def write_engine_files(o, cfg, quant: int, main_path: str, mtp_path: str, max_position: int = 4096) -> None:
+    """Write the weights of an oracle engine `o` as the converter's two files."""
+    for is_mtp, path in ((False, main_path), (True, mtp_path)):
+        tensors = []
+        for layer, kind, name in tensor_kinds(cfg, is_mtp):
+            ot, oq, os_ = o.tensor(layer, kind)
+            if ot == 2:
+                tensors.append((name, "f32", (oq.size,), oq.astype(np.float32).tobytes(), None))
+            else:
+                cols = oq.shape[1] * (1 if ot == 0 else 2)
+                tensors.append((name, "q8_0" if ot == 0 else "q4_0", (oq.shape[0], cols), oq.tobytes(),
+                                os_.reshape(-1)))
+        write(path, "oracle", "q8_0" if is_mtp or quant == 0 else "q4_0", config_dict(cfg, max_position), tensors)

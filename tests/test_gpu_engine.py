@@ -140,7 +140,84 @@ def test_generate_matches_oracle(pair, spec):
     print(f"spec={spec} matched {matched}/64 drafted {rg['drafted']}/{ro['drafted']} "
           f"accepted {rg['accepted']}/{ro['accepted']}", flush=True)
     if matched == 64 and spec:
-        assert rg["drafted"] == ro["drafted"]
+        assert (rg["drafted"], rg["accepted"]) == (ro["drafted"], ro["accepted"])
+
+
+def test_accept_path_matches_oracle(pair):
+    """The calls the decode loop makes after an accepted draft (src/worker.rs:236-246): the verify
+    [t, d] stays committed and the MTP head then drafts over 2 pairs (hidden rows 1 and 2 of the
+    verify, tokens d and t2) at cache slot `pos before the verify`; then the next verify."""
+    cfg, g, o = pair
+    n = 12
+    prompt = _prompt(n, cfg.vocab, seed=15)
+    pos = [[i] * 3 for i in range(n)]
+    for e in (g, o):
+        e.reset()
+    g.forward(prompt, pos, logit_rows=1)
+    lg_o = o.forward(prompt, pos, logit_rows=1)
+    for e in (g, o):
+        e.mtp(1, prompt[1:], pos[:n - 1], 0, False)
+    t = int(np.argmax(lg_o[0]))
+    d_g, _, dl_g = g.mtp(g.hid_rows, [t], [[n - 1] * 3], n - 1, True, want_logits=True)
+    d_o, dl_o = o.mtp(o.hid_rows, [t], [[n - 1] * 3], n - 1, True)
+    assert np.abs(dl_g - dl_o).max() / np.abs(dl_o).max() < 1e-3
+    _check_pick(d_g, d_o, dl_o)
+    d = d_o
+    p2 = [[n] * 3, [n + 1] * 3]
+    v_g, _ = g.forward([t, d], p2, logit_rows=2, ckpt=True)
+    v_o = o.forward([t, d], p2, logit_rows=2, ckpt=True)
+    assert np.abs(v_g - v_o).max() / np.abs(v_o).max() < 1e-3
+    t2 = int(np.argmax(v_o[1]))
+    d2_g, _, dl2_g = g.mtp(1, [d, t2], p2, n, True, want_logits=True)
+    d2_o, dl2_o = o.mtp(1, [d, t2], p2, n, True)
+    assert np.abs(dl2_g - dl2_o).max() / np.abs(dl2_o).max() < 1e-3
+    _check_pick(d2_g, d2_o, dl2_o)
+    p3 = [[n + 2] * 3, [n + 3] * 3]
+    v3_g, _ = g.forward([t2, d2_o], p3, logit_rows=2, ckpt=True)
+    v3_o = o.forward([t2, d2_o], p3, logit_rows=2, ckpt=True)
+    assert np.abs(v3_g - v3_o).max() / np.abs(v3_o).max() < 1e-3
+    st_g = g.buffer(3)
+    st_o = o.buf(3, st_g.size)
+    assert np.abs(st_g - st_o).max() / np.abs(st_o).max() < 1e-2
+
+
+def _check_pick(got, ref, ref_logits):
+    """Token ids equal unless the oracle's top-2 gap is a near-tie."""
+    top = np.sort(ref_logits)[-2:]
+    assert got == ref or top[1] - top[0] < TIE, (got, ref, top[1] - top[0])
+
+
+@pytest.mark.parametrize("quant", [0, 1], ids=["q8", "q4"])
+def test_forced_acceptance_matches_oracle(snl_mod, oracle, quant, tmp_path):
+    """Random weights never accept a draft, so the accept branch of the decode loop is driven
+    with a head that confines every argmax to 5 tokens: the LM head's block scales are zeroed
+    from row 4 on (those logits are exactly 0, the first of them wins when the live rows are
+    all negative).  The same weights go to the oracle and, through a `.snl` file, to the GPU.
+    Streams, drafted and accepted counts must agree, with MTP on and off."""
+    import snl_format as F
+
+    cfg = snl_mod.tiny_config()
+    o = oracle.Engine(cfg, seed=13, quant=quant, ctx=256, max_m=512)
+    o.zero_rows(-1, oracle.K_LM_HEAD, 4)
+    main, mtp = str(tmp_path / "model.snl"), str(tmp_path / "mtp.snl")
+    F.write_engine_files(o, cfg, quant, main, mtp)
+    g = snl_mod.Engine.load(main, mtp, ctx=256)
+    try:
+        for seed in (1, 2):
+            prompt = _prompt(24, cfg.vocab, seed=seed)
+            ro = o.generate(prompt, 64, True)
+            rg = g.generate(prompt, 64, True)
+            off = g.generate(prompt, 64, False)
+            matched = _compare_streams(rg["tokens"], ro["tokens"], ro["gaps"])
+            print(f"forced acceptance quant={quant} seed={seed}: matched {matched}/64 drafted "
+                  f"{rg['drafted']}/{ro['drafted']} accepted {rg['accepted']}/{ro['accepted']}", flush=True)
+            assert ro["accepted"] > 0 and rg["accepted"] > 0
+            assert off["tokens"] == rg["tokens"]
+            if matched == 64:
+                assert (rg["drafted"], rg["accepted"]) == (ro["drafted"], ro["accepted"])
+    finally:
+        g.close()
+        o.close()
 
 
 def test_mtp_on_off_identical(pair):
@@ -256,6 +333,22 @@ def test_prompt_across_prefill_chunks(snl_mod, oracle, quant):
         st_g = g.buffer(3)
         st_o = o.buf(3, st_g.size)
         assert np.abs(st_g - st_o).max() / np.abs(st_o).max() < 1e-2
+        # the worker's feed (src/worker.rs:291-323): each 512-row chunk, then the MTP head over its
+        # pairs; then the first draft from hidden row hid_rows (the last chunk's last row)
+        chunk = g.prefill_chunk
+        for e in (g, o):
+            e.reset()
+            for c0 in range(0, 1100, chunk):
+                c1 = min(c0 + chunk, 1100)
+                e.forward(prompt[c0:c1], pos[c0:c1], logit_rows=1 if c1 == 1100 else 0)
+                r0 = 1 if c0 == 0 else 0
+                e.mtp(r0, prompt[c0 + r0:c1], pos[c0 + r0 - 1:c1 - 1], c0 + r0 - 1, False)
+        assert g.hid_rows == o.hid_rows == 1100 - 2 * chunk
+        t = int(np.argmax(lg_o[1]))
+        d_g, _, dl_g = g.mtp(g.hid_rows, [t], [[1099] * 3], 1099, True, want_logits=True)
+        d_o, dl_o = o.mtp(o.hid_rows, [t], [[1099] * 3], 1099, True)
+        assert np.abs(dl_g - dl_o).max() / np.abs(dl_o).max() < 1e-3
+        _check_pick(d_g, d_o, dl_o)
         for spec in (True, False):
             g.reset()
             o.reset()

@@ -28,25 +28,7 @@ def snl_mod():
 
 def _kinds(snl, cfg, mtp):
     """(layer, kind, name) of each tensor in the converter's order (src/convert.rs:203-311)."""
-    E = snl.engine
-    if mtp:
-        L = E.MTP_LAYER
-        ks = [(20, "fc_e"), (21, "fc_h"), (22, "norm_e"), (23, "norm_h"), (24, "norm"), (1, "in_ln"), (2, "post_ln"),
-              (3, "qk_norm"), (5, "qkv"), (6, "o_proj"), (9, "gate_up"), (10, "down")]
-        return [(L, k, "mtp." + n) for k, n in ks]
-    out = [(-1, E.K_EMBED, "embed"), (-1, E.K_LM_HEAD, "lm_head"), (-1, E.K_NORM, "norm")]
-    for i in range(cfg.n_layers):
-        out += [(i, 1, f"l{i}.in_ln"), (i, 2, f"l{i}.post_ln")]
-        out += [(i, 3, f"l{i}.qk_norm")] if cfg.full_attention[i] else [(i, 4, f"l{i}.lin")]
-        if cfg.is_mhc(i):
-            out += [(i, 11, f"l{i}.mhc_attn"), (i, 12, f"l{i}.mhc_ffn")]
-    for i in range(cfg.n_layers):
-        if cfg.full_attention[i]:
-            out += [(i, 5, f"l{i}.qkv"), (i, 6, f"l{i}.o_proj")]
-        else:
-            out += [(i, 7, f"l{i}.in_proj"), (i, 8, f"l{i}.out_proj")]
-        out += [(i, 9, f"l{i}.gate_up"), (i, 10, f"l{i}.down")]
-    return out
+    return F.tensor_kinds(cfg, mtp, snl.engine.MTP_LAYER)
 
 
 def _prompt(n, vocab, seed=1):
@@ -120,19 +102,8 @@ def test_loaded_engine_is_bitwise_the_saved_one(snl_mod, saved):
 
 def test_file_written_from_the_oracle_loads(snl_mod, saved, tmp_path):
     cfg, quant, g, o, main, mtp = saved
-    paths = []
-    for is_mtp in (False, True):
-        tensors = []
-        for layer, kind, name in _kinds(snl_mod, cfg, is_mtp):
-            ot, oq, os_ = o.tensor(layer, kind)
-            if ot == 2:
-                tensors.append((name, "f32", (oq.size,), oq.astype(np.float32).tobytes(), None))
-            else:
-                cols = oq.shape[1] * (1 if ot == 0 else 2)
-                tensors.append((name, "q8_0" if ot == 0 else "q4_0", (oq.shape[0], cols), oq.tobytes(), os_.reshape(-1)))
-        p = str(tmp_path / ("mtp.snl" if is_mtp else "model.snl"))
-        F.write(p, "oracle", "q8_0" if is_mtp or quant == 0 else "q4_0", F.config_dict(cfg, 4096), tensors)
-        paths.append(p)
+    paths = [str(tmp_path / "model.snl"), str(tmp_path / "mtp.snl")]
+    F.write_engine_files(o, cfg, quant, paths[0], paths[1])
     e = snl_mod.Engine.load(paths[0], paths[1], ctx=256)
     try:
         prompt = _prompt(7, cfg.vocab, seed=2)
