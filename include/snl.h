@@ -304,6 +304,15 @@ int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kca
 /* Greedy pick of `rows` device logits rows of length V into device picks_out. */
 int snl_pick_rows(const float* logits, int V, int rows, snl_pick* picks_out, void* stream);
 
+/* snl_pick_rows without any device allocation.  No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc).  The block partials live in a static 48 KiB device array, one per GPU, held until
+ * the process ends, so rows * ceil(V / 2048) may be at most 4096 (e.g. 33 rows of a 248320-entry
+ * vocabulary; SNL_EARG beyond).  The call only enqueues work on `stream`, a stream of the current
+ * device, and returns; picks_out is ready when the stream reaches it.  Calls that overlap on one
+ * GPU share the array and race. */
+int snl_pick_rows_noalloc(const float* logits, int V, int rows, snl_pick* picks_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

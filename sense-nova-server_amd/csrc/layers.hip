@@ -2,6 +2,9 @@
 // Semantics follow src/shaders/layers.wgsl, src/engine.rs:777-790 and src/sampler.rs:169-177.
 #include <float.h>
 
+#include <mutex>
+
+#include "../../include/snl.h"
 #include "common.h"
 #include "kernels.h"
 
@@ -366,3 +369,45 @@ int launch_copy(float* dst, const float* src, size_t n, hipStream_t s) {
 }
 
 }  // namespace snl
+
+// ---- greedy pick without device allocation ----
+//
+// The block partials of launch_pick live in this file-scope array instead of a buffer the caller
+// or the library allocates.  Each GPU holds its own copy until the process ends; host code reaches
+// it only through the address hipGetSymbolAddress returns on that device (the array's name is a
+// host-side stand-in, not a device address).  pick_partial_kernel writes every partial that
+// pick_final_kernel reads, so nothing needs clearing between calls.
+namespace snl {
+namespace {
+constexpr int kNoAllocPickBlocks = 4096;  // rows * ceil(V / 2048) at most: 48 KiB
+static __device__ __align__(256) float scratch[kNoAllocPickBlocks * 3];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device.
+int scratch_address(float** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SNL_EDEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SNL_EDEVICE;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return SNL_OK;
+}
+}  // namespace
+
+}  // namespace snl
+
+extern "C" int snl_pick_rows_noalloc(const float* logits, int V, int rows, snl_pick* picks_out, void* stream) {
+    using namespace snl;
+    if (!logits || !picks_out || V < 1 || rows < 1 || rows > 64) return SNL_EARG;
+    if ((size_t)rows * ((V + kPickChunk - 1) / kPickChunk) > (size_t)kNoAllocPickBlocks) return SNL_EARG;
+    float* sp = nullptr;
+    if (const int rc = scratch_address(&sp)) return rc;
+    return launch_pick(logits, V, rows, sp, reinterpret_cast<Pick*>(picks_out), (hipStream_t)stream) ? SNL_EDEVICE
+                                                                                                       : SNL_OK;
+}

@@ -165,6 +165,7 @@ def lib() -> ctypes.CDLL:
                                     ctypes.c_int, ctypes.c_float, ctypes.c_float, i32p, ctypes.c_int, ctypes.c_int,
                                     ctypes.c_int, u32p, vp]
         L.snl_pick_rows.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.snl_pick_rows_noalloc.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, vp]
         _LIB = L
     return _LIB
 
@@ -542,3 +543,10 @@ class kernels:
         rc = lib().snl_pick_rows(logits.data_ptr(), V, rows, picks.data_ptr(), kernels._stream())
         if rc != SNL_OK:
             raise SnlError(rc, "snl_pick_rows")
+
+    @staticmethod
+    def pick_rows_noalloc(logits, V: int, rows: int, picks):
+        """snl_pick_rows_noalloc: enqueued on torch's current stream, no device allocation."""
+        rc = lib().snl_pick_rows_noalloc(logits.data_ptr(), V, rows, picks.data_ptr(), kernels._stream())
+        if rc != SNL_OK:
+            raise SnlError(rc, "snl_pick_rows_noalloc")
