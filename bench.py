@@ -10,10 +10,14 @@ device synchronisations; value = tokens emitted in those K steps / their wall ti
 
 roofline: the dominant kernel is the verify pass's gate_up GEMV (Q8_0, M=2, N=24576, K=4096 with
 the fused mHC/RMSNorm prologue and SwiGLU epilogue, 43% of the pass's weight bytes).  After the
-timed region the engine launches only that op of a verify pass, `--roofline-reps` passes back to
-back (56 launches per pass, each layer's own 113 MB matrix, so nothing is served from the 256 MB
-Infinity Cache), between two HIP events on the engine's stream; achieved = algorithmic bytes per
-launch / mean time per launch.  A per-op table of an eagerly launched verify pass goes to stderr.
+timed region, `--profile-passes` verify passes are launched op by op with HIP events around each
+op on the engine's stream; achieved = algorithmic bytes per gate_up launch / its mean duration in
+those passes (each launch streams its own layer's 113 MB matrix).  The same op launched alone,
+back to back, is reported beside it (isolated_achieved).  A per-op table goes to stderr.
+
+config.gemv_microbench: the skinny GEMV alone, M in {1, 2} x K = 4096 x N in {4096, 12288,
+248320}, Q8_0 and Q4_0, weights rotated over >= 1 GB of distinct copies (GB/s and fraction of the
+8 TB/s HBM peak per shape).
 
 cpu_baseline: the CPU oracle (oracle/, a C restatement of the reference's kernels, OpenMP) running
 the same 9B model on the host cores for a bounded sample (a 2-token prompt, then a few
@@ -90,6 +94,183 @@ def measured_traffic():
     if rec.get("kernel_sources_sha256") != kernel_source_hash():
         return None
     return round(rec["traffic_bytes"])
+
+
+# kernels launched by each op of a verify pass, in launch order
+OP_KERNELS = {"attention": ["prep_kernel", "attend_kernel<2>", "combine_kernel"],
+              "pick": ["pick_partial_kernel", "pick_final_kernel"]}
+
+
+def pmc_decode(snl, np, ops_out: str, passes: int = 3) -> int:
+    """Counter workload: the bench's 9B Q8_0 engine and 1024-token prompt, 6 graph-launched MTP
+    steps, then `passes` verify passes launched op by op (rolled back).  The op sequence of those
+    passes goes to ops_out, so the per-dispatch counters and trace can be labelled by op."""
+    cfg = snl.nine_b_config()
+    eng = snl.Engine(cfg, seed=1, quant=0, ctx=PROMPT + 64)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, PROMPT).tolist()
+    dec = eng.decoder(prompt, spec=True)
+    for _ in range(6):
+        dec.step()
+    dec.close()
+    pos = eng.pos
+    ops = []
+    for p in range(passes):
+        recs = eng.forward_profiled([11 + p, 12 + p], [[pos] * 3, [pos + 1] * 3], logit_rows=2, ckpt=True)
+        eng.rollback()
+        ops = [(name, b) for name, b, _ in recs if name != "end"]
+    eng.close()
+    with open(ops_out, "w") as fh:
+        json.dump({"verify_ops": ops, "passes": passes, "pos": pos, "kv_dim": cfg.n_kv_heads * cfg.head_dim}, fh)
+    log(f"pmc decode workload: {len(ops)} ops per verify pass, {passes} eager passes at position {pos}")
+    return 0
+
+
+def pmc_attention(snl, np, pos0: int, calls: int = 8) -> int:
+    """Counter workload: decode attention alone for a 2-token verify at cache position pos0 (the 9B
+    head shape, 16 q / 4 kv heads x 256), `calls` kernel-level calls over a random f16 cache."""
+    import torch
+
+    ctx = pos0 + 64
+    n_heads, n_kv = 16, 4
+    stride = 2 * n_heads * 256 + 2 * n_kv * 256
+    r = np.random.default_rng(3)
+    kc = torch.from_numpy(r.standard_normal((ctx, n_kv * 256)).astype(np.float16).view(np.int16)).cuda()
+    vc = torch.from_numpy(r.standard_normal((ctx, n_kv * 256)).astype(np.float16).view(np.int16)).cuda()
+    proj = torch.from_numpy(r.standard_normal((2, stride)).astype(np.float32)).cuda()
+    norms = torch.zeros(512, dtype=torch.float32, device="cuda")
+    qbuf = torch.zeros((2, n_heads * 256), dtype=torch.float32, device="cuda")
+    out = torch.zeros_like(qbuf)
+    partial = torch.zeros(2 * n_heads * ((ctx + 63) // 64) * 258, dtype=torch.float32, device="cuda")
+    rpos = np.array([[pos0] * 3, [pos0 + 1] * 3], np.uint32)
+    for _ in range(calls):
+        snl.kernels.attention(proj, stride, qbuf, kc, vc, norms, out, partial, n_heads, n_kv, 64, 1e7, 1e-6,
+                              (11, 11, 10), ctx, 2, pos0, rpos)
+    torch.cuda.synchronize()
+    log(f"pmc attention workload: {calls} calls at position {pos0}")
+    return 0
+
+
+def _csv_rows(path: str):
+    import csv
+
+    rows = list(csv.DictReader(open(path)))
+    key = "Start_Timestamp" if rows and "Start_Timestamp" in rows[0] else "Dispatch_Id"
+    return sorted(rows, key=lambda r: int(r[key]))
+
+
+def _short(name: str) -> str:
+    import re
+
+    n = name.replace("snl::(anonymous namespace)::", "").replace("void ", "")
+    return re.sub(r"\(.*", "", n).strip()
+
+
+def summarize_decode_pmc(d: str) -> str:
+    """Per-op HBM traffic and in-pass durations of the verify pass, as a markdown table.
+
+    d holds: ops.json (pmc_decode), pf/pw (FETCH_SIZE / WRITE_SIZE of pmc_decode), kt (kernel trace
+    of pmc_decode), af/aw/at (the same for pmc_attention at 32K), cf/cw (the copy probe).  The last
+    passes x dispatches-per-pass counter rows are the op-by-op verify passes, labelled in launch
+    order; durations come from the graph-launched verify passes of the trace (same kernel order)."""
+    info = json.load(open(os.path.join(d, "ops.json")))
+    ops, passes, pos = info["verify_ops"], info["passes"], info["pos"]
+    labels = []  # (op, kernel, algorithmic bytes) per dispatch of one verify pass
+    for name, b in ops:
+        ks = OP_KERNELS.get(name)
+        if ks:
+            for k in ks:
+                ab = (pos + 2) * info["kv_dim"] * 2 * 2 if k.startswith("attend") else 0.0
+                labels.append((name, k, ab))
+        else:
+            labels.append((name, None, b))
+    per = len(labels)
+    true_kib = 256 * 1024.0
+    ff = true_kib / _pmc_mean(os.path.join(d, "cf_counter_collection.csv"), "copyBuffer")
+    wf = true_kib / _pmc_mean(os.path.join(d, "cw_counter_collection.csv"), "copyBuffer")
+
+    def counters(tag):
+        rows = _csv_rows(os.path.join(d, f"{tag}_counter_collection.csv"))
+        return rows
+
+    fr, wr = counters("pf"), counters("pw")
+    fr, wr = fr[-passes * per:], wr[-passes * per:]
+    # graph verify passes in the trace: segments whose kernel names follow the labelled sequence
+    kt = _csv_rows(os.path.join(d, "kt_kernel_trace.csv"))
+    names = [_short(r["Kernel_Name"]) for r in kt]
+    seq = [_short(fr[i]["Kernel_Name"]) for i in range(per)]
+    dur = [[] for _ in range(per)]
+    i = 0
+    while i + per <= len(kt) - passes * per:
+        if names[i:i + per] == seq:
+            for j in range(per):
+                dur[j].append((int(kt[i + j]["End_Timestamp"]) - int(kt[i + j]["Start_Timestamp"])) / 1e3)
+            i += per
+        else:
+            i += 1
+    agg = {}
+    order = []
+    for j, (op, k, ab) in enumerate(labels):
+        kname = seq[j]
+        key = (op, kname)
+        if key not in agg:
+            agg[key] = {"n": 0, "alg": 0.0, "fetch": 0.0, "write": 0.0, "us": []}
+            order.append(key)
+        a = agg[key]
+        a["n"] += 1
+        a["alg"] += ab
+        for p in range(passes):
+            a["fetch"] += float(fr[p * per + j]["Counter_Value"]) * ff * 1024.0 / passes
+            a["write"] += float(wr[p * per + j]["Counter_Value"]) * wf * 1024.0 / passes
+        a["us"] += dur[j]
+    n_graph = len(dur[0]) if dur else 0
+    out = [f"Verify pass at position {pos} (9B Q8_0, M = 2): {per} dispatches; counters averaged over "
+           f"{passes} op-by-op passes, durations over {n_graph} graph-launched passes of the same run.",
+           f"Calibration (256 MiB device copy): FETCH_SIZE x {ff:.4f}, WRITE_SIZE x {wf:.4f}.", "",
+           "| op | kernel | launches/pass | algorithmic MB/launch | counter MB/launch (fetch + write) | ratio "
+           "| us/launch in pass | GB/s (algorithmic) | fraction of 8 TB/s |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for key in order:
+        a = agg[key]
+        n = a["n"]
+        alg, cnt = a["alg"] / n, (a["fetch"] + a["write"]) / n
+        us = sum(a["us"]) / len(a["us"]) if a["us"] else float("nan")
+        gbs = alg / (us * 1e-6) / 1e9 if alg > 0 else 0.0
+        ratio = f"{cnt / alg:.3f}" if alg > 0 else "-"
+        out.append(f"| {key[0]} | `{key[1]}` | {n} | {alg / 1e6:.2f} | {cnt / 1e6:.2f} | {ratio} | {us:.2f} | "
+                   f"{gbs:.0f} | {gbs / HBM_PEAK_GBS:.3f} |")
+    # decode attention at 32K keys (kernel-level calls)
+    if os.path.exists(os.path.join(d, "af_counter_collection.csv")):
+        ainfo = json.load(open(os.path.join(d, "attn.json")))
+        p0 = ainfo["pos"]
+        fa = [r for r in counters("af") if "attend_kernel" in r["Kernel_Name"]]
+        wa = [r for r in counters("aw") if "attend_kernel" in r["Kernel_Name"]]
+        ta = [r for r in _csv_rows(os.path.join(d, "at_kernel_trace.csv")) if "attend_kernel" in r["Kernel_Name"]]
+        cnt = (sum(float(r["Counter_Value"]) for r in fa) / len(fa) * ff +
+               sum(float(r["Counter_Value"]) for r in wa) / len(wa) * wf) * 1024.0
+        us = sum((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in ta) / len(ta)
+        alg = (p0 + 2) * 1024 * 2 * 2
+        gbs = alg / (us * 1e-6) / 1e9
+        out.append(f"| attention at {p0} keys (kernel-level) | `attend_kernel<2>` | - | {alg / 1e6:.2f} | "
+                   f"{cnt / 1e6:.2f} | {cnt / alg:.3f} | {us:.2f} | {gbs:.0f} | {gbs / HBM_PEAK_GBS:.3f} |")
+    return "\n".join(out) + "\n"
+
+
+def gemv_microbench(snl, reps: int) -> list:
+    """The skinny GEMV alone at the shapes of the Q8 GEMV microbench: M in {1, 2} (decode, MTP
+    verify) x K = 4096 x N in {4096, 12288, 248320}, Q8_0 and Q4_0 with f32 block scales, each shape's
+    weights rotated over >= 1 GB of distinct copies; GB/s = algorithmic bytes / mean launch time."""
+    out = []
+    for quant in (0, 1):
+        for n in (4096, 12288, 248320):
+            for m in (1, 2):
+                ms, b, copies = snl.kernels.gemv_time(quant, n, 4096, m, reps)
+                gbs = b / (ms * 1e-3) / 1e9
+                out.append({"quant": "q8_0" if quant == 0 else "q4_0", "M": m, "N": n, "K": 4096,
+                            "us": round(ms * 1e3, 2), "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                            "copies": copies})
+                log(f"gemv {out[-1]['quant']} M={m} N={n:6d} K=4096: {ms * 1e3:8.2f} us  {gbs:7.1f} GB/s "
+                    f"({gbs / HBM_PEAK_GBS:.3f} of peak, {copies} copies)")
+    return out
 
 
 def cpu_baseline(steps: int) -> dict:
@@ -203,18 +384,26 @@ def main() -> int:
     ap.add_argument("--roofline-reps", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--gemv-reps", type=int, default=40,
+                    help="launches per shape of the skinny GEMV microbench (0: skip it)")
     ap.add_argument("--op-times", action="store_true",
                     help="also print each op of a verify pass timed in isolation (stderr)")
     ap.add_argument("--summarize-pmc", metavar="DIR",
                     help="write the roofline kernel's HBM traffic record from rocprofv3 --pmc CSVs in DIR and exit")
     ap.add_argument("--long-context", action="store_true",
                     help="run the Q4_0 32K two-turn prefix-cache workload instead and print its own line")
+    ap.add_argument("--pmc-decode", metavar="OPS_JSON",
+                    help="counter workload: a few decode steps and op-by-op verify passes; writes the op sequence")
+    ap.add_argument("--pmc-attention", nargs=2, metavar=("POS", "INFO_JSON"),
+                    help="counter workload: decode attention alone at cache position POS")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only copy a buffer of this many MiB 4 times on the GPU and exit: the known-size "
                          "kernel that HBM byte counters are calibrated against")
     args = ap.parse_args()
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(args.summarize_pmc, args.copy_probe_mb or 256), indent=1))
+        if os.path.exists(os.path.join(args.summarize_pmc, "ops.json")):
+            print(summarize_decode_pmc(args.summarize_pmc))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs on a single MI355X (multi-GPU sharding is a "
@@ -237,6 +426,12 @@ def main() -> int:
         return 0
     if args.long_context:
         return long_context(snl, np)
+    if args.pmc_decode:
+        return pmc_decode(snl, np, args.pmc_decode)
+    if args.pmc_attention:
+        with open(args.pmc_attention[1], "w") as fh:
+            json.dump({"pos": int(args.pmc_attention[0])}, fh)
+        return pmc_attention(snl, np, int(args.pmc_attention[0]))
     cfg = snl.nine_b_config()
     ctx = PROMPT + 2 * (args.warmup + args.steps) + args.profile_passes + 64
     t0 = time.perf_counter()
@@ -287,8 +482,14 @@ def main() -> int:
             ms, b, n = eng.time_op(name, args.roofline_reps)
             gbs = b / (ms * 1e-3) / 1e9 if b > 0 else 0.0
             log(f"  isolated {name:<16} {n:3d}/pass  {ms * 1e3:8.2f} us/launch  {b / 1e6:9.2f} MB  {gbs:8.1f} GB/s")
-    gu_ms, gu_bytes, gu_n = eng.time_op("gemv_gate_up", args.roofline_reps)
-    achieved = gu_bytes / (gu_ms * 1e-3) / 1e9
+    # the roofline kernel in the pass: gate_up launches of the eagerly launched verify passes, each
+    # between two HIP events on the engine stream (48 of a pass's 56 are the mHC variant)
+    gu_n_pass, gu_b, gu_t = per_op["gemv_gate_up"]
+    inpass_us = gu_t / gu_n_pass * 1e3
+    gu_bytes = gu_b / gu_n_pass
+    achieved = gu_bytes / (inpass_us * 1e-6) / 1e9
+    gu_ms, _, gu_n = eng.time_op("gemv_gate_up", args.roofline_reps)
+    isolated = gu_bytes / (gu_ms * 1e-3) / 1e9
     gemv_bytes = sum(v[1] for k, v in per_op.items() if k.startswith("gemv")) / args.profile_passes
     gemv_ms = sum(v[2] for k, v in per_op.items() if k.startswith("gemv")) / args.profile_passes
     pass_ms = sum(v[2] for v in per_op.values()) / args.profile_passes
@@ -296,8 +497,8 @@ def main() -> int:
         gbs = b / (ms * 1e-3) / 1e9 if ms > 0 and b > 0 else 0.0
         log(f"  {name:<16} calls {n / args.profile_passes:6.1f}/pass  {ms / args.profile_passes:8.3f} ms/pass"
             f"  {gbs:8.1f} GB/s")
-    log(f"gate_up GEMV alone ({gu_n} launches/pass x {args.roofline_reps}): {gu_bytes / 1e6:.2f} MB/launch, "
-        f"{gu_ms * 1e3:.2f} us -> {achieved:.0f} GB/s; all GEMVs "
+    log(f"gate_up GEMV in the pass: {inpass_us:.2f} us/launch -> {achieved:.0f} GB/s; alone ({gu_n} launches/pass x "
+        f"{args.roofline_reps}): {gu_bytes / 1e6:.2f} MB/launch, {gu_ms * 1e3:.2f} us -> {isolated:.0f} GB/s; all GEMVs "
         f"{gemv_bytes / 1e9:.3f} GB in {gemv_ms:.3f} ms/pass; eager pass {pass_ms:.3f} ms")
 
     weights_per_verify = 14765064192.0  # f32-scale layout, 56 layer visits + LM head
@@ -328,8 +529,13 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "mgemv_kernel<Q8_0, M=2, SwiGLU, mHC-RMSNorm prologue> (gate_up, N=24576, K=4096)",
+            "kernel": "gate_up GEMV, mgemv_kernel<0, 1, 3, 2, 4, 1> (mHC-RMSNorm prologue, 48 launches per "
+                      "verify pass) and <0, 1, 3, 1, 4, 1> (RMSNorm prologue, 8), Q8_0, M=2, N=24576, K=4096, "
+                      "SwiGLU epilogue",
             "achieved": round(achieved, 1),
+            "launch_us": round(inpass_us, 3),
+            "bytes_per_launch": round(gu_bytes),
+            "isolated_achieved": round(isolated, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -338,6 +544,8 @@ def main() -> int:
         "cpu_baseline": None,
     }
     eng.close()
+    if args.gemv_reps > 0:
+        result["config"]["gemv_microbench"] = gemv_microbench(snl, args.gemv_reps)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.cpu_steps)
     print(json.dumps(result), flush=True)

@@ -281,6 +281,14 @@ int snl_gemv(int quant, const void* wq, const float* ws, const float* x, float* 
 #define SNL_PREFILL_M 512
 int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* y, int M, int N, int K,
              int x_stride, int y_stride, void* stream);
+/* Times the decode GEMV alone (measurement; no reference counterpart, it serves the skinny GEMV
+ * microbench over src/shaders/matmul.wgsl:102-198): enough distinct seeded N x K matrices in tile
+ * order to span at least 1 GB (*copies_out, nullable), launched in turn `reps` times with M random
+ * token rows between two HIP events on a stream of its own.  *ms_per_launch receives the mean and
+ * *bytes_per_launch (nullable) the algorithmic bytes of one launch: quants, f32 block scales, the
+ * M input rows and the M output rows. */
+int snl_gemv_time(int quant, int N, int K, int M, int reps, double* ms_per_launch, double* bytes_per_launch,
+                  int* copies_out);
 /* Times the prefill GEMM alone (measurement): seeded N x K weights in panel order and M random
  * token rows, `reps` launches back to back between two HIP events on a stream of its own;
  * *ms_per_launch receives the mean. */

@@ -189,16 +189,16 @@ __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
 // mHC router dots of one token -> [pre0, pre1, post0, post1, mix00, mix01, mix10, mix11]
 // (layers.wgsl:94-126): raw = 8 router-row dots and the sum of squares of the 2-stream row of
-// length d; mhc_w = router [8][d] then bias[8].  The 2x2 mix is `iterations` Sinkhorn steps (rows,
+// length d; bias = the router's 8 biases.  The 2x2 mix is `iterations` Sinkhorn steps (rows,
 // then columns).  The reference runs them in log space, p -= log(exp(p) + exp(q)); here they run
 // on the exponentiated matrix, a /= a + b, which is the same iteration in exact arithmetic at a
 // reciprocal per row instead of an exp and a log, on one thread's critical path.  Exponents are
 // taken relative to the largest logit and floored at -80, so no entry underflows.
-__device__ inline void mhc_coefficients(const float* raw, const float* mhc_w, int d, int iterations, float* cf) {
+__device__ inline void mhc_coefficients_b(const float* raw, const float (&bias)[8], int d, int iterations, float* cf) {
     const float rinv = 1.0f / sqrtf(raw[8] / (float)d + 1e-6f);
     float lg[8];
 #pragma unroll
-    for (int o = 0; o < 8; ++o) lg[o] = raw[o] * rinv + mhc_w[(size_t)8 * d + o];
+    for (int o = 0; o < 8; ++o) lg[o] = raw[o] * rinv + bias[o];
     const float mx = fmaxf(fmaxf(lg[4], lg[5]), fmaxf(lg[6], lg[7]));
     float a = __expf(fmaxf(lg[4] - mx, -80.0f)), b = __expf(fmaxf(lg[5] - mx, -80.0f));
     float c = __expf(fmaxf(lg[6] - mx, -80.0f)), e = __expf(fmaxf(lg[7] - mx, -80.0f));
@@ -222,6 +222,13 @@ __device__ inline void mhc_coefficients(const float* raw, const float* mhc_w, in
     cf[5] = b;
     cf[6] = c;
     cf[7] = e;
+}
+// the same with the biases read from the router (mhc_w = router [8][d] then bias[8])
+__device__ inline void mhc_coefficients(const float* raw, const float* mhc_w, int d, int iterations, float* cf) {
+    float bias[8];
+#pragma unroll
+    for (int o = 0; o < 8; ++o) bias[o] = mhc_w[(size_t)8 * d + o];
+    mhc_coefficients_b(raw, bias, d, iterations, cf);
 }
 __device__ __forceinline__ float sigmoidf_(float v) { return 1.0f / (1.0f + expf(-v)); }
 

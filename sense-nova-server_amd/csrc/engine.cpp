@@ -1748,6 +1748,79 @@ int snl_gemm(int quant, const void* wq, const float* ws, const float* x, float* 
     return SNL_OK;
 }
 
+// The decode GEMV alone (measurement): `copies` distinct N x K matrices in tile order, together at
+// least 1 GB so that the 256 MB Infinity Cache cannot serve a repeat, launched in turn `reps`
+// times between two HIP events on a stream of its own.
+int snl_gemv_time(int quant, int N, int K, int M, int reps, double* ms_per_launch, double* bytes_per_launch,
+                  int* copies_out) {
+    if ((quant != 0 && quant != 1) || K % 128 || M < 1 || M > SNL_MAX_M || N < 16 || reps < 1 || !ms_per_launch)
+        return SNL_EARG;
+    static const int init_rc = gemv_init();
+    if (init_rc) return SNL_EDEVICE;
+    PackGeom pg;
+    if (!pack_geom(quant, N, K, 0, &pg) || !mgemv_fits(M, K)) return SNL_EARG;
+    const size_t mat = pg.q_bytes + pg.s_floats * 4;
+    const int copies = (int)std::max<size_t>(2, ((size_t)1 << 30) / mat + 1);
+    hipStream_t st = nullptr;
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess) return SNL_EDEVICE;
+    const size_t n = (size_t)N * K;
+    uint8_t *q = nullptr, *pq = nullptr;
+    float *s = nullptr, *ps = nullptr, *x = nullptr, *y = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = SNL_OK;
+    if (hipMalloc((void**)&q, quant == 0 ? n : n / 2) != hipSuccess || hipMalloc((void**)&s, n / 32 * 4) != hipSuccess ||
+        hipMalloc((void**)&pq, pg.q_bytes * copies) != hipSuccess ||
+        hipMalloc((void**)&ps, pg.s_floats * 4 * copies) != hipSuccess ||
+        hipMalloc((void**)&x, (size_t)M * K * 4) != hipSuccess || hipMalloc((void**)&y, (size_t)M * N * 4) != hipSuccess ||
+        hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        rc = SNL_ENOMEM;
+    } else {
+        if (launch_gen_matrix(0x5EEDull, N, K, 0.02f, quant, q, s, st) ||
+            launch_gen_vector(0x5EEEull, (int64_t)M * K, 0, 1.0f, 0, 0, x, st))
+            rc = SNL_EDEVICE;
+        for (int c = 0; !rc && c < copies; ++c)
+            if (launch_pack_matrix(pg, q, s, pq + pg.q_bytes * c, ps + pg.s_floats * c, st)) rc = SNL_EDEVICE;
+        GemvArgs g{};
+        g.packed = 1;
+        g.x = x;
+        g.x_stride = K;
+        g.y = y;
+        g.y_stride = N;
+        g.N = N;
+        g.K = K;
+        g.epi = GEMV_STORE;
+        auto launch = [&](int i) {
+            const int c = i % copies;
+            g.wq = pq + pg.q_bytes * c;
+            g.ws = ps + pg.s_floats * c;
+            return launch_gemv(g, quant, M, st);
+        };
+        for (int i = 0; !rc && i < copies; ++i)  // warm-up: every copy once
+            if (launch(i)) rc = SNL_EDEVICE;
+        float ms = 0.0f;
+        if (!rc && hipEventRecord(e0, st) != hipSuccess) rc = SNL_EDEVICE;
+        for (int i = 0; !rc && i < reps; ++i)
+            if (launch(i)) rc = SNL_EDEVICE;
+        if (!rc && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                    hipEventElapsedTime(&ms, e0, e1) != hipSuccess))
+            rc = SNL_EDEVICE;
+        if (!rc) {
+            *ms_per_launch = (double)ms / reps;
+            // algorithmic bytes: quants + f32 block scales + the M input rows + the M output rows
+            if (bytes_per_launch)
+                *bytes_per_launch = (double)n * (quant == 0 ? 1.0 : 0.5) + (double)(n / 32) * 4 + (double)M * K * 4 +
+                                    (double)M * N * 4;
+            if (copies_out) *copies_out = copies;
+        }
+    }
+    (void)hipStreamSynchronize(st);
+    for (void* p : {(void*)q, (void*)s, (void*)pq, (void*)ps, (void*)x, (void*)y}) (void)hipFree(p);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamDestroy(st);
+    return rc;
+}
+
 int snl_gemm_time(int quant, int N, int K, int M, int reps, double* ms_per_launch) {
     if ((quant != 0 && quant != 1) || K % 128 || K > 16384 || M < 1 || M > SNL_PREFILL_M || N < 1 || reps < 1 ||
         !ms_per_launch)

@@ -140,8 +140,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                                                                int nss_w, int tiles, int il) {
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
-    __shared__ float wred_s[kMaxWaves][2 * P][2];
-    __shared__ float tok_s[2 * P][2];  // per token: input factor, output factor
+    __shared__ float wst_s[kMaxWaves][2 * P][5];  // per-wave token statistics (sums, then maxima)
+    __shared__ __align__(16) float tok_s[2 * P][4];  // per token: input factor, output factor, pre0, pre1
     __shared__ float raw_s[2 * P][9];  // mHC site sums (NORM_MHC)
     __shared__ float cf_s[2 * P][8];   // mHC token coefficients (MHC epilogue)
     __shared__ float pr_s[kMaxWaves * 16 / 32][2 * P][9];  // next-site router sums per 32-row group
@@ -233,6 +233,15 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         sw0 = a.site_w[(size_t)16 * K];
         sw1 = a.site_w[(size_t)16 * K + 1];
     }
+    // the site's 8 router biases for block 0, which forms the token coefficients
+    float bias8[8];
+#pragma unroll
+    for (int o = 0; o < 8; ++o) bias8[o] = 0.0f;
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        if (blockIdx.x == 0 && tid < M)
+#pragma unroll
+            for (int o = 0; o < 8; ++o) bias8[o] = a.site_w[(size_t)16 * K + o];
+    }
     // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
     // of squares.
     float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
@@ -308,13 +317,95 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const bool early = il == 0 && (wave & 1) != 0;
     if (early) issue(w1, s1, 1);
 
-    float pre0[2 * P], pre1[2 * P];
+    // ---- prologue, part 2: per-token statistics of the branch input, one block barrier ----
+    // NORM: the sum of squares and the largest |x (1 + w)|.  NORM_MHC: the input is the pre-mix
+    // v = pre0 x0 + pre1 x1 with pre from this site's router sums, which arrive with the rows; so the
+    // waves gather sum x0^2, sum x0 x1, sum x1^2 and the largest |x0 (1 + w)|, |x1 (1 + w)| before
+    // pre is known, and the router sums and these statistics cross the block in the same barrier:
+    // sum v^2 = pre0^2 sum x0^2 + 2 pre0 pre1 sum x0 x1 + pre1^2 sum x1^2, and the f16 range check
+    // takes pre0 max|x0 (1 + w)| + pre1 max|x1 (1 + w)| (pre >= 0) as the bound of max|v (1 + w)|.
+    // GNORM applies the DeltaNet head factors now; PLAIN only needs the largest |x|.
+    constexpr int NS = PRO == GEMV_NORM_MHC ? 5 : 2;  // statistics per token
+    float stat[2 * P][NS];
 #pragma unroll
-    for (int m = 0; m < 2 * P; ++m) {
-        pre0[m] = 1.0f;
-        pre1[m] = 0.0f;
+    for (int m = 0; m < 2 * P; ++m)
+#pragma unroll
+        for (int k = 0; k < NS; ++k) stat[m][k] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+        if (tid + u * nthr >= K8) continue;
+#pragma unroll
+        for (int m = 0; m < 2 * P; ++m) {
+            if (m >= M) continue;
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float4 t = xa[m][u][hh];
+                if constexpr (PRO == GEMV_GNORM) {  // the head factor of linear.wgsl:131-133
+                    const float4 pp = gp[m][u];
+                    const float var_o = (((pp.x + pp.y) + pp.z) + pp.w) / 128.0f;
+                    const float rr = 1.0f / sqrtf(var_o + a.eps);
+                    t.x = t.x * rr;
+                    t.y = t.y * rr;
+                    t.z = t.z * rr;
+                    t.w = t.w * rr;
+                    xa[m][u][hh] = t;
+                }
+                if constexpr (PRO == GEMV_NORM_MHC) {
+                    const float4 b = xb[m][u][hh], w = nw[u][hh];
+                    const float av[4] = {t.x, t.y, t.z, t.w}, bv[4] = {b.x, b.y, b.z, b.w};
+                    const float wv[4] = {1.0f + w.x, 1.0f + w.y, 1.0f + w.z, 1.0f + w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        stat[m][0] = fmaf(av[e], av[e], stat[m][0]);
+                        stat[m][1] = fmaf(av[e], bv[e], stat[m][1]);
+                        stat[m][2] = fmaf(bv[e], bv[e], stat[m][2]);
+                        stat[m][3] = fmaxf(stat[m][3], fabsf(av[e] * wv[e]));
+                        stat[m][4] = fmaxf(stat[m][4], fabsf(bv[e] * wv[e]));
+                    }
+                } else {
+                    if constexpr (PRO == GEMV_NORM) {
+                        stat[m][0] = fmaf(t.x, t.x, stat[m][0]);
+                        stat[m][0] = fmaf(t.y, t.y, stat[m][0]);
+                        stat[m][0] = fmaf(t.z, t.z, stat[m][0]);
+                        stat[m][0] = fmaf(t.w, t.w, stat[m][0]);
+                        const float4 w = nw[u][hh];
+                        t.x = t.x * (1.0f + w.x);
+                        t.y = t.y * (1.0f + w.y);
+                        t.z = t.z * (1.0f + w.z);
+                        t.w = t.w * (1.0f + w.w);
+                        xa[m][u][hh] = t;
+                    }
+                    stat[m][1] = fmaxf(stat[m][1],
+                                       fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
+                }
+            }
+        }
+    }
+    {
+        float sums[2 * P][NS == 5 ? 3 : 1], maxs[2 * P][2];
+#pragma unroll
+        for (int m = 0; m < 2 * P; ++m) {
+            if constexpr (NS == 5) {
+                sums[m][0] = stat[m][0], sums[m][1] = stat[m][1], sums[m][2] = stat[m][2];
+                maxs[m][0] = stat[m][3], maxs[m][1] = stat[m][4];
+            } else {
+                sums[m][0] = stat[m][0];
+                maxs[m][0] = stat[m][1], maxs[m][1] = 0.0f;
+            }
+        }
+        wave_sum_n(*reinterpret_cast<float(*)[2 * P * (NS == 5 ? 3 : 1)]>(&sums[0][0]));
+        wave_max_n(*reinterpret_cast<float(*)[2 * P * 2]>(&maxs[0][0]));
+        if (lane == 0)
+#pragma unroll
+            for (int m = 0; m < 2 * P; ++m) {
+#pragma unroll
+                for (int k = 0; k < (NS == 5 ? 3 : 1); ++k) wst_s[wave][m][k] = sums[m][k];
+                wst_s[wave][m][3] = maxs[m][0];
+                wst_s[wave][m][4] = maxs[m][1];
+            }
     }
     if constexpr (PRO == GEMV_NORM_MHC) {
+        // this site's router sums (layers.wgsl:94-102) from the producer's block partials
         float rsum[3];
 #pragma unroll
         for (int pi = 0; pi < 3; ++pi) {
@@ -334,92 +425,81 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             const int n = wave + nwv * pi;
             if (lane == 0 && n < 9 * M) raw_s[n / 9][n - 9 * (n / 9)] = rsum[pi];
         }
-        lds_barrier();
-        const int d = 2 * K;
-#pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            if (m >= M) continue;
-            const float rinv = 1.0f / sqrtf(raw_s[m][8] / (float)d + 1e-6f);
-            pre0[m] = 1.0f / (1.0f + __expf(-(raw_s[m][0] * rinv + sw0)));
-            pre1[m] = 1.0f / (1.0f + __expf(-(raw_s[m][1] * rinv + sw1)));
-        }
-        if (blockIdx.x == 0 && tid < 9 * M) a.raw[tid] = raw_s[tid / 9][tid - 9 * (tid / 9)];
     }
-
-    // ---- prologue, part 2: branch input, per-token sums, f16 hi/lo in MFMA fragment order ----
-    float ssq[2 * P], amax[2 * P];
-#pragma unroll
-    for (int m = 0; m < 2 * P; ++m) {
-        ssq[m] = 0.0f;
-        amax[m] = 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-        if (tid + u * nthr >= K8) continue;
-#pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            if (m >= M) continue;
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                float4 t = xa[m][u][hh];
-                if constexpr (PRO == GEMV_NORM_MHC) {
-                    const float4 v1 = xb[m][u][hh];
-                    t.x = pre0[m] * t.x + pre1[m] * v1.x;
-                    t.y = pre0[m] * t.y + pre1[m] * v1.y;
-                    t.z = pre0[m] * t.z + pre1[m] * v1.z;
-                    t.w = pre0[m] * t.w + pre1[m] * v1.w;
-                }
-                if constexpr (PRO == GEMV_GNORM) {  // the head factor of linear.wgsl:131-133
-                    const float4 pp = gp[m][u];
-                    const float var_o = (((pp.x + pp.y) + pp.z) + pp.w) / 128.0f;
-                    const float rr = 1.0f / sqrtf(var_o + a.eps);
-                    t.x = t.x * rr;
-                    t.y = t.y * rr;
-                    t.z = t.z * rr;
-                    t.w = t.w * rr;
-                }
-                if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
-                    ssq[m] = fmaf(t.x, t.x, ssq[m]);
-                    ssq[m] = fmaf(t.y, t.y, ssq[m]);
-                    ssq[m] = fmaf(t.z, t.z, ssq[m]);
-                    ssq[m] = fmaf(t.w, t.w, ssq[m]);
-                    const float4 w = nw[u][hh];
-                    t.x = t.x * (1.0f + w.x);
-                    t.y = t.y * (1.0f + w.y);
-                    t.z = t.z * (1.0f + w.z);
-                    t.w = t.w * (1.0f + w.w);
-                }
-                amax[m] = fmaxf(amax[m], fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
-                xa[m][u][hh] = t;
-            }
-        }
-    }
-    wave_sum_n(ssq);
-    wave_max_n(amax);
-    if (lane == 0)
-#pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            wred_s[wave][m][0] = ssq[m];
-            wred_s[wave][m][1] = amax[m];
-        }
     if (tid < kZeroBytes / 16)
         reinterpret_cast<float4*>(lds + (size_t)P * nb * 256)[tid] = make_float4(0, 0, 0, 0);
     lds_barrier();
+    // thread m < 2P forms token m's factors from the waves' statistics (added in wave order): the
+    // input factor scales the row before the f16 split, the output factor the dot products after
     if (tid < 2 * P) {
         const int m = tid;
-        float ss = 0.0f, mx = 0.0f;
+        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, m0 = 0.0f, m1 = 0.0f;
         for (int w = 0; w < nwv; ++w) {
-            ss = ss + wred_s[w][m][0];
-            mx = fmaxf(mx, wred_s[w][m][1]);
+            s0 = s0 + wst_s[w][m][0];
+            if constexpr (NS == 5) {
+                s1 = s1 + wst_s[w][m][1];
+                s2 = s2 + wst_s[w][m][2];
+            }
+            m0 = fmaxf(m0, wst_s[w][m][3]);
+            m1 = fmaxf(m1, wst_s[w][m][4]);
         }
-        const float rinv = PRO == GEMV_NORM || PRO == GEMV_NORM_MHC ? 1.0f / sqrtf(ss / (float)K + a.eps) : 1.0f;
-        const float top = mx * rinv;
+        float rinv = 1.0f, top = m0, p0 = 1.0f, p1 = 0.0f;
+        if constexpr (PRO == GEMV_NORM_MHC) {
+            if (m < M) {
+                const float rr = 1.0f / sqrtf(raw_s[m][8] / (float)(2 * K) + 1e-6f);
+                p0 = 1.0f / (1.0f + __expf(-(raw_s[m][0] * rr + sw0)));
+                p1 = 1.0f / (1.0f + __expf(-(raw_s[m][1] * rr + sw1)));
+            }
+            const float ss = (p0 * p0 * s0 + 2.0f * p0 * p1 * s1) + p1 * p1 * s2;
+            rinv = 1.0f / sqrtf(ss / (float)K + a.eps);
+            top = (p0 * m0 + p1 * m1) * rinv;
+        } else if constexpr (PRO == GEMV_NORM) {
+            rinv = 1.0f / sqrtf(s0 / (float)K + a.eps);
+            top = m0 * rinv;
+        }
         // keep |x| * factor below 2^14 so the f16 high part cannot overflow
         const int e = top >= 16384.0f ? ilogbf(top) - 13 : 0;
         tok_s[m][0] = m < M ? ldexpf(rinv, -e) : 0.0f;
         tok_s[m][1] = ldexpf(1.0f, e);
+        tok_s[m][2] = p0;
+        tok_s[m][3] = p1;
     }
     lds_barrier();
+    float tokf[2 * P], toko[2 * P], pre0[2 * P], pre1[2 * P];
+#pragma unroll
+    for (int m = 0; m < 2 * P; ++m) {
+        const float4 t = *reinterpret_cast<const float4*>(tok_s[m]);
+        tokf[m] = t.x;
+        toko[m] = t.y;
+        pre0[m] = t.z;
+        pre1[m] = t.w;
+    }
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        if (blockIdx.x == 0 && tid < 9 * M) a.raw[tid] = raw_s[tid / 9][tid - 9 * (tid / 9)];
+        // the pre-mix and the norm weight of the branch input (layers.wgsl:57-73)
+#pragma unroll
+        for (int u = 0; u < UPT; ++u) {
+            if (tid + u * nthr >= K8) continue;
+#pragma unroll
+            for (int m = 0; m < 2 * P; ++m) {
+                if (m >= M) continue;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float4 t = xa[m][u][hh];
+                    const float4 v1 = xb[m][u][hh], w = nw[u][hh];
+                    t.x = pre0[m] * t.x + pre1[m] * v1.x;
+                    t.y = pre0[m] * t.y + pre1[m] * v1.y;
+                    t.z = pre0[m] * t.z + pre1[m] * v1.z;
+                    t.w = pre0[m] * t.w + pre1[m] * v1.w;
+                    t.x = t.x * (1.0f + w.x);
+                    t.y = t.y * (1.0f + w.y);
+                    t.z = t.z * (1.0f + w.z);
+                    t.w = t.w * (1.0f + w.w);
+                    xa[m][u][hh] = t;
+                }
+            }
+        }
+    }
     // unit k8 of token m -> 8 hi then 8 lo f16 in fragment order inside region (pair, block, token)
 #pragma unroll
     for (int u = 0; u < UPT; ++u) {
@@ -427,7 +507,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         if (k8 >= K8) continue;
 #pragma unroll
         for (int m = 0; m < 2 * P; ++m) {
-            const float f = tok_s[m][0];
+            const float f = tokf[m];
             const float v[8] = {xa[m][u][0].x, xa[m][u][0].y, xa[m][u][0].z, xa[m][u][0].w,
                                 xa[m][u][1].x, xa[m][u][1].y, xa[m][u][1].z, xa[m][u][1].w};
             half8_t hi, lo;
@@ -459,6 +539,17 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     if (!early) issue(w1, s1, 1);
     issue(w2, s2, 2);
     lds_barrier();
+    if constexpr (PRO == GEMV_NORM_MHC) {
+        // block 0 turns the site sums into the token coefficients (2x2 Sinkhorn) for the MHC epilogue
+        // of the same site, a later launch; done here, while its weight ring is in flight, so it does
+        // not lengthen the launch's tail
+        if (blockIdx.x == 0 && tid < M) {
+            float cf[8];
+            mhc_coefficients_b(raw_s[tid], bias8, 2 * K, a.iterations, cf);
+#pragma unroll
+            for (int o = 0; o < 8; ++o) a.coef[tid * 8 + o] = cf[o];
+        }
+    }
     if constexpr (EPI == GEMV_MHC) {
         if (tid < 8 * M) cf_s[tid >> 3][tid & 7] = cfv;
     }
@@ -543,12 +634,16 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         const int t2 = e_r >> 4;
         float v = 0.0f;
         for (int k = 0; k < KS; ++k) v = v + red_s[((t2 * KS + k) * 16 + e_j) * 2 * P + e_m];
-        v = v * tok_s[e_m][1];
+        float of = toko[0];
+#pragma unroll
+        for (int m = 1; m < 2 * P; ++m)
+            if (e_m == m) of = toko[m];
+        v = v * of;
         float* y = a.y + (size_t)e_m * a.y_stride;
         if constexpr (EPI == GEMV_SWIGLU) {
             float u = 0.0f;
             for (int k = 0; k < KS; ++k) u = u + red_s[((t2 * KS + k) * 16 + e_j + 8) * 2 * P + e_m];
-            u = u * tok_s[e_m][1];
+            u = u * of;
             y[e_T * 8 + e_j] = v / (1.0f + expf(-v)) * u;
         } else if constexpr (EPI == GEMV_STORE) {
             y[a.n_off + e_row] = v;
@@ -586,30 +681,32 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                 for (int o = 0; o < 8; ++o) c[o] = 0.0f;
             }
             c[8] = x0n * x0n + x1n * x1n;
-            for (int off = M; off < 32 * M; off <<= 1)
+            // butterflies over the 32 rows of a token (lanes M apart), through DPP and permlane swaps
+            if (M == 2) {
 #pragma unroll
-                for (int o = 0; o < 9; ++o) c[o] = c[o] + __shfl_xor(c[o], off, 64);
-            if (((tid / M) & 31) == 0 && tid < cnt * 16 * M)
+                for (int o = 0; o < 9; ++o) c[o] = xor_sum<32>(xor_sum<16>(xor_sum<8>(xor_sum<4>(xor_sum<2>(c[o])))));
+            } else {
 #pragma unroll
-                for (int o = 0; o < 9; ++o) pr_s[(tid / M) >> 5][tid % M][o] = c[o];
-            __syncthreads();
-            if (tid < 9 * M) {
-                const int m = tid / 9, o = tid - 9 * (tid / 9);
-                const int groups = (cnt * 16 + 31) / 32;
-                float t = 0.0f;
-                for (int gi = 0; gi < groups; ++gi) t = t + pr_s[gi][m][o];
-                a.rpart[(size_t)(m * 9 + o) * gridDim.x + blockIdx.x] = t;
+                for (int o = 0; o < 9; ++o) c[o] = xor_sum<16>(xor_sum<8>(xor_sum<4>(xor_sum<2>(xor_sum<1>(c[o])))));
             }
-        }
-    }
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        // block 0 turns the site sums into the token coefficients (2x2 Sinkhorn) for the MHC
-        // epilogue of the same site, after its own work
-        if (blockIdx.x == 0 && tid < M) {
-            float cf[8];
-            mhc_coefficients(raw_s[tid], a.site_w, 2 * K, a.iterations, cf);
+            const int groups = (cnt * 16 + 31) / 32;
+            if (groups == 1) {
+                // every output of the block sits in wave 0: lane m holds token m's sums
+                if (tid < M)
 #pragma unroll
-            for (int o = 0; o < 8; ++o) a.coef[tid * 8 + o] = cf[o];
+                    for (int o = 0; o < 9; ++o) a.rpart[(size_t)(tid * 9 + o) * gridDim.x + blockIdx.x] = 0.0f + c[o];
+            } else {
+                if (((tid / M) & 31) == 0 && tid < cnt * 16 * M)
+#pragma unroll
+                    for (int o = 0; o < 9; ++o) pr_s[(tid / M) >> 5][tid % M][o] = c[o];
+                __syncthreads();
+                if (tid < 9 * M) {
+                    const int m = tid / 9, o = tid - 9 * (tid / 9);
+                    float t = 0.0f;
+                    for (int gi = 0; gi < groups; ++gi) t = t + pr_s[gi][m][o];
+                    a.rpart[(size_t)(m * 9 + o) * gridDim.x + blockIdx.x] = t;
+                }
+            }
         }
     }
 }

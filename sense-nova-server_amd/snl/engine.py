@@ -159,6 +159,7 @@ def lib() -> ctypes.CDLL:
         L.snl_gemv.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
         L.snl_gemm.argtypes = [ctypes.c_int, vp, vp, vp, vp] + [ctypes.c_int] * 5 + [vp]
         L.snl_gemm_time.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_double)]
+        L.snl_gemv_time.argtypes = [ctypes.c_int] * 5 + [ctypes.POINTER(ctypes.c_double)] * 2 + [i32p]
         L.snl_deltanet.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                    ctypes.c_float] + [ctypes.c_int] * 5 + [vp]
         L.snl_attention.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int,
@@ -508,6 +509,18 @@ class kernels:
                             y_stride, kernels._stream())
         if rc != SNL_OK:
             raise SnlError(rc, "snl_gemm")
+
+    @staticmethod
+    def gemv_time(quant: int, N: int, K: int, M: int, reps: int = 40):
+        """(ms per launch, algorithmic bytes per launch, distinct weight copies) of the decode GEMV
+        alone, weights rotated over at least 1 GB."""
+        ms = ctypes.c_double()
+        b = ctypes.c_double()
+        c = ctypes.c_int32()
+        rc = lib().snl_gemv_time(quant, N, K, M, reps, ctypes.byref(ms), ctypes.byref(b), ctypes.byref(c))
+        if rc != SNL_OK:
+            raise SnlError(rc, "snl_gemv_time")
+        return ms.value, b.value, c.value
 
     @staticmethod
     def gemm_time(quant: int, N: int, K: int, M: int, reps: int = 20) -> float:
