@@ -97,7 +97,7 @@ def measured_traffic():
 
 
 # kernels launched by each op of a verify pass, in launch order
-OP_KERNELS = {"attention": ["prep_kernel", "attend_kernel<2>", "combine_kernel"],
+OP_KERNELS = {"attention": ["attend_kernel<2>", "combine_kernel"],
               "pick": ["pick_partial_kernel", "pick_final_kernel"]}
 
 

@@ -22,54 +22,6 @@ namespace {
 
 constexpr int HD = 256, G = 4, kPart = 64;
 
-// attention.wgsl:59-127: block (slot, token); slots [0, nh) queries, then keys, then values.
-__global__ __launch_bounds__(256) void prep_kernel(AttnArgs a) {
-    __shared__ float sh[HD];
-    __shared__ float red[4];
-    const int slot = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
-    const StepDev* st = a.step;
-    const int pos = st->pos0 + m;
-    const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
-    const float* row = a.proj + (size_t)m * a.proj_stride;
-    if (slot >= a.n_heads + a.n_kv) {
-        const int kh = slot - a.n_heads - a.n_kv;
-        const float v = row[2 * q_dim + kv_dim + kh * HD + d];
-        a.vcache[(size_t)pos * kv_dim + kh * HD + d] = __half_as_ushort(__float2half_rn(v));
-        return;
-    }
-    const bool is_q = slot < a.n_heads;
-    float v = is_q ? row[slot * 2 * HD + d] : row[2 * q_dim + (slot - a.n_heads) * HD + d];
-    // the norm weight and the rotary position go out with the row: a global load placed after a
-    // barrier waits for it, and each such wait is one more memory round trip
-    const float nw = a.norms[(is_q ? 0 : HD) + d];
-    const int half = a.rot_dim / 2;
-    uint32_t rot_pos = 0;
-    if (d < a.rot_dim) {
-        const int fi = d % half;
-        const uint32_t* rp = st->rpos[m];
-        rot_pos = rp[0];
-        if (fi % 3 == 1 && (uint32_t)fi < (a.mrope >> 16)) rot_pos = rp[1];
-        else if (fi % 3 == 2 && (uint32_t)fi < (a.mrope & 0xFFFFu)) rot_pos = rp[2];
-    }
-    const float total = block_sum<256>(v * v, red);
-    v = (v * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nw);
-    sh[d] = v;
-    __syncthreads();
-    if (d < a.rot_dim) {
-        const int fi = d % half;
-        const float inv_freq = powf(a.rope_theta, -(float)(2 * fi) / (float)a.rot_dim);
-        const float ang = (float)rot_pos * inv_freq;
-        const float cs = cosf(ang), sn = sinf(ang);
-        v = d < half ? sh[d] * cs - sh[d + half] * sn : sh[d] * cs + sh[d - half] * sn;
-    }
-    if (is_q) {
-        a.qbuf[(size_t)m * q_dim + slot * HD + d] = v;
-    } else {
-        const int kh = slot - a.n_heads;
-        a.kcache[(size_t)pos * kv_dim + kh * HD + d] = __half_as_ushort(__float2half_rn(v));
-    }
-}
-
 __device__ __forceinline__ float h2f(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -110,9 +62,17 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     constexpr int NC = G * M;
     static_assert(NC == 4 || NC == 8, "M = 1 or 2");
     constexpr int VROW = HD + 16;  // V tile row in halfs (544 bytes: a transposed read's 4 rows on distinct banks)
+    constexpr int NS = G * M + M;  // sums of squares: the group's queries (head, token), the new keys
     __shared__ __align__(16) _Float16 vt[kPart * VROW];
     __shared__ __align__(16) float sc[16][kPart];  // by MFMA column
     __shared__ float smax[16], ssum[16];
+    __shared__ float red[4][NS];
+    __shared__ __align__(16) _Float16 knew[M][HD], vnew[M][HD];  // this part's new keys (normed, rotated) and values
+    // before the value tile is written, its space holds the queries and new keys: normed, then rotated
+    float* const qs = reinterpret_cast<float*>(vt);  // [G * M][HD]
+    float* const qr = qs + G * M * HD;               // [G * M][HD]
+    float* const ks = qr + G * M * HD;               // [M][HD]
+    static_assert((2 * G * M + M) * HD * 4 <= kPart * VROW * 2, "prep staging fits the value tile");
     const int kh = blockIdx.x, p = blockIdx.y;
     const StepDev* st = a.step;
     const int pos0 = st->pos0;
@@ -128,8 +88,12 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     for (int m = 0; m < M; ++m)
         if ((n >> 2) == ((pos0 + m) & 1)) cm = m;
     const int chh = n & 3;  // its head in the group
+    bool mine[M];           // token m's own key and value fall in this part
+#pragma unroll
+    for (int m = 0; m < M; ++m) mine[m] = pos0 + m >= kstart && pos0 + m < kstart + kPart;
 
-    // ---- loads: the part's values (for the LDS tile), this wave's keys, the queries ----
+    // ---- loads: the part's values (for the LDS tile), this wave's keys (both straight from the
+    // cache, which the rows of this call's positions patch below), then this call's rows ----
     const unsigned row_bytes = (unsigned)kv_dim * 2;
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.kcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.vcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
@@ -141,13 +105,92 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
         kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
+    // attention.wgsl:59-127 for the group's 4 query heads and this part's new key / value rows:
+    // thread d holds dim d of each row
+    const int d = tid;
+    float qv0[G][M], kv0[M], vv0[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float* row = a.proj + (size_t)m * a.proj_stride;
+#pragma unroll
+        for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
+        kv0[m] = mine[m] ? row[2 * q_dim + kh * HD + d] : 0.0f;
+        vv0[m] = mine[m] ? row[2 * q_dim + kv_dim + kh * HD + d] : 0.0f;
+    }
+    const float nq = a.norms[d], nk = a.norms[HD + d];
+    // the rotary cos / sin of this dim's frequency for each token, formed on the host
+    const int half = a.rot_dim / 2;
+    float rcs[M], rsn[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        rcs[m] = 1.0f;
+        rsn[m] = 0.0f;
+        if (d < a.rot_dim) {
+            const float2 t = *reinterpret_cast<const float2*>(st->rope[m][d % half]);
+            rcs[m] = t.x;
+            rsn[m] = t.y;
+        }
+    }
+    // RMSNorm (1 + w) over each row's 256 dims: wave sums, then the 4 waves in order
+    float ss[NS];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) ss[j * M + m] = qv0[j][m] * qv0[j][m];
+        ss[G * M + m] = kv0[m] * kv0[m];
+    }
+    wave_sum_n(ss);
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < NS; ++i) red[w][i] = ss[i];
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int i = j * M + m;
+            const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
+            qs[i * HD + d] = (qv0[j][m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nq);
+        }
+        if (mine[m]) {
+            const int i = G * M + m;
+            const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
+            ks[m * HD + d] = (kv0[m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nk);
+        }
+    }
+    __syncthreads();
+    // rotate-half RoPE on the first rot_dim dims; the new keys and values go to the cache
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float cs = rcs[m], sn = rsn[m];
+        auto rot = [&](const float* v) {
+            if (d >= a.rot_dim) return v[d];
+            return d < half ? v[d] * cs - v[d + half] * sn : v[d] * cs + v[d - half] * sn;
+        };
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const float q = rot(qs + (j * M + m) * HD);
+            qr[(j * M + m) * HD + d] = q;
+            if (p == 0) a.qbuf[(size_t)m * q_dim + (kh * G + j) * HD + d] = q;
+        }
+        if (mine[m]) {
+            const _Float16 kq = (_Float16)rot(ks + m * HD), vq = (_Float16)vv0[m];
+            knew[m][d] = kq;
+            vnew[m][d] = vq;
+            const size_t c = (size_t)(pos0 + m) * kv_dim + kh * HD + d;
+            a.kcache[c] = __builtin_bit_cast(uint16_t, kq);
+            a.vcache[c] = __builtin_bit_cast(uint16_t, vq);
+        }
+    }
+    __syncthreads();
+    // the query fragments: lane (column n, k-group g) takes dims 32s + 8g .. + 7 of its column
     float qv[HD / 32][8];
     float amax = 0.0f;
 #pragma unroll
     for (int s = 0; s < HD / 32; ++s) {
         float4 u0 = make_float4(0.f, 0.f, 0.f, 0.f), u1 = u0;
         if (cm >= 0) {
-            const float4* qp = reinterpret_cast<const float4*>(a.qbuf + (size_t)cm * q_dim + (kh * G + chh) * HD + 32 * s + 8 * g);
+            const float4* qp = reinterpret_cast<const float4*>(qr + (chh * M + cm) * HD + 32 * s + 8 * g);
             u0 = qp[0];
             u1 = qp[1];
         }
@@ -156,6 +199,12 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[s][e]));
     }
+    // the key rows of this call's positions come from knew, not from the cache loads above
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+        if (mine[m] && kstart + 16 * w + n == pos0 + m)
+#pragma unroll
+            for (int s = 0; s < HD / 32; ++s) kf[s] = *reinterpret_cast<const u32x4_t*>(&knew[m][32 * s + 8 * g]);
     amax = xor_max<32>(xor_max<16>(amax));  // the 4 lanes of column n
     const int ex = amax > 0.0f ? max(ilogbf(amax) - 14, -110) : 0;
     const float down = ldexpf(1.0f, -ex), up = ldexpf(1.0f, ex) * a.scale;
@@ -169,9 +218,16 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
             qh[s][e] = hv;
             ql[s][e] = (_Float16)(v - (float)hv);
         }
+    __syncthreads();  // the staging above is read: the value tile may now take its space
 #pragma unroll
-    for (int i = 0; i < kPart / 8; ++i)
-        *reinterpret_cast<u32x4_t*>(vt + ((tid >> 5) + 8 * i) * VROW + (tid & 31) * 8) = vv[i];
+    for (int i = 0; i < kPart / 8; ++i) {
+        const int r = (tid >> 5) + 8 * i;
+        u32x4_t val = vv[i];
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            if (mine[m] && kstart + r == pos0 + m) val = *reinterpret_cast<const u32x4_t*>(&vnew[m][(tid & 31) * 8]);
+        *reinterpret_cast<u32x4_t*>(vt + r * VROW + (tid & 31) * 8) = val;
+    }
 
     // ---- scores: lane (column n, k-group g) ends with keys 16w + 4g + r ----
     f32x4_t c = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -316,7 +372,6 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
 int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
     if (M < 1 || M > 2 || a.n_heads != G * a.n_kv || a.rot_dim > HD || a.rot_dim % 2) return -1;
     if (a.ctx > kMaxCtx) return -1;
-    hipLaunchKernelGGL(prep_kernel, dim3(a.n_heads + 2 * a.n_kv, M), dim3(256), 0, s, a);
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     dim3 grid(a.n_kv, parts_max);
     switch (M) {

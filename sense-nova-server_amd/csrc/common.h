@@ -32,7 +32,11 @@ struct StepDev {
     int32_t x_off;  // LM head: first row of `hid` whose logits are produced
     uint32_t tokens[SNL_MAX_M];
     uint32_t rpos[SNL_MAX_M][4];  // rotary (t, h, w, 0) position of each row
+    // cos and sin of each row's rotary angles (attention.wgsl:90-110), formed on the host with
+    // the row's positions: rope[m][f] for frequency f < rot_dim / 2 (SNL_ROPE_MAX at most)
+    float rope[SNL_MAX_M][64][2];
 };
+#define SNL_ROPE_MAX 64
 
 // Token rows of one prefill pass (chunked prefill and the MTP head's catch-up over a prompt).
 #define SNL_PF_M 512

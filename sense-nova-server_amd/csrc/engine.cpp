@@ -25,6 +25,24 @@
 
 namespace snl {
 
+// cos / sin of the rotary angles of the step's rows (the reference's prep, attention.wgsl:90-110):
+// frequency f < rot_dim / 2 turns by pos * theta^(-2f / rot_dim), where pos is the row's t, h or w
+// position by the M-RoPE interleave (f % 3 == 1 below 3 * section[1] takes h, f % 3 == 2 below
+// 3 * section[2] takes w, the rest t).  The same float operations as a device-side prep.
+void step_rope(StepDev& st, int rows, float theta, int rot_dim, const int32_t* section) {
+    const int half = rot_dim / 2;
+    for (int m = 0; m < rows; ++m)
+        for (int f = 0; f < half && f < SNL_ROPE_MAX; ++f) {
+            uint32_t rp = st.rpos[m][0];
+            if (f % 3 == 1 && f < 3 * section[1]) rp = st.rpos[m][1];
+            else if (f % 3 == 2 && f < 3 * section[2]) rp = st.rpos[m][2];
+            const float inv_freq = powf(theta, -(float)(2 * f) / (float)rot_dim);
+            const float ang = (float)rp * inv_freq;
+            st.rope[m][f][0] = cosf(ang);
+            st.rope[m][f][1] = sinf(ang);
+        }
+}
+
 int device_error(hipError_t e, const char* what) {
     (void)e;
     (void)what;
@@ -502,6 +520,7 @@ static const char* validate(const snl_config* c) {
     if (c->lin_k_heads < 1 || c->lin_v_heads % c->lin_k_heads != 0)
         return "linear value heads must be a multiple of key heads";
     if (c->rot_dim % 2 != 0 || c->rot_dim > c->head_dim || c->rot_dim < 2) return "invalid rotary dim";
+    if (c->rot_dim > 2 * SNL_ROPE_MAX) return "rotary dim must be at most 128";
     if (c->mrope_section[0] + c->mrope_section[1] + c->mrope_section[2] != c->rot_dim / 2)
         return "M-RoPE sections must cover the rotary dims";
     if (!(c->loop_start < c->loop_end && c->loop_end <= c->n_layers && c->loop_count >= 1)) return "invalid loop range";
@@ -1193,6 +1212,7 @@ int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* po
             for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[i * 3 + k] : (uint32_t)(e->pos + i);
             st.rpos[i][3] = 0;
         }
+        step_rope(st, n, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
         int rc = e->run(0, n, rows, ckpt ? 1 : 0);
         if (rc) return rc;
         // the step record is reused by the next call: wait for this one
@@ -1238,6 +1258,7 @@ int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uin
         st.tokens[i] = tokens[i];
         for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3 ? pos3[i * 3 + k] : (uint32_t)(e->pos + i);
     }
+    step_rope(st, n, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
     if (hipMemcpyAsync(e->d_step, &st, sizeof(StepDev), hipMemcpyHostToDevice, e->stream) != hipSuccess)
         return e->fail(SNL_EDEVICE, "step upload failed");
     std::vector<snl_engine::Mark> marks;
@@ -1290,6 +1311,7 @@ int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch
     st.s_out = (e->cur + 2) % 3;
     for (int i = 0; i < 2; ++i)
         for (int k = 0; k < 3; ++k) st.rpos[i][k] = (uint32_t)(e->pos + i);
+    step_rope(st, 2, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
     if (hipMemcpyAsync(e->d_step, &st, sizeof(StepDev), hipMemcpyHostToDevice, e->stream) != hipSuccess)
         return e->fail(SNL_EDEVICE, "step upload failed");
     hipEvent_t t0 = nullptr, t1 = nullptr;
@@ -1352,6 +1374,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
             st.tokens[i] = tokens[c0 + i];
             for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3[(c0 + i) * 3 + k];
         }
+        step_rope(st, m, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
         int rc = e->run(1, m, last && draft ? 1 : 0, 0);
         if (rc) return rc;
         if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "mtp failed on device");
@@ -1935,13 +1958,16 @@ int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kca
                   float eps, const int32_t* mrope_section, int ctx, int M, int pos0, const uint32_t* rpos,
                   void* stream) {
     if (!proj || !qbuf || !kcache || !vcache || !norms || !out || !partial || !mrope_section || !rpos) return SNL_EARG;
-    if (M < 1 || M > 2 || pos0 < 0 || pos0 + M > ctx || n_heads != 4 * n_kv) return SNL_EARG;
+    if (M < 1 || M > 2 || pos0 < 0 || pos0 + M > ctx || n_heads != 4 * n_kv || rot_dim < 2 || rot_dim % 2 ||
+        rot_dim > 2 * SNL_ROPE_MAX)
+        return SNL_EARG;
     std::lock_guard<std::mutex> lk(g_kstep_mu);
     StepDev h{};
     h.pos0 = pos0;
     h.m = M;
     for (int i = 0; i < M; ++i)
         for (int k = 0; k < 3; ++k) h.rpos[i][k] = rpos[i * 3 + k];
+    step_rope(h, M, rope_theta, rot_dim, mrope_section);
     hipStream_t s = (hipStream_t)stream;
     StepDev* d = kernel_step(h, s);
     if (!d) return SNL_EDEVICE;
