@@ -120,7 +120,8 @@ def pmc_decode(snl, np, ops_out: str, passes: int = 3) -> int:
         ops = [(name, b) for name, b, _ in recs if name != "end"]
     eng.close()
     with open(ops_out, "w") as fh:
-        json.dump({"verify_ops": ops, "passes": passes, "pos": pos, "kv_dim": cfg.n_kv_heads * cfg.head_dim}, fh)
+        json.dump({"verify_ops": ops, "passes": passes, "pos": pos, "kv_dim": cfg.n_kv_heads * cfg.head_dim,
+                   "vocab": cfg.vocab}, fh)
     log(f"pmc decode workload: {len(ops)} ops per verify pass, {passes} eager passes at position {pos}")
     return 0
 
@@ -169,38 +170,53 @@ def summarize_decode_pmc(d: str) -> str:
     """Per-op HBM traffic and in-pass durations of the verify pass, as a markdown table.
 
     d holds: ops.json (pmc_decode), pf/pw (FETCH_SIZE / WRITE_SIZE of pmc_decode), kt (kernel trace
-    of pmc_decode), af/aw/at (the same for pmc_attention at 32K), cf/cw (the copy probe).  The last
-    passes x dispatches-per-pass counter rows are the op-by-op verify passes, labelled in launch
-    order; durations come from the graph-launched verify passes of the trace (same kernel order)."""
+    of pmc_decode), af/aw/at (the same for pmc_attention at 32K), cf/cw (the copy probe).  Each
+    op-by-op verify pass starts at its embed_kernel dispatch; its first dispatches are labelled with
+    the recorded ops in launch order (the engine's copies between passes are not labelled).
+    Durations come from the graph-launched verify passes of the trace, found as the runs of the same
+    kernel sequence that precede the op-by-op passes."""
     info = json.load(open(os.path.join(d, "ops.json")))
     ops, passes, pos = info["verify_ops"], info["passes"], info["pos"]
-    labels = []  # (op, kernel, algorithmic bytes) per dispatch of one verify pass
+    labels = []  # (op, algorithmic bytes) per dispatch of one verify pass
     for name, b in ops:
         ks = OP_KERNELS.get(name)
         if ks:
             for k in ks:
-                ab = (pos + 2) * info["kv_dim"] * 2 * 2 if k.startswith("attend") else 0.0
-                labels.append((name, k, ab))
+                if k.startswith("attend"):  # the K and V cache rows of one layer, f16
+                    ab = (pos + 2) * info["kv_dim"] * 2 * 2
+                elif k.startswith("pick_partial"):  # two rows of f32 logits
+                    ab = 2 * info.get("vocab", 248320) * 4
+                else:
+                    ab = 0.0
+                labels.append((name, ab))
         else:
-            labels.append((name, None, b))
+            labels.append((name, b))
     per = len(labels)
     true_kib = 256 * 1024.0
     ff = true_kib / _pmc_mean(os.path.join(d, "cf_counter_collection.csv"), "copyBuffer")
     wf = true_kib / _pmc_mean(os.path.join(d, "cw_counter_collection.csv"), "copyBuffer")
 
-    def counters(tag):
-        rows = _csv_rows(os.path.join(d, f"{tag}_counter_collection.csv"))
-        return rows
+    def passes_of(rows):
+        nm = [_short(r["Kernel_Name"]) for r in rows]
+        starts = [i for i, n in enumerate(nm) if n.startswith("embed_kernel")][-passes:]
+        segs = [rows[s:s + per] for s in starts]
+        seq = [_short(r["Kernel_Name"]) for r in segs[-1]]
+        for sg in segs:
+            if [_short(r["Kernel_Name"]) for r in sg] != seq:
+                raise SystemExit("op-by-op verify passes do not share one kernel sequence")
+        return segs, seq, nm, starts[0]
 
-    fr, wr = counters("pf"), counters("pw")
-    fr, wr = fr[-passes * per:], wr[-passes * per:]
-    # graph verify passes in the trace: segments whose kernel names follow the labelled sequence
+    fseg, seq, _, _ = passes_of(_csv_rows(os.path.join(d, "pf_counter_collection.csv")))
+    wseg, wseq, _, _ = passes_of(_csv_rows(os.path.join(d, "pw_counter_collection.csv")))
+    if wseq != seq:
+        raise SystemExit("FETCH_SIZE and WRITE_SIZE runs launched different kernels")
     kt = _csv_rows(os.path.join(d, "kt_kernel_trace.csv"))
-    names = [_short(r["Kernel_Name"]) for r in kt]
-    seq = [_short(fr[i]["Kernel_Name"]) for i in range(per)]
+    _, tseq, names, first_eager = passes_of(kt)
+    if tseq != seq:
+        raise SystemExit("the trace run launched different kernels")
     dur = [[] for _ in range(per)]
     i = 0
-    while i + per <= len(kt) - passes * per:
+    while i + per <= first_eager:
         if names[i:i + per] == seq:
             for j in range(per):
                 dur[j].append((int(kt[i + j]["End_Timestamp"]) - int(kt[i + j]["Start_Timestamp"])) / 1e3)
@@ -209,9 +225,8 @@ def summarize_decode_pmc(d: str) -> str:
             i += 1
     agg = {}
     order = []
-    for j, (op, k, ab) in enumerate(labels):
-        kname = seq[j]
-        key = (op, kname)
+    for j, (op, ab) in enumerate(labels):
+        key = (op, seq[j])
         if key not in agg:
             agg[key] = {"n": 0, "alg": 0.0, "fetch": 0.0, "write": 0.0, "us": []}
             order.append(key)
@@ -219,8 +234,8 @@ def summarize_decode_pmc(d: str) -> str:
         a["n"] += 1
         a["alg"] += ab
         for p in range(passes):
-            a["fetch"] += float(fr[p * per + j]["Counter_Value"]) * ff * 1024.0 / passes
-            a["write"] += float(wr[p * per + j]["Counter_Value"]) * wf * 1024.0 / passes
+            a["fetch"] += float(fseg[p][j]["Counter_Value"]) * ff * 1024.0 / passes
+            a["write"] += float(wseg[p][j]["Counter_Value"]) * wf * 1024.0 / passes
         a["us"] += dur[j]
     n_graph = len(dur[0]) if dur else 0
     out = [f"Verify pass at position {pos} (9B Q8_0, M = 2): {per} dispatches; counters averaged over "
@@ -238,12 +253,19 @@ def summarize_decode_pmc(d: str) -> str:
         ratio = f"{cnt / alg:.3f}" if alg > 0 else "-"
         out.append(f"| {key[0]} | `{key[1]}` | {n} | {alg / 1e6:.2f} | {cnt / 1e6:.2f} | {ratio} | {us:.2f} | "
                    f"{gbs:.0f} | {gbs / HBM_PEAK_GBS:.3f} |")
+    if n_graph:
+        t_us = sum(sum(a["us"]) / len(a["us"]) * a["n"] for a in agg.values())
+        t_alg = sum(a["alg"] for a in agg.values())
+        t_cnt = sum(a["fetch"] + a["write"] for a in agg.values())
+        g = t_alg / (t_us * 1e-6) / 1e9
+        out.append(f"| whole pass | {per} kernels | 1 | {t_alg / 1e6:.2f} | {t_cnt / 1e6:.2f} | "
+                   f"{t_cnt / t_alg:.3f} | {t_us:.2f} | {g:.0f} | {g / HBM_PEAK_GBS:.3f} |")
     # decode attention at 32K keys (kernel-level calls)
     if os.path.exists(os.path.join(d, "af_counter_collection.csv")):
         ainfo = json.load(open(os.path.join(d, "attn.json")))
         p0 = ainfo["pos"]
-        fa = [r for r in counters("af") if "attend_kernel" in r["Kernel_Name"]]
-        wa = [r for r in counters("aw") if "attend_kernel" in r["Kernel_Name"]]
+        fa = [r for r in _csv_rows(os.path.join(d, "af_counter_collection.csv")) if "attend_kernel" in r["Kernel_Name"]]
+        wa = [r for r in _csv_rows(os.path.join(d, "aw_counter_collection.csv")) if "attend_kernel" in r["Kernel_Name"]]
         ta = [r for r in _csv_rows(os.path.join(d, "at_kernel_trace.csv")) if "attend_kernel" in r["Kernel_Name"]]
         cnt = (sum(float(r["Counter_Value"]) for r in fa) / len(fa) * ff +
                sum(float(r["Counter_Value"]) for r in wa) / len(wa) * wf) * 1024.0
