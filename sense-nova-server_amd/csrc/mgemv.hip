@@ -134,30 +134,51 @@ __device__ __forceinline__ int a_pos(int e) {
 }
 
 // QT: 0 Q8_0, 1 Q4_0.  P: token pairs (M <= 2P).  U: quant blocks per lane group per superstep.
-// UPT: 8-element units of each token row per thread (K <= 8 * UPT * 512).
-template <int QT, int P, int EPI, int PRO, int U, int UPT>
+// UPT: 8-element units of each token row per staging thread.  IL: 1 chunk-major, 0 tile-major.
+//
+// Wave roles.  Chunk-major launches (one block per CU) run two kinds of waves: waves [0, sw0)
+// stream the weights (one (tile, slice) item each) and waves [sw0, nwv) stage the token rows.
+// The streaming waves issue their whole three-chunk ring at once and wait at the one block
+// barrier; a wave stalled at issue behind its own weights is then not holding up the prologue,
+// and the HBM stream starts with the kernel.  Tile-major launches (sw0 = 0) have every wave do
+// both, the first chunk before the staging and the others after it.
+//
+// The staging needs no block barrier of its own.  Each staged superstep of a token (512 or 128
+// elements) is one wave's lanes, which find its largest |value| by themselves and scale it by a
+// power of two into [2^13, 2^14) before the f16 hi + lo split; the main loop multiplies each
+// chunk's block scales by the superstep's inverse power of two (exact).  The RMSNorm factor
+// 1/rms of the branch input is applied to the dot products in the epilogue, from the staging
+// waves' sums of squares; the mHC pre-mix coefficients come from the router sums, which every
+// staging wave adds up itself from the producer's partials.
+template <int QT, int P, int EPI, int PRO, int U, int UPT, int IL>
 __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int base, int extra,
-                                                               int nss_w, int tiles, int il) {
+                                                               int nss_w, int tiles, int sw0) {
+    constexpr int il = IL;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
-    __shared__ float wst_s[kMaxWaves][2 * P][5];  // per-wave token statistics (sums, then maxima)
-    __shared__ __align__(16) float tok_s[2 * P][4];  // per token: input factor, output factor, pre0, pre1
-    __shared__ float raw_s[2 * P][9];  // mHC site sums (NORM_MHC)
-    __shared__ float cf_s[2 * P][8];   // mHC token coefficients (MHC epilogue)
+    __shared__ float ssq_s[kMaxWaves][2 * P];        // staging waves' sums of squares, per token
+    __shared__ float cf_s[2 * P][8];                 // mHC token coefficients (MHC epilogue)
     __shared__ float pr_s[kMaxWaves * 16 / 32][2 * P][9];  // next-site router sums per 32-row group
     constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
     constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
-    const int K = a.K, nb = K >> 5, K4 = K >> 2;
+    constexpr int SSU = 16 * U;               // 8-element units per superstep
+    const int K = a.K, nb = K >> 5, K4 = K >> 2, nss = K / (128 * U);
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int nthr = blockDim.x, nwv = nthr >> 6;
     const int bi = blockIdx.x;
     const int tile0 = bi * base + (bi < extra ? bi : extra);                 // first tile of the block
     const int cnt = min(base + (bi < extra ? 1 : 0), tiles - tile0);        // its tiles
     const int tw = wave / KS, ks = wave - tw * KS;
-    const bool active = tw < cnt;  // waves past the block's tiles only stage rows and reduce
+    const bool active = tw < cnt;  // staging waves (tw >= base + 1) and spare ones stream nothing
+    const bool stager = wave >= sw0;
     const int Tl = tile0 + (active ? tw : 0);
     const int j = lane & 15, g = lane >> 4;
-    const int nss = nss_w * KS;
+    const int tw_max = base + (extra ? 1 : 0);
+    // LDS: token fragments [P][nb][256 B], a zero fragment, the next site's router rows (rpart),
+    // then the superstep multipliers [P][nss][2]
+    const int zero_off = P * nb * 256;
+    const int rrow_off = zero_off + kZeroBytes;
+    float* const mult_s = reinterpret_cast<float*>(lds + rrow_off + (a.rpart ? tw_max * 16 * M * 64 : 0));
     // Weights stream through a ring of three chunks of CL loads (half a superstep when U == 4)
     // with the CS = U*CL/NI scales of their quant blocks.  Chunk q of this wave's item
     // i = T*KS + ks is at chunk index q*items + i (chunk-major, il) or i*nch + q (tile-major) of
@@ -202,78 +223,74 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     };
     // ---- prologue, part 1: every load of the token rows comes before the first weight load ----
     // Vector loads complete in issue order, so a row load issued after the weights would wait for
-    // them; this way the rows are staged while the weights stream in.  Thread tid owns the
-    // 8-element units tid + u*nthr (u < UPT) of every token row.
+    // them.  Staging thread ts owns the 8-element units ts + u*nst (u < UPT) of every token row.
+    const int ts = tid - sw0 * 64, nst = nthr - sw0 * 64;
     const int row0 = a.row_base ? *a.row_base : 0;
     const int K8 = K >> 3;
     const float4* xrow[2 * P];
 #pragma unroll
     for (int m = 0; m < 2 * P; ++m)
         xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
-    // mHC site sums: wave w adds sums w, w + 8, w + 16 (sum n = 9m + o) over the producer's blocks,
-    // lane l taking blocks l, l + 64, ... in order (partials are laid out [m][o][block]).  The
-    // first kRinBatch per lane are loaded here, in one batch; more producer blocks than
-    // 64 * kRinBatch are added later by a loop.
+    // mHC: the staging waves add this site's router sums 0, 1 and 8 of each token
+    // (layers.wgsl:94-102) from the producer's block partials, laid out [m][o][block]: lane l takes
+    // blocks l, l + 64, ... in order, the first kRinBatch of them loaded here in one batch.
     constexpr int kRinBatch = 4;
-    float rv[3][kRinBatch];
-    float sw0 = 0.0f, sw1 = 0.0f;
+    constexpr int kRinO[3] = {0, 1, 8};
+    float rv[2 * P][3][kRinBatch];
+    float sw0f = 0.0f, sw1f = 0.0f;
     if constexpr (PRO == GEMV_NORM_MHC) {
-        // buffer loads: a block past the producer's count, or a sum this launch does not have,
-        // reads zero, so the batch has no branches and no waits
+        if (stager) {
+            // buffer loads: a block past the producer's count, or a token this launch does not
+            // have, reads zero, so the batch has no branches and no waits
 #pragma unroll
-        for (int pi = 0; pi < 3; ++pi) {
-            const int n = wave + nwv * pi;
-            const bool on = n < 9 * M;
-            const __amdgpu_buffer_rsrc_t rr =
-                make_rsrc(a.rin + (size_t)(on ? n : 0) * a.rin_n, on ? (unsigned)a.rin_n * 4 : 0u);
+            for (int m = 0; m < 2 * P; ++m)
 #pragma unroll
-            for (int r = 0; r < kRinBatch; ++r)
-                rv[pi][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (lane + 64 * r) * 4, 0, 0));
+                for (int c = 0; c < 3; ++c) {
+                    const bool on = m < M;
+                    const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rin + (size_t)(on ? 9 * m + kRinO[c] : 0) * a.rin_n,
+                                                                on ? (unsigned)a.rin_n * 4 : 0u);
+#pragma unroll
+                    for (int r = 0; r < kRinBatch; ++r)
+                        rv[m][c][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (lane + 64 * r) * 4, 0, 0));
+                }
+            sw0f = a.site_w[(size_t)16 * K];
+            sw1f = a.site_w[(size_t)16 * K + 1];
         }
-        sw0 = a.site_w[(size_t)16 * K];
-        sw1 = a.site_w[(size_t)16 * K + 1];
-    }
-    // the site's 8 router biases for block 0, which forms the token coefficients
-    float bias8[8];
-#pragma unroll
-    for (int o = 0; o < 8; ++o) bias8[o] = 0.0f;
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        if (blockIdx.x == 0 && tid < M)
-#pragma unroll
-            for (int o = 0; o < 8; ++o) bias8[o] = a.site_w[(size_t)16 * K + o];
     }
     // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
     // of squares.
     float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
+    if (stager) {
 #pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-        const int k8 = tid + u * nthr;
-        const int kk = k8 < K8 ? k8 : 0;
-        if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
-            nw[u][0] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk];
-            nw[u][1] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk + 1];
-        }
+        for (int u = 0; u < UPT; ++u) {
+            const int k8 = ts + u * nst;
+            const int kk = k8 < K8 ? k8 : 0;
+            if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
+                nw[u][0] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk];
+                nw[u][1] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk + 1];
+            }
 #pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            if (m < M) {
-                xa[m][u][0] = xrow[m][2 * kk];
-                xa[m][u][1] = xrow[m][2 * kk + 1];
-                if constexpr (PRO == GEMV_NORM_MHC) {
-                    xb[m][u][0] = xrow[m][K4 + 2 * kk];
-                    xb[m][u][1] = xrow[m][K4 + 2 * kk + 1];
-                } else if constexpr (PRO == GEMV_GNORM) {
-                    gp[m][u] = reinterpret_cast<const float4*>(a.rin)[(size_t)m * (K / 128) + kk / 16];
+            for (int m = 0; m < 2 * P; ++m) {
+                if (m < M) {
+                    xa[m][u][0] = xrow[m][2 * kk];
+                    xa[m][u][1] = xrow[m][2 * kk + 1];
+                    if constexpr (PRO == GEMV_NORM_MHC) {
+                        xb[m][u][0] = xrow[m][K4 + 2 * kk];
+                        xb[m][u][1] = xrow[m][K4 + 2 * kk + 1];
+                    } else if constexpr (PRO == GEMV_GNORM) {
+                        gp[m][u] = reinterpret_cast<const float4*>(a.rin)[(size_t)m * (K / 128) + kk / 16];
+                    }
+                } else {
+                    xa[m][u][0] = xa[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    xb[m][u][0] = xb[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    gp[m][u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 }
-            } else {
-                xa[m][u][0] = xa[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                xb[m][u][0] = xb[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                gp[m][u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
         }
     }
 
-    // Thread tid owns output tid of the block (cnt*16*M <= 64*KS*cnt outputs, fewer than the
-    // threads); the residual it will update is read now, also ahead of the weights.
+    // Thread tid owns output tid of the block (cnt*16*M outputs, all in streaming waves); the
+    // residual it will update is read now, also ahead of the weights.
     const int e_m = tid % M, e_r = tid / M;
     const int e_T = tile0 + (e_r >> 4), e_j = e_r & 15;
     const int e_row = tid < cnt * 16 * M && !(EPI == GEMV_SWIGLU && e_j >= 8) ? tile_row<EPI>(a, e_T, e_j) : -1;
@@ -303,317 +320,312 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             }
     }
 
-    // Every wave of the block has issued its row loads before any wave issues weights, so the rows
-    // are not queued behind the block's weight stream.  Only the first chunk of the ring goes out
-    // before the rows are staged: a CU holds a bounded number of vector memory instructions in
-    // flight, and a wave that issued its whole ring here would stall at issue, behind its own
-    // weights, before it could stage the rows that had already arrived.
-    __builtin_amdgcn_s_barrier();
-    issue(w0, s0, 0);
-    // Tall tile-major matrices (the vocabulary head: many short blocks, several resident per CU)
-    // gain from odd waves sending their second chunk before the prologue as well: 168 -> 163 us
-    // per 248320 x 4096 Q8_0 head.  One block per CU loses from it: its waves then stall at issue
-    // and the block's prologue ends later.
-    const bool early = il == 0 && (wave & 1) != 0;
-    if (early) issue(w1, s1, 1);
-
-    // ---- prologue, part 2: per-token statistics of the branch input, one block barrier ----
-    // NORM: the sum of squares and the largest |x (1 + w)|.  NORM_MHC: the input is the pre-mix
-    // v = pre0 x0 + pre1 x1 with pre from this site's router sums, which arrive with the rows; so the
-    // waves gather sum x0^2, sum x0 x1, sum x1^2 and the largest |x0 (1 + w)|, |x1 (1 + w)| before
-    // pre is known, and the router sums and these statistics cross the block in the same barrier:
-    // sum v^2 = pre0^2 sum x0^2 + 2 pre0 pre1 sum x0 x1 + pre1^2 sum x1^2, and the f16 range check
-    // takes pre0 max|x0 (1 + w)| + pre1 max|x1 (1 + w)| (pre >= 0) as the bound of max|v (1 + w)|.
-    // GNORM applies the DeltaNet head factors now; PLAIN only needs the largest |x|.
-    constexpr int NS = PRO == GEMV_NORM_MHC ? 5 : 2;  // statistics per token
-    float stat[2 * P][NS];
+    // ---- prologue, part 2: the staging, wave by wave ----
+    float ssq[2 * P];  // this thread's sum of squares of the branch input, per token
 #pragma unroll
-    for (int m = 0; m < 2 * P; ++m)
+    for (int m = 0; m < 2 * P; ++m) ssq[m] = 0.0f;
+    auto stage = [&]() {
+        if (stager) {
+            float pre0[2 * P], pre1[2 * P];
 #pragma unroll
-        for (int k = 0; k < NS; ++k) stat[m][k] = 0.0f;
+            for (int m = 0; m < 2 * P; ++m) pre0[m] = 1.0f, pre1[m] = 0.0f;
+            if constexpr (PRO == GEMV_NORM_MHC) {
+                float rs[2 * P * 3];
 #pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-        if (tid + u * nthr >= K8) continue;
+                for (int m = 0; m < 2 * P; ++m)
 #pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            if (m >= M) continue;
+                    for (int c = 0; c < 3; ++c) {
+                        float t = 0.0f;
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                float4 t = xa[m][u][hh];
-                if constexpr (PRO == GEMV_GNORM) {  // the head factor of linear.wgsl:131-133
-                    const float4 pp = gp[m][u];
-                    const float var_o = (((pp.x + pp.y) + pp.z) + pp.w) / 128.0f;
-                    const float rr = 1.0f / sqrtf(var_o + a.eps);
-                    t.x = t.x * rr;
-                    t.y = t.y * rr;
-                    t.z = t.z * rr;
-                    t.w = t.w * rr;
-                    xa[m][u][hh] = t;
-                }
-                if constexpr (PRO == GEMV_NORM_MHC) {
-                    const float4 b = xb[m][u][hh], w = nw[u][hh];
-                    const float av[4] = {t.x, t.y, t.z, t.w}, bv[4] = {b.x, b.y, b.z, b.w};
-                    const float wv[4] = {1.0f + w.x, 1.0f + w.y, 1.0f + w.z, 1.0f + w.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        stat[m][0] = fmaf(av[e], av[e], stat[m][0]);
-                        stat[m][1] = fmaf(av[e], bv[e], stat[m][1]);
-                        stat[m][2] = fmaf(bv[e], bv[e], stat[m][2]);
-                        stat[m][3] = fmaxf(stat[m][3], fabsf(av[e] * wv[e]));
-                        stat[m][4] = fmaxf(stat[m][4], fabsf(bv[e] * wv[e]));
+                        for (int r = 0; r < kRinBatch; ++r) t = t + rv[m][c][r];
+                        if (m < M && a.rin_n > 64 * kRinBatch)
+                            for (int b = lane + 64 * kRinBatch; b < a.rin_n; b += 64)
+                                t = t + a.rin[(size_t)(9 * m + kRinO[c]) * a.rin_n + b];
+                        rs[m * 3 + c] = t;
                     }
-                } else {
-                    if constexpr (PRO == GEMV_NORM) {
-                        stat[m][0] = fmaf(t.x, t.x, stat[m][0]);
-                        stat[m][0] = fmaf(t.y, t.y, stat[m][0]);
-                        stat[m][0] = fmaf(t.z, t.z, stat[m][0]);
-                        stat[m][0] = fmaf(t.w, t.w, stat[m][0]);
-                        const float4 w = nw[u][hh];
-                        t.x = t.x * (1.0f + w.x);
-                        t.y = t.y * (1.0f + w.y);
-                        t.z = t.z * (1.0f + w.z);
-                        t.w = t.w * (1.0f + w.w);
+                wave_sum_n(rs);
+#pragma unroll
+                for (int m = 0; m < 2 * P; ++m) {
+                    if (m >= M) continue;
+                    const float rr = 1.0f / sqrtf(rs[m * 3 + 2] / (float)(2 * K) + 1e-6f);
+                    pre0[m] = 1.0f / (1.0f + __expf(-(rs[m * 3 + 0] * rr + sw0f)));
+                    pre1[m] = 1.0f / (1.0f + __expf(-(rs[m * 3 + 1] * rr + sw1f)));
+                }
+            }
+            // the branch input of each unit (layers.wgsl:57-73: pre-mix, then the (1 + w) weight; the
+            // 1/rms factor waits for the epilogue), its sum of squares, and its largest |value|
+            float umax[2 * P][UPT];
+#pragma unroll
+            for (int u = 0; u < UPT; ++u) {
+                const bool on = ts + u * nst < K8;
+#pragma unroll
+                for (int m = 0; m < 2 * P; ++m) {
+                    umax[m][u] = 0.0f;
+                    if (!on || m >= M) continue;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        float4 t = xa[m][u][hh];
+                        if constexpr (PRO == GEMV_GNORM) {  // the head factor of linear.wgsl:131-133
+                            const float4 pp = gp[m][u];
+                            const float var_o = (((pp.x + pp.y) + pp.z) + pp.w) / 128.0f;
+                            const float rr = 1.0f / sqrtf(var_o + a.eps);
+                            t.x = t.x * rr;
+                            t.y = t.y * rr;
+                            t.z = t.z * rr;
+                            t.w = t.w * rr;
+                        }
+                        if constexpr (PRO == GEMV_NORM_MHC) {
+                            const float4 v1 = xb[m][u][hh];
+                            t.x = pre0[m] * t.x + pre1[m] * v1.x;
+                            t.y = pre0[m] * t.y + pre1[m] * v1.y;
+                            t.z = pre0[m] * t.z + pre1[m] * v1.z;
+                            t.w = pre0[m] * t.w + pre1[m] * v1.w;
+                        }
+                        if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
+                            ssq[m] = fmaf(t.x, t.x, ssq[m]);
+                            ssq[m] = fmaf(t.y, t.y, ssq[m]);
+                            ssq[m] = fmaf(t.z, t.z, ssq[m]);
+                            ssq[m] = fmaf(t.w, t.w, ssq[m]);
+                            const float4 w = nw[u][hh];
+                            t.x = t.x * (1.0f + w.x);
+                            t.y = t.y * (1.0f + w.y);
+                            t.z = t.z * (1.0f + w.z);
+                            t.w = t.w * (1.0f + w.w);
+                        }
                         xa[m][u][hh] = t;
+                        umax[m][u] = fmaxf(umax[m][u], fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
                     }
-                    stat[m][1] = fmaxf(stat[m][1],
-                                       fmaxf(fmaxf(fabsf(t.x), fabsf(t.y)), fmaxf(fabsf(t.z), fabsf(t.w))));
                 }
             }
-        }
-    }
-    {
-        float sums[2 * P][NS == 5 ? 3 : 1], maxs[2 * P][2];
+            // superstep maxima: the SSU units of a superstep are SSU consecutive lanes of this wave
 #pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            if constexpr (NS == 5) {
-                sums[m][0] = stat[m][0], sums[m][1] = stat[m][1], sums[m][2] = stat[m][2];
-                maxs[m][0] = stat[m][3], maxs[m][1] = stat[m][4];
-            } else {
-                sums[m][0] = stat[m][0];
-                maxs[m][0] = stat[m][1], maxs[m][1] = 0.0f;
+            for (int u = 0; u < UPT; ++u)
+#pragma unroll
+                for (int m = 0; m < 2 * P; ++m) {
+                    float v = umax[m][u];
+                    v = xor_max<1>(v);
+                    v = xor_max<2>(v);
+                    v = xor_max<4>(v);
+                    v = xor_max<8>(v);
+                    if constexpr (SSU == 64) {
+                        v = xor_max<16>(v);
+                        v = xor_max<32>(v);
+                    }
+                    umax[m][u] = v;
+                }
+            // power-of-two scale per (token, superstep): the largest |value| lands in [2^13, 2^14), so
+            // the f16 high part cannot overflow and keeps 11 bits, the low part 11 more
+#pragma unroll
+            for (int u = 0; u < UPT; ++u) {
+                const int k8 = ts + u * nst;
+                if (k8 >= K8) continue;
+                const int S = k8 / SSU;
+#pragma unroll
+                for (int m = 0; m < 2 * P; ++m) {
+                    const float mx = umax[m][u];
+                    int e = mx > 0.0f ? ilogbf(mx) - 13 : 0;
+                    e = e < -120 ? -120 : (e > 120 ? 120 : e);
+                    const float f = ldexpf(1.0f, -e);
+                    if (k8 % SSU == 0) mult_s[((m >> 1) * nss + S) * 2 + (m & 1)] = ldexpf(1.0f, e);
+                    // unit k8 of token m -> 8 hi then 8 lo f16 in fragment order inside region (pair, block, token)
+                    const float v[8] = {xa[m][u][0].x, xa[m][u][0].y, xa[m][u][0].z, xa[m][u][0].w,
+                                        xa[m][u][1].x, xa[m][u][1].y, xa[m][u][1].z, xa[m][u][1].w};
+                    half8_t hi, lo;
+#pragma unroll
+                    for (int e8 = 0; e8 < 8; ++e8) {
+                        const float y = v[e8] * f;
+                        const _Float16 hv = (_Float16)y;
+                        const int pidx = a_pos<QT>(e8);
+                        hi[pidx] = hv;
+                        lo[pidx] = (_Float16)(y - (float)hv);
+                    }
+                    unsigned char* bp =
+                        lds + ((size_t)(m >> 1) * nb + (k8 >> 2)) * 256 + (m & 1) * 128 + (k8 & 3) * 16;
+                    *reinterpret_cast<half8_t*>(bp) = hi;
+                    *reinterpret_cast<half8_t*>(bp + 64) = lo;
+                }
+            }
+            if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
+                wave_sum_n(ssq);
+                if (lane == 0)
+#pragma unroll
+                    for (int m = 0; m < 2 * P; ++m) ssq_s[wave][m] = ssq[m];
             }
         }
-        wave_sum_n(*reinterpret_cast<float(*)[2 * P * (NS == 5 ? 3 : 1)]>(&sums[0][0]));
-        wave_max_n(*reinterpret_cast<float(*)[2 * P * 2]>(&maxs[0][0]));
-        if (lane == 0)
-#pragma unroll
-            for (int m = 0; m < 2 * P; ++m) {
-#pragma unroll
-                for (int k = 0; k < (NS == 5 ? 3 : 1); ++k) wst_s[wave][m][k] = sums[m][k];
-                wst_s[wave][m][3] = maxs[m][0];
-                wst_s[wave][m][4] = maxs[m][1];
+    };
+    // small LDS items: the zero fragment, the next site's router rows, the token coefficients
+    auto side_lds = [&]() {
+        if (tid < kZeroBytes / 16)
+            reinterpret_cast<float4*>(lds + zero_off)[tid] = make_float4(0, 0, 0, 0);
+        // the next site's router rows wait in LDS until the epilogue, instead of holding 16 registers
+        // through the main loop
+        if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
+            if (a.rpart && e_row >= 0) {
+                float4* st = reinterpret_cast<float4*>(lds + rrow_off) + tid * 4;
+                st[0] = make_float4(nr0[0], nr0[1], nr0[2], nr0[3]);
+                st[1] = make_float4(nr0[4], nr0[5], nr0[6], nr0[7]);
+                st[2] = make_float4(nr1[0], nr1[1], nr1[2], nr1[3]);
+                st[3] = make_float4(nr1[4], nr1[5], nr1[6], nr1[7]);
             }
-    }
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        // this site's router sums (layers.wgsl:94-102) from the producer's block partials
-        float rsum[3];
-#pragma unroll
-        for (int pi = 0; pi < 3; ++pi) {
-            float t = 0.0f;
-#pragma unroll
-            for (int r = 0; r < kRinBatch; ++r) t = t + rv[pi][r];
-            const int n = wave + nwv * pi;
-            if (n < 9 * M && a.rin_n > 64 * kRinBatch) {
-                const int m = n / 9, o = n - 9 * (n / 9);
-                for (int b = lane + 64 * kRinBatch; b < a.rin_n; b += 64) t = t + a.rin[(size_t)(m * 9 + o) * a.rin_n + b];
-            }
-            rsum[pi] = t;
         }
-        wave_sum_n(rsum);
-#pragma unroll
-        for (int pi = 0; pi < 3; ++pi) {
-            const int n = wave + nwv * pi;
-            if (lane == 0 && n < 9 * M) raw_s[n / 9][n - 9 * (n / 9)] = rsum[pi];
+        if constexpr (EPI == GEMV_MHC) {
+            if (tid < 8 * M) cf_s[tid >> 3][tid & 7] = cfv;
         }
-    }
-    if (tid < kZeroBytes / 16)
-        reinterpret_cast<float4*>(lds + (size_t)P * nb * 256)[tid] = make_float4(0, 0, 0, 0);
-    lds_barrier();
-    // thread m < 2P forms token m's factors from the waves' statistics (added in wave order): the
-    // input factor scales the row before the f16 split, the output factor the dot products after
-    if (tid < 2 * P) {
-        const int m = tid;
-        float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, m0 = 0.0f, m1 = 0.0f;
-        for (int w = 0; w < nwv; ++w) {
-            s0 = s0 + wst_s[w][m][0];
-            if constexpr (NS == 5) {
-                s1 = s1 + wst_s[w][m][1];
-                s2 = s2 + wst_s[w][m][2];
-            }
-            m0 = fmaxf(m0, wst_s[w][m][3]);
-            m1 = fmaxf(m1, wst_s[w][m][4]);
-        }
-        float rinv = 1.0f, top = m0, p0 = 1.0f, p1 = 0.0f;
+    };
+    auto sinkhorn = [&]() {
         if constexpr (PRO == GEMV_NORM_MHC) {
-            if (m < M) {
-                const float rr = 1.0f / sqrtf(raw_s[m][8] / (float)(2 * K) + 1e-6f);
-                p0 = 1.0f / (1.0f + __expf(-(raw_s[m][0] * rr + sw0)));
-                p1 = 1.0f / (1.0f + __expf(-(raw_s[m][1] * rr + sw1)));
-            }
-            const float ss = (p0 * p0 * s0 + 2.0f * p0 * p1 * s1) + p1 * p1 * s2;
-            rinv = 1.0f / sqrtf(ss / (float)K + a.eps);
-            top = (p0 * m0 + p1 * m1) * rinv;
-        } else if constexpr (PRO == GEMV_NORM) {
-            rinv = 1.0f / sqrtf(s0 / (float)K + a.eps);
-            top = m0 * rinv;
-        }
-        // keep |x| * factor below 2^14 so the f16 high part cannot overflow
-        const int e = top >= 16384.0f ? ilogbf(top) - 13 : 0;
-        tok_s[m][0] = m < M ? ldexpf(rinv, -e) : 0.0f;
-        tok_s[m][1] = ldexpf(1.0f, e);
-        tok_s[m][2] = p0;
-        tok_s[m][3] = p1;
-    }
-    lds_barrier();
-    float tokf[2 * P], toko[2 * P], pre0[2 * P], pre1[2 * P];
+            // Block 0's last wave (a staging wave, idle during the main loop) adds all nine site sums
+            // of each token the same way, stores them, and turns them into the token coefficients
+            // (2x2 Sinkhorn) for the MHC epilogue of the same site, a later launch.
+            if (blockIdx.x == 0 && wave == nwv - 1) {
+                // one batch of range-checked loads, as in the staging (a block past the producer's
+                // count reads zero), then the sums in the same order
+                float rs[2 * P * 9], rb[2 * P][9][kRinBatch];
 #pragma unroll
-    for (int m = 0; m < 2 * P; ++m) {
-        const float4 t = *reinterpret_cast<const float4*>(tok_s[m]);
-        tokf[m] = t.x;
-        toko[m] = t.y;
-        pre0[m] = t.z;
-        pre1[m] = t.w;
-    }
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        if (blockIdx.x == 0 && tid < 9 * M) a.raw[tid] = raw_s[tid / 9][tid - 9 * (tid / 9)];
-        // the pre-mix and the norm weight of the branch input (layers.wgsl:57-73)
+                for (int m = 0; m < 2 * P; ++m)
 #pragma unroll
-        for (int u = 0; u < UPT; ++u) {
-            if (tid + u * nthr >= K8) continue;
+                    for (int o = 0; o < 9; ++o) {
+                        const bool on = m < M;
+                        const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rin + (size_t)(on ? 9 * m + o : 0) * a.rin_n,
+                                                                    on ? (unsigned)a.rin_n * 4 : 0u);
 #pragma unroll
-            for (int m = 0; m < 2 * P; ++m) {
-                if (m >= M) continue;
+                        for (int r = 0; r < kRinBatch; ++r)
+                            rb[m][o][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (lane + 64 * r) * 4, 0, 0));
+                    }
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    float4 t = xa[m][u][hh];
-                    const float4 v1 = xb[m][u][hh], w = nw[u][hh];
-                    t.x = pre0[m] * t.x + pre1[m] * v1.x;
-                    t.y = pre0[m] * t.y + pre1[m] * v1.y;
-                    t.z = pre0[m] * t.z + pre1[m] * v1.z;
-                    t.w = pre0[m] * t.w + pre1[m] * v1.w;
-                    t.x = t.x * (1.0f + w.x);
-                    t.y = t.y * (1.0f + w.y);
-                    t.z = t.z * (1.0f + w.z);
-                    t.w = t.w * (1.0f + w.w);
-                    xa[m][u][hh] = t;
+                for (int m = 0; m < 2 * P; ++m)
+#pragma unroll
+                    for (int o = 0; o < 9; ++o) {
+                        float t = 0.0f;
+#pragma unroll
+                        for (int r = 0; r < kRinBatch; ++r) t = t + rb[m][o][r];
+                        if (m < M && a.rin_n > 64 * kRinBatch)
+                            for (int b = lane + 64 * kRinBatch; b < a.rin_n; b += 64) t = t + a.rin[(size_t)(9 * m + o) * a.rin_n + b];
+                        rs[m * 9 + o] = t;
+                    }
+                wave_sum_n(rs);
+                if (lane < M) {
+                    float raw[9], bias8[8], cf[8];
+#pragma unroll
+                    for (int o = 0; o < 9; ++o) raw[o] = lane == 0 ? rs[o] : rs[9 + o];
+#pragma unroll
+                    for (int o = 0; o < 9; ++o) a.raw[lane * 9 + o] = raw[o];
+#pragma unroll
+                    for (int o = 0; o < 8; ++o) bias8[o] = a.site_w[(size_t)16 * K + o];
+                    mhc_coefficients_b(raw, bias8, 2 * K, a.iterations, cf);
+#pragma unroll
+                    for (int o = 0; o < 8; ++o) a.coef[lane * 8 + o] = cf[o];
                 }
             }
         }
-    }
-    // unit k8 of token m -> 8 hi then 8 lo f16 in fragment order inside region (pair, block, token)
-#pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-        const int k8 = tid + u * nthr;
-        if (k8 >= K8) continue;
-#pragma unroll
-        for (int m = 0; m < 2 * P; ++m) {
-            const float f = tokf[m];
-            const float v[8] = {xa[m][u][0].x, xa[m][u][0].y, xa[m][u][0].z, xa[m][u][0].w,
-                                xa[m][u][1].x, xa[m][u][1].y, xa[m][u][1].z, xa[m][u][1].w};
-            half8_t hi, lo;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float y = v[e] * f;
-                const _Float16 hv = (_Float16)y;
-                const int pidx = a_pos<QT>(e);
-                hi[pidx] = hv;
-                lo[pidx] = (_Float16)(y - (float)hv);
-            }
-            unsigned char* base =
-                lds + ((size_t)(m >> 1) * nb + (k8 >> 2)) * 256 + (m & 1) * 128 + (k8 & 3) * 16;
-            *reinterpret_cast<half8_t*>(base) = hi;
-            *reinterpret_cast<half8_t*>(base + 64) = lo;
-        }
-    }
-    // the next site's router rows wait in LDS (after the staged rows and the zero fragment) until
-    // the epilogue, instead of holding 16 registers through the main loop
-    if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
-        if (a.rpart && e_row >= 0) {
-            float4* st = reinterpret_cast<float4*>(lds + (size_t)P * nb * 256 + kZeroBytes) + tid * 4;
-            st[0] = make_float4(nr0[0], nr0[1], nr0[2], nr0[3]);
-            st[1] = make_float4(nr0[4], nr0[5], nr0[6], nr0[7]);
-            st[2] = make_float4(nr1[0], nr1[1], nr1[2], nr1[3]);
-            st[3] = make_float4(nr1[4], nr1[5], nr1[6], nr1[7]);
-        }
-    }
-    if (!early) issue(w1, s1, 1);
-    issue(w2, s2, 2);
-    lds_barrier();
-    if constexpr (PRO == GEMV_NORM_MHC) {
-        // block 0 turns the site sums into the token coefficients (2x2 Sinkhorn) for the MHC epilogue
-        // of the same site, a later launch; done here, while its weight ring is in flight, so it does
-        // not lengthen the launch's tail
-        if (blockIdx.x == 0 && tid < M) {
-            float cf[8];
-            mhc_coefficients_b(raw_s[tid], bias8, 2 * K, a.iterations, cf);
-#pragma unroll
-            for (int o = 0; o < 8; ++o) a.coef[tid * 8 + o] = cf[o];
-        }
-    }
-    if constexpr (EPI == GEMV_MHC) {
-        if (tid < 8 * M) cf_s[tid >> 3][tid & 7] = cfv;
-    }
+
+    };
 
     // ---- main loop ----
-    // lane (j, g) feeds A row j = 4*slot + combo; it carries data only when slot == g
-    const int slot = j >> 2, combo = j & 3;
-    const bool a_on = slot == g;
     f32x4_t acc[P];
 #pragma unroll
     for (int p = 0; p < P; ++p) acc[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const int zero_off = P * nb * 256;
+    auto main_loop = [&]() {
+        // lane (j, g) feeds A row j = 4*slot + combo; it carries data only when slot == g
+        const int slot = j >> 2, combo = j & 3;
+        const bool a_on = slot == g;
 
-    auto compute = [&](const uint4 (&w)[CL], const float (&sc)[CS], int q) {
-        const int S = ks * nss_w + q / CPS;  // superstep within the row
+        auto compute = [&](const uint4 (&w)[CL], const float (&sc)[CS], int q) {
+            const int S = ks * nss_w + q / CPS;  // superstep within the row
+            float2 mm[P];                        // its power-of-two multipliers, token 0 and 1 of each pair
 #pragma unroll
-        for (int i0 = 0; i0 < CL; ++i0) {
-            const int v = (q % CPS) * CL + i0;                              // load within the superstep
-            const int blk = S * 4 * U + U * g + (QT == 0 ? (v >> 1) : v);  // quant block of this load
-            const int eoff = QT == 0 ? (v & 1) * 16 : 0;                  // first element in the block
-            int abase[P];
+            for (int p = 0; p < P; ++p) mm[p] = *reinterpret_cast<const float2*>(mult_s + (p * nss + S) * 2);
 #pragma unroll
-            for (int p = 0; p < P; ++p)
-                abase[p] = a_on ? ((p * nb + blk) * 4 + combo) * 64 + eoff * 2 : zero_off;
-            f32x4_t d[P];
+            for (int i0 = 0; i0 < CL; ++i0) {
+                const int v = (q % CPS) * CL + i0;                              // load within the superstep
+                const int blk = S * 4 * U + U * g + (QT == 0 ? (v >> 1) : v);  // quant block of this load
+                const int eoff = QT == 0 ? (v & 1) * 16 : 0;                  // first element in the block
+                int abase[P];
 #pragma unroll
-            for (int p = 0; p < P; ++p) d[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int p = 0; p < P; ++p)
+                    abase[p] = a_on ? ((p * nb + blk) * 4 + combo) * 64 + eoff * 2 : zero_off;
+                f32x4_t d[P];
 #pragma unroll
-            for (int i = 0; i < NM; ++i) {
-                const half8_t b = dequant8<QT>(w[i0], i);
+                for (int p = 0; p < P; ++p) d[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int i = 0; i < NM; ++i) {
+                    const half8_t b = dequant8<QT>(w[i0], i);
+#pragma unroll
+                    for (int p = 0; p < P; ++p) {
+                        const half8_t av = *reinterpret_cast<const half8_t*>(lds + abase[p] + (a_on ? 16 * i : 0));
+                        d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, d[p], 0, 0, 0);
+                    }
+                }
+                const float scale = sc[QT == 0 ? (i0 >> 1) : i0];
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
-                    const half8_t av = *reinterpret_cast<const half8_t*>(lds + abase[p] + (a_on ? 16 * i : 0));
-                    d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, d[p], 0, 0, 0);
+                    // combos 0, 1: token 0 hi, lo; combos 2, 3: token 1
+                    const float sm0 = scale * mm[p].x, sm1 = scale * mm[p].y;
+                    acc[p][0] = fmaf(sm0, d[p][0], acc[p][0]);
+                    acc[p][1] = fmaf(sm0, d[p][1], acc[p][1]);
+                    acc[p][2] = fmaf(sm1, d[p][2], acc[p][2]);
+                    acc[p][3] = fmaf(sm1, d[p][3], acc[p][3]);
                 }
             }
-            const float scale = sc[QT == 0 ? (i0 >> 1) : i0];
-#pragma unroll
-            for (int p = 0; p < P; ++p)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[p][r] = fmaf(scale, d[p][r], acc[p][r]);
+        };
+
+        // Steady state: compute a chunk, issue the one three ahead.  The last five chunks or fewer run
+        // as a straight-line tail that issues nothing past the slice.
+        const int nrun = active ? nch : 0;
+        int q = 0;
+        for (; q + 5 < nrun; q += 3) {
+            compute(w0, s0, q);
+            issue(w0, s0, q + 3);
+            compute(w1, s1, q + 1);
+            issue(w1, s1, q + 4);
+            compute(w2, s2, q + 2);
+            issue(w2, s2, q + 5);
         }
+        const int rem = nrun - q;  // 0 (idle wave) .. 5
+        if (rem >= 1) compute(w0, s0, q);
+        if (rem >= 4) issue(w0, s0, q + 3);
+        if (rem >= 2) compute(w1, s1, q + 1);
+        if (rem >= 5) issue(w1, s1, q + 4);
+        if (rem >= 3) compute(w2, s2, q + 2);
+        if (rem >= 4) compute(w0, s0, q + 3);
+        if (rem >= 5) compute(w1, s1, q + 4);
+
     };
 
-    // Steady state: compute a chunk, issue the one three ahead.  The last five chunks or fewer run
-    // as a straight-line tail that issues nothing past the slice.
-    const int nrun = active ? nch : 0;
-    int q = 0;
-    for (; q + 5 < nrun; q += 3) {
-        compute(w0, s0, q);
-        issue(w0, s0, q + 3);
-        compute(w1, s1, q + 1);
-        issue(w1, s1, q + 4);
-        compute(w2, s2, q + 2);
-        issue(w2, s2, q + 5);
+    // Every wave of the block has issued its row loads before any wave issues weights, so the rows
+    // are not queued behind the block's weight stream.  The two roles run in separate branches, so
+    // a staging wave holds no weight ring and a streaming wave no token rows.
+    __builtin_amdgcn_s_barrier();
+    if constexpr (IL == 1) {
+        if (stager) {
+            stage();
+            side_lds();
+            lds_barrier();
+            sinkhorn();
+        } else {
+            // streaming-only waves send the whole ring at once
+            issue(w0, s0, 0);
+            issue(w1, s1, 1);
+            issue(w2, s2, 2);
+            side_lds();
+            lds_barrier();
+            main_loop();
+        }
+    } else {
+        // Tile-major launches (the vocabulary head: many short blocks, several resident per CU):
+        // the odd waves send their second chunk before the staging too (168 -> 163 us per
+        // 248320 x 4096 Q8_0 head), the others after it.
+        issue(w0, s0, 0);
+        const bool early = (wave & 1) != 0;
+        if (early) issue(w1, s1, 1);
+        stage();
+        side_lds();
+        if (!early) issue(w1, s1, 1);
+        issue(w2, s2, 2);
+        lds_barrier();
+        sinkhorn();
+        main_loop();
     }
-    const int rem = nrun - q;  // 0 (idle wave) .. 5
-    if (rem >= 1) compute(w0, s0, q);
-    if (rem >= 4) issue(w0, s0, q + 3);
-    if (rem >= 2) compute(w1, s1, q + 1);
-    if (rem >= 5) issue(w1, s1, q + 4);
-    if (rem >= 3) compute(w2, s2, q + 2);
-    if (rem >= 4) compute(w0, s0, q + 3);
-    if (rem >= 5) compute(w1, s1, q + 4);
 
     // ---- reduction: hi + lo, then the 4 lane groups, then the K slices in order ----
 #pragma unroll
@@ -634,10 +646,13 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         const int t2 = e_r >> 4;
         float v = 0.0f;
         for (int k = 0; k < KS; ++k) v = v + red_s[((t2 * KS + k) * 16 + e_j) * 2 * P + e_m];
-        float of = toko[0];
-#pragma unroll
-        for (int m = 1; m < 2 * P; ++m)
-            if (e_m == m) of = toko[m];
+        // the RMSNorm factor of the branch input, from the staging waves' sums in wave order
+        float of = 1.0f;
+        if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
+            float ss = 0.0f;
+            for (int w = sw0; w < nwv; ++w) ss = ss + ssq_s[w][e_m];
+            of = 1.0f / sqrtf(ss / (float)K + a.eps);
+        }
         v = v * of;
         float* y = a.y + (size_t)e_m * a.y_stride;
         if constexpr (EPI == GEMV_SWIGLU) {
@@ -670,7 +685,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             // the association is the same for every M
             float c[9];
             if (e_row >= 0) {
-                const float4* st = reinterpret_cast<const float4*>(lds + (size_t)P * nb * 256 + kZeroBytes) + tid * 4;
+                const float4* st = reinterpret_cast<const float4*>(lds + rrow_off) + tid * 4;
                 const float4 q0 = st[0], q1 = st[1], q2 = st[2], q3 = st[3];
                 const float r0[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
                 const float r1[8] = {q2.x, q2.y, q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
@@ -714,20 +729,30 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
 using KernelFn = void (*)(GemvArgs, int, int, int, int, int, int, int);
 
 template <int QT, int U, int UPT>
-KernelFn pick_fn(int P, int epi, int pro) {
+KernelFn pick_fn(int P, int epi, int pro, int il) {
 #define SNL_G(E, PR) \
-    if (epi == E && pro == PR) return &mgemv_kernel<QT, 1, E, PR, U, UPT>;
+    if (epi == E && pro == PR) return &mgemv_kernel<QT, 1, E, PR, U, UPT, 1>;
+    if (il == 0) {
+        // tile-major (the vocabulary head, the draft's with its final norm): the plain store
+        if constexpr (UPT <= 2) {
+            if (P == 1 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 1, GEMV_STORE, GEMV_PLAIN, U, UPT, 0>;
+            if (P == 1 && epi == GEMV_STORE && pro == GEMV_NORM) return &mgemv_kernel<QT, 1, GEMV_STORE, GEMV_NORM, U, UPT, 0>;
+        }
+        if constexpr (UPT == 1)
+            if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U, 1, 0>;
+        return nullptr;
+    }
     if (P == 1) {
         SNL_G(GEMV_STORE, GEMV_PLAIN)
-        SNL_G(GEMV_STORE, GEMV_NORM)
         SNL_G(GEMV_ADD, GEMV_PLAIN)
-        SNL_G(GEMV_ADD, GEMV_NORM)
         SNL_G(GEMV_MHC, GEMV_PLAIN)
-        SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
-        SNL_G(GEMV_SWIGLU, GEMV_NORM)
-        // the mHC pre-mix reads two residual streams of the hidden size, the gated head norm the
-        // DeltaNet output: K <= 8192 (one unit per thread)
-        if constexpr (UPT == 1) {
+        // a normed branch input, the mHC pre-mix of two residual streams of the hidden size and the
+        // gated head norm of the DeltaNet output: at most 2 units per staging thread
+        if constexpr (UPT <= 2) {
+            SNL_G(GEMV_STORE, GEMV_NORM)
+            SNL_G(GEMV_ADD, GEMV_NORM)
+            SNL_G(GEMV_SWIGLU, GEMV_PLAIN)
+            SNL_G(GEMV_SWIGLU, GEMV_NORM)
             SNL_G(GEMV_STORE, GEMV_NORM_MHC)
             SNL_G(GEMV_SWIGLU, GEMV_NORM_MHC)
             SNL_G(GEMV_ADD, GEMV_GNORM)
@@ -736,21 +761,24 @@ KernelFn pick_fn(int P, int epi, int pro) {
         }
     }
 #undef SNL_G
-    // two token pairs: the plain product at K <= 4096 only (kernel-level calls with M = 3, 4)
-    if constexpr (UPT == 1)
-        if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U, 1>;
+    // two token pairs: the plain product with at most 2 units per staging thread (kernel-level
+    // calls with M = 3, 4)
+    if constexpr (UPT <= 2)
+        if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U, UPT, 1>;
     return nullptr;
 }
 
-KernelFn pick(int quant, int U, int UPT, int P, int epi, int pro) {
-    if (UPT == 1) {
-        if (quant == 0) return U == 4 ? pick_fn<0, 4, 1>(P, epi, pro) : pick_fn<0, 1, 1>(P, epi, pro);
-        return U == 4 ? pick_fn<1, 4, 1>(P, epi, pro) : pick_fn<1, 1, 1>(P, epi, pro);
-    }
-    if (UPT == 3) {
-        if (quant == 0) return U == 4 ? pick_fn<0, 4, 3>(P, epi, pro) : pick_fn<0, 1, 3>(P, epi, pro);
-        return U == 4 ? pick_fn<1, 4, 3>(P, epi, pro) : pick_fn<1, 1, 3>(P, epi, pro);
-    }
+template <int UPT>
+KernelFn pick_upt(int quant, int U, int P, int epi, int pro, int il) {
+    if (quant == 0) return U == 4 ? pick_fn<0, 4, UPT>(P, epi, pro, il) : pick_fn<0, 1, UPT>(P, epi, pro, il);
+    return U == 4 ? pick_fn<1, 4, UPT>(P, epi, pro, il) : pick_fn<1, 1, UPT>(P, epi, pro, il);
+}
+
+// UPT: 1 to 3 units per staging thread
+KernelFn pick(int quant, int U, int UPT, int P, int epi, int pro, int il) {
+    if (UPT == 1) return pick_upt<1>(quant, U, P, epi, pro, il);
+    if (UPT == 2) return pick_upt<2>(quant, U, P, epi, pro, il);
+    if (UPT == 3) return pick_upt<3>(quant, U, P, epi, pro, il);
     return nullptr;
 }
 
@@ -795,16 +823,17 @@ int launch_pack_matrix(const PackGeom& g, const void* q, const float* s, void* q
 int mgemv_init() {
     for (int q = 0; q < 2; ++q)
         for (int U = 1; U <= 4; U += 3)
-            for (int upt = 1; upt <= 3; upt += 2)
+            for (int upt = 1; upt <= 3; ++upt)
                 for (int P = 1; P <= 2; ++P)
                     for (int e = 0; e < 4; ++e)
-                        for (int p = 0; p < 4; ++p) {
-                            KernelFn f = pick(q, U, upt, P, e, p);
-                            if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
-                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                         kLdsLimit) != hipSuccess)
-                                return -2;
-                        }
+                        for (int p = 0; p < 4; ++p)
+                            for (int il = 0; il < 2; ++il) {
+                                KernelFn f = pick(q, U, upt, P, e, p, il);
+                                if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
+                                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                             kLdsLimit) != hipSuccess)
+                                    return -2;
+                            }
     return 0;
 }
 
@@ -813,40 +842,53 @@ namespace {
 // Launch shape, from the matrix shape only (the K split is the packing's, packing.h).
 struct Shape {
     int KS, base, extra, blocks, waves, nss_w, upt;
+    int sw0;           // streaming-only waves (chunk-major); 0: every wave stages and streams
     size_t lds_floor;  // dynamic LDS requested at least (keeps one block per CU)
 };
 
 // Chunk-major matrices: one block per CU (fewer when there are fewer tiles), tiles spread base /
-// base + 1 per block; such a block asks for more than half a CU's LDS, so no CU holds two.
+// base + 1 per block, one streaming wave per (tile, slice) item and pack_stage_waves(K) staging
+// waves; such a block asks for more than half a CU's LDS, so no CU holds two.
 // Tile-major (the vocabulary head): short blocks of 2 tiles x KS slices, several per CU
-// (measured: 248320 x 4096 Q8_0, 215 us with 1 slice x 8 tiles, 180 us at 4 x 2).  Blocks have at
-// least 8 waves and enough threads that a token row is at most 3 units of 8 elements per thread.
+// (measured: 248320 x 4096 Q8_0, 215 us with 1 slice x 8 tiles, 180 us at 4 x 2), at least 8
+// waves, every wave staging.  A staging thread takes at most 3 units of 8 elements of a row.
 bool mgemv_shape(const PackGeom& g, Shape* sh) {
     int TW;
+    const int K8 = g.K / 8;
     if (g.il) {
         sh->blocks = g.tiles < kCUs ? g.tiles : kCUs;
         sh->base = g.tiles / sh->blocks;
         sh->extra = g.tiles % sh->blocks;
         TW = sh->base + (sh->extra ? 1 : 0);
         sh->lds_floor = 84 * 1024;
+        sh->sw0 = g.KS * TW;
+        sh->waves = sh->sw0 + pack_stage_waves(g.K);
     } else {
         TW = 8 / g.KS;
         sh->base = TW;
         sh->extra = 0;
         sh->blocks = (g.tiles + TW - 1) / TW;
         sh->lds_floor = 0;
+        sh->sw0 = 0;
+        int waves = g.KS * TW;
+        if (waves < 8) waves = 8;
+        while (waves < kMaxWaves && waves * 64 < K8) ++waves;  // one unit per thread where that fits
+        sh->waves = waves;
     }
-    const int K8 = g.K / 8;
-    int waves = g.KS * TW;
-    if (waves < 8) waves = 8;
-    while (waves < kMaxWaves && waves * 64 < K8) ++waves;  // one unit per thread where that fits
-    const int upt = (K8 + waves * 64 - 1) / (waves * 64);
-    if (upt > 3 || g.KS * TW > kMaxWaves) return false;
+    if (sh->waves > kMaxWaves) return false;
+    const int nst = (sh->waves - sh->sw0) * 64;
+    const int upt = (K8 + nst - 1) / nst;
+    if (upt > 3) return false;
     sh->KS = g.KS;
-    sh->waves = waves;
     sh->nss_w = g.nss_w;
-    sh->upt = upt == 1 ? 1 : 3;
+    sh->upt = upt;
     return true;
+}
+
+// dynamic LDS: token fragments, the zero fragment, the next site's router rows, the multipliers
+size_t lds_bytes(int M, int K, int U, size_t rrow_bytes) {
+    const int P = M <= 2 ? 1 : 2;
+    return (size_t)P * (K / 32) * 256 + kZeroBytes + rrow_bytes + (size_t)P * (K / (128 * U)) * 8;
 }
 }  // namespace
 
@@ -857,13 +899,11 @@ int mgemv_blocks(int quant, int N, int K, int inter) {
     return sh.blocks;
 }
 
-size_t mgemv_lds_bytes(int M, int K) { return (size_t)(M <= 2 ? 1 : 2) * (K / 32) * 256 + kZeroBytes; }
-
 bool mgemv_fits(int M, int K) {
     PackGeom g;
     Shape sh;
     if (!pack_geom(0, 16, K, 0, &g) || !mgemv_shape(g, &sh)) return false;
-    return (M <= 2 || sh.upt == 1) && mgemv_lds_bytes(M, K) <= (size_t)kLdsLimit;
+    return (M <= 2 || sh.upt <= 2) && lds_bytes(M, K, g.U, 0) <= (size_t)kLdsLimit;
 }
 
 // 0: launched; 1: this call is not served (M too large for LDS at this K); < 0 error.
@@ -875,8 +915,8 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if (!mgemv_shape(g, &sh)) return 1;
     const int P = M <= 2 ? 1 : 2;
     const int tw_max = sh.base + (sh.extra ? 1 : 0);
-    const size_t need = mgemv_lds_bytes(M, a.K) + (a.rpart ? (size_t)tw_max * 16 * M * 64 : 0);
-    if (need > (size_t)kLdsLimit || (P == 2 && sh.upt != 1)) return 1;
+    const size_t need = lds_bytes(M, a.K, g.U, a.rpart ? (size_t)tw_max * 16 * M * 64 : 0);
+    if (need > (size_t)kLdsLimit || (P == 2 && sh.upt > 2)) return 1;
     const size_t lds = need > sh.lds_floor ? need : sh.lds_floor;
     if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
         (reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_stride & 3))
@@ -886,10 +926,10 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if (a.epi == GEMV_MHC && !a.coef) return -1;
     if (a.rpart && (!a.next_w || (a.epi != GEMV_ADD && a.epi != GEMV_MHC) || (M & (M - 1)))) return -1;
     if (a.epi == GEMV_ADD && a.rpart && !a.expand) return -1;  // an ADD producer starts the mHC range
-    KernelFn f = pick(quant, g.U, sh.upt, P, a.epi, a.pro);
+    KernelFn f = pick(quant, g.U, sh.upt, P, a.epi, a.pro, g.il);
     if (!f) return 1;
     hipLaunchKernelGGL(f, dim3(sh.blocks), dim3(sh.waves * 64), lds, s, a, M, sh.KS, sh.base, sh.extra, sh.nss_w,
-                       g.tiles, g.il);
+                       g.tiles, sh.sw0);
     return hipGetLastError() == hipSuccess ? 0 : -2;
 }
 

@@ -52,18 +52,27 @@ struct PackGeom {
 };
 
 constexpr int kPackCUs = 256;       // MI355X compute units
-constexpr int kPackMaxWaves = 16;   // waves per GEMV block
+constexpr int kPackWaves = 16;      // waves per chunk-major GEMV block
 
-// The K split: up to 16 tiles per CU, one block per CU holds base or base + 1 tiles and KS is the
-// largest divisor of the superstep count with KS * (base + 1) <= 16 waves (chunk-major order);
-// taller matrices run many blocks of 2 tiles x KS <= 4 slices (tile-major order).
+// Waves of a chunk-major block that stage the token rows: enough that a staging thread takes at
+// most 3 units of 8 elements of a row, and at least 4.  The other waves stream the weights.
+__host__ __device__ inline int pack_stage_waves(int K) {
+    const int w = (K / 8 + 191) / 192;
+    return w < 4 ? 4 : w;
+}
+
+// The K split: one block per CU holds base or base + 1 tiles and KS is the largest divisor of the
+// superstep count with KS * (base + 1) streaming waves at most (chunk-major order: up to 12 tiles
+// per CU at K <= 6144); taller matrices run many blocks of 2 tiles x KS <= 4 slices (tile-major
+// order).
 __host__ __device__ inline void pack_split(PackGeom* g) {
     int KS = 1;
+    const int max_items = kPackWaves - pack_stage_waves(g->K);
     // (chunk-major offsets are 32-bit: matrices up to 2 GiB)
-    if (g->tiles <= 16 * kPackCUs && g->q_bytes < ((size_t)1 << 31)) {
+    if (max_items >= 1 && g->tiles <= max_items * kPackCUs && g->q_bytes < ((size_t)1 << 31)) {
         const int blocks = g->tiles < kPackCUs ? g->tiles : kPackCUs;
         const int tw = g->tiles / blocks + (g->tiles % blocks ? 1 : 0);
-        for (int d = 1; d <= g->nss && d * tw <= kPackMaxWaves; ++d)
+        for (int d = 1; d <= g->nss && d * tw <= max_items; ++d)
             if (g->nss % d == 0) KS = d;
         g->il = 1;
     } else {
