@@ -102,6 +102,21 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// 16 bytes per lane from global memory straight into LDS (lane i at dst + 16 i), by DMA: no
+// register receives the data.  Issued as inline assembly, so the compiler's wait insertion does
+// not see it; the reader waits on the vector memory count itself.
+__device__ __forceinline__ void copy16_to_lds(const char* base, unsigned voff, unsigned dst) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(base)
+                 : "memory", "m0");
+}
+
+// Makes a loaded value opaque to the compiler at this point (no instruction is emitted), so that
+// its first use, and the wait for the load, cannot be hoisted above: the staging waves issue every
+// load of the prologue first and consume them only after the block barrier that orders the weight
+// stream behind them.  (Without it the compiler waited for the first loads before issuing the rest.)
+__device__ __forceinline__ void opaque(float& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void opaque(f32x4_t& v) { asm volatile("" : "+v"(v)); }
+
 // 8 weights of one 16-byte load as exact f16: MFMA i (0..NM-1) of the load.
 // Q8 order: elements 8i..8i+7.  Q4 order (word i): elements 8i + {0, 4, 1, 5, 2, 6, 3, 7}.
 template <int QT>
@@ -158,6 +173,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
     __shared__ float ssq_s[kMaxWaves][2 * P];        // staging waves' sums of squares, per token
     __shared__ float cf_s[2 * P][8];                 // mHC token coefficients (MHC epilogue)
+    __shared__ float raw_s[2 * P][9];                // last block: this site's router sums (NORM_MHC)
     __shared__ float pr_s[kMaxWaves * 16 / 32][2 * P][9];  // next-site router sums per 32-row group
     constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
     constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
@@ -227,63 +243,79 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const int ts = tid - sw0 * 64, nst = nthr - sw0 * 64;
     const int row0 = a.row_base ? *a.row_base : 0;
     const int K8 = K >> 3;
-    const float4* xrow[2 * P];
+    // Every staging load is a range-checked buffer load without a branch: a token past M, a unit
+    // past the row or a GNORM head past the buffer reads zero.  (A branch would join the loaded
+    // value with a constant, and that join waits for the load.)
+    const unsigned row_bytes = (unsigned)(PRO == GEMV_NORM_MHC ? 2 * K : K) * 4;
+    __amdgpu_buffer_rsrc_t xr[2 * P];
 #pragma unroll
     for (int m = 0; m < 2 * P; ++m)
-        xrow[m] = reinterpret_cast<const float4*>(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride);
+        xr[m] = make_rsrc(a.x + (size_t)(row0 + (m < M ? m : 0)) * a.x_stride, m < M ? row_bytes : 0u);
+    auto ld4 = [](__amdgpu_buffer_rsrc_t r, int off) {
+        return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    };
     // mHC: the staging waves add this site's router sums 0, 1 and 8 of each token
     // (layers.wgsl:94-102) from the producer's block partials, laid out [m][o][block]: lane l takes
-    // blocks l, l + 64, ... in order, the first kRinBatch of them loaded here in one batch.
-    constexpr int kRinBatch = 4;
+    // blocks l, l + 64, ... in order.  The first 256 partials of each sum go to the wave's own LDS
+    // slots by DMA (global_load_lds: no registers, so nothing is consumed before the barrier);
+    // more producer blocks than 256 are added later from global memory.  The last block also needs
+    // the site's other sums (o = 2..7) for the token coefficients: the 6M of them are spread over
+    // its staging waves, kXtra each.
     constexpr int kRinO[3] = {0, 1, 8};
-    float rv[2 * P][3][kRinBatch];
-    float sw0f = 0.0f, sw1f = 0.0f;
+    constexpr int kXtra = 3;                         // 6M <= 12 sums over >= 4 staging waves
+    constexpr int kRinSlots = 2 * P * 3 + kXtra;     // 1 KiB LDS slots per staging wave
+    const unsigned rin_off = ((unsigned)(reinterpret_cast<unsigned char*>(mult_s) - lds) + (unsigned)P * nss * 8 + 15u) & ~15u;
+    const unsigned rin_w = rin_off + (unsigned)(wave - sw0) * kRinSlots * 1024;  // this wave's slots
+    f32x4_t sb[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};  // the 8 router biases
     if constexpr (PRO == GEMV_NORM_MHC) {
         if (stager) {
-            // buffer loads: a block past the producer's count, or a token this launch does not
-            // have, reads zero, so the batch has no branches and no waits
+            const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
+            // the 256-partial window may run past a shorter producer into other sums (masked when
+            // added) but stays inside the partials buffer (kPartBlocks rows per sum)
 #pragma unroll
             for (int m = 0; m < 2 * P; ++m)
 #pragma unroll
-                for (int c = 0; c < 3; ++c) {
-                    const bool on = m < M;
-                    const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rin + (size_t)(on ? 9 * m + kRinO[c] : 0) * a.rin_n,
-                                                                on ? (unsigned)a.rin_n * 4 : 0u);
+                for (int c = 0; c < 3; ++c)
+                    if (m < M)
+                        copy16_to_lds(reinterpret_cast<const char*>(a.rin + (size_t)(9 * m + kRinO[c]) * a.rin_n),
+                                      (unsigned)lane * 16u, lds_base + rin_w + (unsigned)(m * 3 + c) * 1024u);
+            if (blockIdx.x == gridDim.x - 1)
 #pragma unroll
-                    for (int r = 0; r < kRinBatch; ++r)
-                        rv[m][c][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (lane + 64 * r) * 4, 0, 0));
+                for (int x = 0; x < kXtra; ++x) {
+                    const int k = (wave - sw0) + (nwv - sw0) * x;  // sum index m*6 + (o - 2)
+                    if (k < 6 * M)
+                        copy16_to_lds(reinterpret_cast<const char*>(a.rin + (size_t)(9 * (k / 6) + 2 + k % 6) * a.rin_n),
+                                      (unsigned)lane * 16u, lds_base + rin_w + (unsigned)(2 * P * 3 + x) * 1024u);
                 }
-            sw0f = a.site_w[(size_t)16 * K];
-            sw1f = a.site_w[(size_t)16 * K + 1];
+            const __amdgpu_buffer_rsrc_t br = make_rsrc(a.site_w + (size_t)16 * K, 32u);
+            sb[0] = ld4(br, 0);
+            sb[1] = ld4(br, 16);
         }
     }
     // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
     // of squares.
-    float4 xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
+    f32x4_t xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
     if (stager) {
+        const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.norm_w, (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) ? (unsigned)K * 4 : 0u);
+        // GNORM: the head partials [M][K/128][4]
+        const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.rin, PRO == GEMV_GNORM ? (unsigned)(M * (K / 128) * 16) : 0u);
 #pragma unroll
         for (int u = 0; u < UPT; ++u) {
             const int k8 = ts + u * nst;
-            const int kk = k8 < K8 ? k8 : 0;
+            const int ko = k8 < K8 ? k8 * 32 : row_bytes;  // byte offset of the unit (past the row: zero)
             if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
-                nw[u][0] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk];
-                nw[u][1] = reinterpret_cast<const float4*>(a.norm_w)[2 * kk + 1];
+                nw[u][0] = ld4(nr, ko);
+                nw[u][1] = ld4(nr, ko + 16);
             }
 #pragma unroll
             for (int m = 0; m < 2 * P; ++m) {
-                if (m < M) {
-                    xa[m][u][0] = xrow[m][2 * kk];
-                    xa[m][u][1] = xrow[m][2 * kk + 1];
-                    if constexpr (PRO == GEMV_NORM_MHC) {
-                        xb[m][u][0] = xrow[m][K4 + 2 * kk];
-                        xb[m][u][1] = xrow[m][K4 + 2 * kk + 1];
-                    } else if constexpr (PRO == GEMV_GNORM) {
-                        gp[m][u] = reinterpret_cast<const float4*>(a.rin)[(size_t)m * (K / 128) + kk / 16];
-                    }
-                } else {
-                    xa[m][u][0] = xa[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    xb[m][u][0] = xb[m][u][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                    gp[m][u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                xa[m][u][0] = ld4(xr[m], ko);
+                xa[m][u][1] = ld4(xr[m], ko + 16);
+                if constexpr (PRO == GEMV_NORM_MHC) {
+                    xb[m][u][0] = ld4(xr[m], K * 4 + ko);
+                    xb[m][u][1] = ld4(xr[m], K * 4 + ko + 16);
+                } else if constexpr (PRO == GEMV_GNORM) {
+                    gp[m][u] = ld4(gr, m < M && k8 < K8 ? (m * (K / 128) + k8 / 16) * 16 : (int)(M * (K / 128) * 16));
                 }
             }
         }
@@ -324,8 +356,34 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     float ssq[2 * P];  // this thread's sum of squares of the branch input, per token
 #pragma unroll
     for (int m = 0; m < 2 * P; ++m) ssq[m] = 0.0f;
+    // sum n of this wave's partial slot: lane l adds blocks l, l + 64, ... in order
+    auto rin_sum = [&](int slot, int n) {
+        const float* pl = reinterpret_cast<const float*>(lds + rin_w + slot * 1024);
+        float t = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int b = lane + 64 * r;
+            t = t + (b < a.rin_n ? pl[b] : 0.0f);
+        }
+        for (int b = lane + 256; b < a.rin_n; b += 64) t = t + a.rin[(size_t)n * a.rin_n + b];
+        return t;
+    };
     auto stage = [&]() {
         if (stager) {
+            if constexpr (PRO == GEMV_NORM_MHC) __builtin_amdgcn_s_waitcnt(0);  // the DMA slots have landed
+#pragma unroll
+            for (int u = 0; u < UPT; ++u) {
+                if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) opaque(nw[u][0]), opaque(nw[u][1]);
+#pragma unroll
+                for (int m = 0; m < 2 * P; ++m) {
+                    opaque(xa[m][u][0]);
+                    opaque(xa[m][u][1]);
+                    if constexpr (PRO == GEMV_NORM_MHC) opaque(xb[m][u][0]), opaque(xb[m][u][1]);
+                    if constexpr (PRO == GEMV_GNORM) opaque(gp[m][u]);
+                }
+            }
+            if constexpr (PRO == GEMV_NORM_MHC) opaque(sb[0]), opaque(sb[1]);
+            const float sw0f = sb[0].x, sw1f = sb[0].y;
             float pre0[2 * P], pre1[2 * P];
 #pragma unroll
             for (int m = 0; m < 2 * P; ++m) pre0[m] = 1.0f, pre1[m] = 0.0f;
@@ -334,15 +392,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
 #pragma unroll
                 for (int m = 0; m < 2 * P; ++m)
 #pragma unroll
-                    for (int c = 0; c < 3; ++c) {
-                        float t = 0.0f;
-#pragma unroll
-                        for (int r = 0; r < kRinBatch; ++r) t = t + rv[m][c][r];
-                        if (m < M && a.rin_n > 64 * kRinBatch)
-                            for (int b = lane + 64 * kRinBatch; b < a.rin_n; b += 64)
-                                t = t + a.rin[(size_t)(9 * m + kRinO[c]) * a.rin_n + b];
-                        rs[m * 3 + c] = t;
-                    }
+                    for (int c = 0; c < 3; ++c) rs[m * 3 + c] = m < M ? rin_sum(m * 3 + c, 9 * m + kRinO[c]) : 0.0f;
                 wave_sum_n(rs);
 #pragma unroll
                 for (int m = 0; m < 2 * P; ++m) {
@@ -350,6 +400,28 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                     const float rr = 1.0f / sqrtf(rs[m * 3 + 2] / (float)(2 * K) + 1e-6f);
                     pre0[m] = 1.0f / (1.0f + __expf(-(rs[m * 3 + 0] * rr + sw0f)));
                     pre1[m] = 1.0f / (1.0f + __expf(-(rs[m * 3 + 1] * rr + sw1f)));
+                }
+                if (blockIdx.x == gridDim.x - 1) {
+                    // the further sums, added in the same order, and all nine to LDS for the
+                    // coefficients after the prologue barrier
+                    float xs[kXtra];
+#pragma unroll
+                    for (int x = 0; x < kXtra; ++x) {
+                        const int k = (wave - sw0) + (nwv - sw0) * x;
+                        xs[x] = k < 6 * M ? rin_sum(2 * P * 3 + x, 9 * (k / 6) + 2 + k % 6) : 0.0f;
+                    }
+                    wave_sum_n(xs);
+                    if (lane == 0) {
+#pragma unroll
+                        for (int x = 0; x < kXtra; ++x) {
+                            const int k = (wave - sw0) + (nwv - sw0) * x;
+                            if (k < 6 * M) raw_s[k / 6][2 + k % 6] = xs[x];
+                        }
+                        if (wave == sw0)
+#pragma unroll
+                            for (int m = 0; m < 2 * P; ++m)
+                                if (m < M) raw_s[m][0] = rs[m * 3], raw_s[m][1] = rs[m * 3 + 1], raw_s[m][8] = rs[m * 3 + 2];
+                    }
                 }
             }
             // the branch input of each unit (layers.wgsl:57-73: pre-mix, then the (1 + w) weight; the
@@ -364,9 +436,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                     if (!on || m >= M) continue;
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        float4 t = xa[m][u][hh];
+                        f32x4_t t = xa[m][u][hh];
                         if constexpr (PRO == GEMV_GNORM) {  // the head factor of linear.wgsl:131-133
-                            const float4 pp = gp[m][u];
+                            const f32x4_t pp = gp[m][u];
                             const float var_o = (((pp.x + pp.y) + pp.z) + pp.w) / 128.0f;
                             const float rr = 1.0f / sqrtf(var_o + a.eps);
                             t.x = t.x * rr;
@@ -375,7 +447,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                             t.w = t.w * rr;
                         }
                         if constexpr (PRO == GEMV_NORM_MHC) {
-                            const float4 v1 = xb[m][u][hh];
+                            const f32x4_t v1 = xb[m][u][hh];
                             t.x = pre0[m] * t.x + pre1[m] * v1.x;
                             t.y = pre0[m] * t.y + pre1[m] * v1.y;
                             t.z = pre0[m] * t.z + pre1[m] * v1.z;
@@ -386,7 +458,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                             ssq[m] = fmaf(t.y, t.y, ssq[m]);
                             ssq[m] = fmaf(t.z, t.z, ssq[m]);
                             ssq[m] = fmaf(t.w, t.w, ssq[m]);
-                            const float4 w = nw[u][hh];
+                            const f32x4_t w = nw[u][hh];
                             t.x = t.x * (1.0f + w.x);
                             t.y = t.y * (1.0f + w.y);
                             t.z = t.z * (1.0f + w.z);
@@ -474,44 +546,20 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     };
     auto sinkhorn = [&]() {
         if constexpr (PRO == GEMV_NORM_MHC) {
-            // Block 0's last wave (a staging wave, idle during the main loop) adds all nine site sums
-            // of each token the same way, stores them, and turns them into the token coefficients
-            // (2x2 Sinkhorn) for the MHC epilogue of the same site, a later launch.
-            if (blockIdx.x == 0 && wave == nwv - 1) {
-                // one batch of range-checked loads, as in the staging (a block past the producer's
-                // count reads zero), then the sums in the same order
-                float rs[2 * P * 9], rb[2 * P][9][kRinBatch];
-#pragma unroll
-                for (int m = 0; m < 2 * P; ++m)
-#pragma unroll
-                    for (int o = 0; o < 9; ++o) {
-                        const bool on = m < M;
-                        const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.rin + (size_t)(on ? 9 * m + o : 0) * a.rin_n,
-                                                                    on ? (unsigned)a.rin_n * 4 : 0u);
-#pragma unroll
-                        for (int r = 0; r < kRinBatch; ++r)
-                            rb[m][o][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rr, (lane + 64 * r) * 4, 0, 0));
-                    }
-#pragma unroll
-                for (int m = 0; m < 2 * P; ++m)
-#pragma unroll
-                    for (int o = 0; o < 9; ++o) {
-                        float t = 0.0f;
-#pragma unroll
-                        for (int r = 0; r < kRinBatch; ++r) t = t + rb[m][o][r];
-                        if (m < M && a.rin_n > 64 * kRinBatch)
-                            for (int b = lane + 64 * kRinBatch; b < a.rin_n; b += 64) t = t + a.rin[(size_t)(9 * m + o) * a.rin_n + b];
-                        rs[m * 9 + o] = t;
-                    }
-                wave_sum_n(rs);
+            // The last block's last wave (a staging wave, idle during the main loop) stores the
+            // site's nine router sums of each token, which its staging waves left in LDS, and turns
+            // them into the token coefficients (2x2 Sinkhorn) for the MHC epilogue of the same site,
+            // a later launch.  It touches no global memory before its stores: a load here would
+            // queue behind the block's weight stream.
+            if (blockIdx.x == gridDim.x - 1 && wave == nwv - 1) {
                 if (lane < M) {
                     float raw[9], bias8[8], cf[8];
 #pragma unroll
-                    for (int o = 0; o < 9; ++o) raw[o] = lane == 0 ? rs[o] : rs[9 + o];
+                    for (int o = 0; o < 9; ++o) raw[o] = raw_s[lane][o];
 #pragma unroll
                     for (int o = 0; o < 9; ++o) a.raw[lane * 9 + o] = raw[o];
 #pragma unroll
-                    for (int o = 0; o < 8; ++o) bias8[o] = a.site_w[(size_t)16 * K + o];
+                    for (int o = 0; o < 4; ++o) bias8[o] = sb[0][o], bias8[4 + o] = sb[1][o];
                     mhc_coefficients_b(raw, bias8, 2 * K, a.iterations, cf);
 #pragma unroll
                     for (int o = 0; o < 8; ++o) a.coef[lane * 8 + o] = cf[o];
@@ -593,8 +641,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     };
 
     // Every wave of the block has issued its row loads before any wave issues weights, so the rows
-    // are not queued behind the block's weight stream.  The two roles run in separate branches, so
-    // a staging wave holds no weight ring and a streaming wave no token rows.
+    // are not queued behind the block's weight stream (issued after it they arrived ~6 us later).
+    // The staging waves reach this barrier without waiting for any load.  The two roles run in
+    // separate branches, so a staging wave holds no weight ring and a streaming wave no token rows.
     __builtin_amdgcn_s_barrier();
     if constexpr (IL == 1) {
         if (stager) {
@@ -885,10 +934,12 @@ bool mgemv_shape(const PackGeom& g, Shape* sh) {
     return true;
 }
 
-// dynamic LDS: token fragments, the zero fragment, the next site's router rows, the multipliers
-size_t lds_bytes(int M, int K, int U, size_t rrow_bytes) {
+// dynamic LDS: token fragments, the zero fragment, the next site's router rows, the multipliers,
+// and (NORM_MHC) the staging waves' router partial slots, 9 KiB each
+size_t lds_bytes(int M, int K, int U, size_t rrow_bytes, int rin_waves = 0) {
     const int P = M <= 2 ? 1 : 2;
-    return (size_t)P * (K / 32) * 256 + kZeroBytes + rrow_bytes + (size_t)P * (K / (128 * U)) * 8;
+    const size_t b = (size_t)P * (K / 32) * 256 + kZeroBytes + rrow_bytes + (size_t)P * (K / (128 * U)) * 8;
+    return rin_waves ? ((b + 15) & ~(size_t)15) + (size_t)rin_waves * 9 * 1024 : b;
 }
 }  // namespace
 
@@ -915,7 +966,8 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if (!mgemv_shape(g, &sh)) return 1;
     const int P = M <= 2 ? 1 : 2;
     const int tw_max = sh.base + (sh.extra ? 1 : 0);
-    const size_t need = lds_bytes(M, a.K, g.U, a.rpart ? (size_t)tw_max * 16 * M * 64 : 0);
+    const size_t need = lds_bytes(M, a.K, g.U, a.rpart ? (size_t)tw_max * 16 * M * 64 : 0,
+                                  a.pro == GEMV_NORM_MHC ? sh.waves - sh.sw0 : 0);
     if (need > (size_t)kLdsLimit || (P == 2 && sh.upt > 2)) return 1;
     const size_t lds = need > sh.lds_floor ? need : sh.lds_floor;
     if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
