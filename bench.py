@@ -37,7 +37,7 @@ sys.path.insert(0, os.path.join(REPO, "sense-nova-server_amd"))
 METRIC = "9B Q8_0 MTP greedy decode tok/s (1 GPU); Q8 GEMV GB/s vs HBM peak"
 HBM_PEAK_GBS = 8000.0
 PROMPT = 1024
-ROOFLINE_KERNEL = "mgemv_kernel<0, 1, 3, 2, 4, 1>"  # Q8_0, one token pair, SwiGLU epilogue, mHC prologue, U=4, UPT=1
+ROOFLINE_KERNEL = "mgemv_kernel<0, 1, 3, 2, 4, 2, 1>"  # Q8_0, one token pair, SwiGLU epilogue, mHC input, U=4, UPT=2, chunk-major
 # HBM traffic of the roofline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (see summarize_pmc);
 # reported only while the kernel sources hash to the value recorded with it.
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "gemv_gate_up_9b_q8_traffic.json")
@@ -551,8 +551,8 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gate_up GEMV, mgemv_kernel<0, 1, 3, 2, 4, 1> (mHC-RMSNorm prologue, 48 launches per "
-                      "verify pass) and <0, 1, 3, 1, 4, 1> (RMSNorm prologue, 8), Q8_0, M=2, N=24576, K=4096, "
+            "kernel": "gate_up GEMV, mgemv_kernel<0, 1, 3, 2, 4, 2, 1> (mHC-RMSNorm input, 48 launches per "
+                      "verify pass) and <0, 1, 3, 1, 4, 2, 1> (RMSNorm input, 8), Q8_0, M=2, N=24576, K=4096, "
                       "SwiGLU epilogue",
             "achieved": round(achieved, 1),
             "launch_us": round(inpass_us, 3),

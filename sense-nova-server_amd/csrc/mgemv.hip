@@ -13,7 +13,8 @@
 //     (the f16 1024 + byte), and one packed f16 subtract of 1152 leaves q; Q4 nibbles are masked
 //     into the same f16 pattern and 1032 is subtracted;
 //   * each token row x (f32) is split into two f16 parts, hi = f16(x) and lo = f16(x - hi), whose
-//     sum carries 22 significant bits; a per-token power of two keeps hi inside the f16 range.
+//     sum carries 22 significant bits; a power of two per token and superstep scales the part's
+//     largest |x| into [2^13, 2^14), so hi cannot overflow and small rows keep their bits.
 // The accumulation is f32 throughout.
 //
 // MFMA orientation.  A (16 x 32) holds x, B (32 x 16) holds 16 weight rows.  The 4 lane groups of
@@ -26,21 +27,20 @@
 //
 // Work split.  A tile is 16 weight rows (SwiGLU: 8 gate rows and the matching 8 up rows).  A
 // superstep is 128*U elements of a row (U = 4 when K % 512 == 0, else 1), 8 KiB of a Q8 tile;
-// K is cut into KS equal slices of supersteps.  Up to 4096 tiles, the grid is one block per CU
-// (at most 256 blocks, one resident per CU): block b owns the consecutive tiles
-// [b*base + min(b, extra), +base + (b < extra)), and its wave w the item (tile w / KS, slice
-// w % KS), so every active wave streams the same bytes and every CU the same number of waves'
-// worth (a block with one tile fewer leaves KS waves idle).  Taller matrices (the vocabulary
-// head) run many short blocks of 4 slices x 2 tiles.  The split depends on the matrix shape
-// alone, never on M.
-// Weights stream through a three-chunk register ring (half supersteps), two chunks ahead of the
-// MFMAs, and the token rows are loaded before the first weight chunk.  Slices are added in slice order through LDS, so a token's
-// result does not depend on M, on its index or on timing (greedy output is then byte-identical
-// with and without speculative drafting).
+// K is cut into KS equal slices of supersteps.  Chunk-major matrices (packing.h) run one block per
+// CU (at most 256 blocks, one resident per CU): block b owns the consecutive tiles
+// [b*base + min(b, extra), +base + (b < extra)), its streaming wave w the item (tile w / KS,
+// slice w % KS), so every active wave streams the same bytes and every CU the same number of
+// waves' worth (a block with one tile fewer leaves KS waves idle), and pack_stage_waves(K) more
+// waves stage the token rows.  Taller matrices (the vocabulary head) run many short blocks of 4
+// slices x 2 tiles whose waves do both.  The split depends on the matrix shape alone, never on M.
+// Weights stream through a three-chunk register ring (half supersteps).  Slices are added in
+// slice order through LDS, so a token's result does not depend on M, on its index or on timing
+// (greedy output is then byte-identical with and without speculative drafting).
 //
-// Prologue (fused branch input, layers.wgsl:46-73 and :94-126): the staged rows are the plain x
-// rows, RMSNorm(x0)*(1+w), or, inside the mHC range, RMSNorm(pre0*x0 + pre1*x1)*(1+w) with the
-// token coefficients left by the router kernel.
+// Branch input (layers.wgsl:46-73 and :94-126): the plain x rows, RMSNorm(x0)*(1+w), or, inside
+// the mHC range, RMSNorm(pre0*x0 + pre1*x1)*(1+w) with pre from this site's router sums, whose
+// block partials the producing GEMV left; the 1/rms factor is applied to the dot products.
 //
 // Epilogues: plain store; residual add into stream 0 (merge mode 0, layers.wgsl:142-145); mHC
 // merge (modes 1/2, layers.wgsl:150-161); SwiGLU (layers.wgsl:164-175).
@@ -583,15 +583,33 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             float2 mm[P];                        // its power-of-two multipliers, token 0 and 1 of each pair
 #pragma unroll
             for (int p = 0; p < P; ++p) mm[p] = *reinterpret_cast<const float2*>(mult_s + (p * nss + S) * 2);
-#pragma unroll
-            for (int i0 = 0; i0 < CL; ++i0) {
+            // the chunk's A fragments first: all LDS reads in flight together instead of one
+            // read-wait-MFMA round trip per fragment (one token pair: two would not fit the
+            // registers, and they read each fragment next to its MFMA)
+            constexpr bool kAhead = P == 1;
+            half8_t av[CL][NM][P];
+            auto read_a = [&](int i0) {
                 const int v = (q % CPS) * CL + i0;                              // load within the superstep
                 const int blk = S * 4 * U + U * g + (QT == 0 ? (v >> 1) : v);  // quant block of this load
                 const int eoff = QT == 0 ? (v & 1) * 16 : 0;                  // first element in the block
-                int abase[P];
 #pragma unroll
-                for (int p = 0; p < P; ++p)
-                    abase[p] = a_on ? ((p * nb + blk) * 4 + combo) * 64 + eoff * 2 : zero_off;
+                for (int p = 0; p < P; ++p) {
+                    const int abase = a_on ? ((p * nb + blk) * 4 + combo) * 64 + eoff * 2 : zero_off;
+#pragma unroll
+                    for (int i = 0; i < NM; ++i)
+                        av[i0][i][p] = *reinterpret_cast<const half8_t*>(lds + abase + (a_on ? 16 * i : 0));
+                }
+            };
+            if constexpr (kAhead) {
+#pragma unroll
+                for (int i0 = 0; i0 < CL; ++i0) read_a(i0);
+                // keep the reads ahead, and each load's dequantisation next to its own MFMAs (so
+                // the converted weights of only one load are live while the fragments are in flight)
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int i0 = 0; i0 < CL; ++i0) {
+                if constexpr (!kAhead) read_a(i0);
                 f32x4_t d[P];
 #pragma unroll
                 for (int p = 0; p < P; ++p) d[p] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -599,10 +617,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                 for (int i = 0; i < NM; ++i) {
                     const half8_t b = dequant8<QT>(w[i0], i);
 #pragma unroll
-                    for (int p = 0; p < P; ++p) {
-                        const half8_t av = *reinterpret_cast<const half8_t*>(lds + abase[p] + (a_on ? 16 * i : 0));
-                        d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, d[p], 0, 0, 0);
-                    }
+                    for (int p = 0; p < P; ++p) d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i0][i][p], b, d[p], 0, 0, 0);
                 }
                 const float scale = sc[QT == 0 ? (i0 >> 1) : i0];
 #pragma unroll
@@ -614,6 +629,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                     acc[p][2] = fmaf(sm1, d[p][2], acc[p][2]);
                     acc[p][3] = fmaf(sm1, d[p][3], acc[p][3]);
                 }
+                if constexpr (kAhead) __builtin_amdgcn_sched_barrier(0);
             }
         };
 
