@@ -6,7 +6,10 @@ weights drawn on the device, batch 1, a 1024-token random prompt, then greedy MT
 
 A step is one speculative decode step: MTP draft + 2-token verify through the weights + greedy
 acceptance (rollback on reject).  W untimed warmup steps, then exactly K timed steps between two
-device synchronisations; value = tokens emitted in those K steps / their wall time.
+device synchronisations; value = tokens emitted in those K steps / their wall time.  The steps run
+through the decoder's native multi-step call (snl_decoder_steps, 100 steps a call): each step is
+queued on the device, its records written there by the previous step's accept decision, before
+the host reads the previous step's outcome.
 
 roofline: the dominant kernel is the verify pass's gate_up GEMV (Q8_0, M=2, N=24576, K=4096 with
 the fused mHC/RMSNorm prologue and SwiGLU epilogue, 43% of the pass's weight bytes).  After the
@@ -468,16 +471,16 @@ def main() -> int:
     prefill_s = time.perf_counter() - t0
     log(f"prefill of {PROMPT} tokens (+ MTP catch-up) in {prefill_s:.3f}s")
 
-    for _ in range(args.warmup):
-        dec.step()
+    dec.steps(args.warmup)
     st0 = dec.stats()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     emitted = 0
-    for i in range(args.steps):
-        emitted += len(dec.step())
-        if (i + 1) % 100 == 0:
-            log(f"step {i + 1}/{args.steps}")
+    # native loop: each step queued on the device before the previous one is read
+    for i0 in range(0, args.steps, 100):
+        k = min(100, args.steps - i0)
+        emitted += len(dec.steps(k))
+        log(f"step {i0 + k}/{args.steps}")
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     st1 = dec.stats()

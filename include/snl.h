@@ -142,6 +142,9 @@ int snl_prefill_chunk(const snl_engine* e);
 
 /* ---- the greedy MTP decode loop (src/worker.rs:123-255) ---------------------------------- */
 
+/* prefill_s, decode_s: host wall time of the prompt and of the decode steps.  draft_s, verify_s:
+   the greedy decode's device time in the MTP draft passes and in the 2-token verify passes
+   (stream events around each pass; the two passes of a step are launched together). */
 typedef struct snl_gen_stats {
     int32_t generated, drafted, accepted, _pad;
     double prefill_s, decode_s, draft_s, verify_s;
@@ -163,6 +166,12 @@ int snl_generate(snl_engine* e, const uint32_t* prompt, int n, int max_tokens, i
 typedef struct snl_decoder snl_decoder;
 int snl_decoder_create(snl_engine* e, const uint32_t* prompt, int n, int spec, snl_decoder** out);
 int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out);
+/* `steps` calls of snl_decoder_step in one native loop (no counterpart in the reference, whose
+ * loop stops at an EOS id): with speculation each step is queued on the device before the host
+ * waits for the one before it, the step's records being written on the device from the previous
+ * step's outcome.  Every queued step has completed when it returns.  out / gaps (nullable) hold
+ * 2 * steps entries; *n_out receives the number of emitted tokens. */
+int snl_decoder_steps(snl_decoder* d, int steps, uint32_t* out, float* gaps, int* n_out);
 int snl_decoder_stats(const snl_decoder* d, snl_gen_stats* out);
 void snl_decoder_destroy(snl_decoder* d);
 

@@ -92,19 +92,11 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) mine[m] = pos0 + m >= kstart && pos0 + m < kstart + kPart;
 
-    // ---- loads: the part's values (for the LDS tile), this wave's keys (both straight from the
-    // cache, which the rows of this call's positions patch below), then this call's rows ----
+    // ---- loads: this call's rows, then the part's values (for the LDS tile) and this wave's keys
+    // (both straight from the cache, which the rows of this call's positions patch below) ----
     const unsigned row_bytes = (unsigned)kv_dim * 2;
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.kcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.vcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
-    u32x4_t vv[kPart / 8];
-#pragma unroll
-    for (int i = 0; i < kPart / 8; ++i)  // thread: keys tid / 32 + 8i, 16-byte segment tid % 32
-        vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((tid >> 5) + 8 * i) * (int)row_bytes + kh * HD * 2 + (tid & 31) * 16, 0, 0);
-    u32x4_t kf[HD / 32];
-#pragma unroll
-    for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
-        kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
     // attention.wgsl:59-127 for the group's 4 query heads and this part's new key / value rows:
     // thread d holds dim d of each row
     const int d = tid;
@@ -131,6 +123,16 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
             rsn[m] = t.y;
         }
     }
+    // then the cache loads: vector loads complete in issue order, so the waits for this call's rows
+    // above do not include them (issued first, they held the row prep back ~1 us)
+    u32x4_t vv[kPart / 8];
+#pragma unroll
+    for (int i = 0; i < kPart / 8; ++i)  // thread: keys tid / 32 + 8i, 16-byte segment tid % 32
+        vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((tid >> 5) + 8 * i) * (int)row_bytes + kh * HD * 2 + (tid & 31) * 16, 0, 0);
+    u32x4_t kf[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
+        kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
     // RMSNorm (1 + w) over each row's 256 dims: wave sums, then the 4 waves in order
     float ss[NS];
 #pragma unroll

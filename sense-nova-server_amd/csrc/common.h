@@ -29,7 +29,9 @@ struct StepDev {
     int32_t s_out;  // recurrent-state slot written after the last row
     int32_t s_ck;   // recurrent-state slot written after row ckpt-1
     int32_t r0;     // MTP: first row of `hid` paired with tokens[0]
-    int32_t x_off;  // LM head: first row of `hid` whose logits are produced
+    int32_t x_off;  // MTP draft head: the row whose logits give the draft
+    uint32_t draft_rows;  // bit m set: row m's token is the MTP draft's pick on the device, not tokens[m]
+    uint32_t seq;         // speculative step number (the outcome ring's index)
     uint32_t tokens[SNL_MAX_M];
     uint32_t rpos[SNL_MAX_M][4];  // rotary (t, h, w, 0) position of each row
     // cos and sin of each row's rotary angles (attention.wgsl:90-110), formed on the host with

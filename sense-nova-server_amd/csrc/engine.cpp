@@ -56,6 +56,7 @@ constexpr int kLogitRows = 2;
 constexpr int kDistMax = 1024;  // largest k the device top-k serves (SNL_DIST_MAX)
 // Token rows per captured pass.  The kernels take up to SNL_MAX_M; passes use 1 or 2.
 constexpr int kMaxM = 2;
+constexpr int kSpecRing = 4;  // speculative step outcomes held in pinned memory
 
 // Tensor kinds of the seeded initialiser: stream id = ((layer + 1) << 8) | kind for layer
 // tensors (layer 0xFFF is the MTP head), kind alone for the globals.
@@ -191,8 +192,19 @@ struct snl_engine {
     float *snap_lin[kSnapshots] = {}, *snap_conv[kSnapshots] = {}, *snap_h[kSnapshots] = {};
     float* pick_scratch = nullptr;
     Pick *d_picks = nullptr, *d_mpick = nullptr;
-    Pick* h_picks = nullptr;  // pinned, 3 entries: 2 forward rows + 1 draft
-    StepDev *d_step = nullptr, *d_mstep = nullptr, *h_step = nullptr;  // h_step: pinned, 2 records
+    Pick* h_picks = nullptr;  // pinned, 3 entries: 2 forward rows + 1 draft, written by the pick kernels
+    Pick* hd_picks = nullptr;  // the device's address of h_picks
+    // speculative steps (run kind 2): two graph instances (parity), each with its events before
+    // the draft, between the passes and after the verify; the outcome ring in pinned memory; the
+    // rotary cos / sin of every text position
+    hipEvent_t spec_ev[2][3] = {};
+    SpecOut* h_ring = nullptr;   // pinned, kSpecRing entries
+    SpecOut* hd_ring = nullptr;  // its device address
+    uint32_t spec_seq = 0;       // number of the next speculative step
+    float* rope_tab = nullptr;   // [rope_rows][SNL_ROPE_MAX][2]
+    int rope_rows = 0;
+    // h_step: pinned, 2 records (forward, MTP); d_step / d_mstep: their device copies, adjacent
+    StepDev *d_step = nullptr, *d_mstep = nullptr, *h_step = nullptr;
 
     int cur = 0, ck_slot = -1;
     int pos = 0, hid_rows = 0;
@@ -422,7 +434,10 @@ struct snl_engine {
         return launch_mhc(pf_x, w, pf_part, h, M, stream) |
                launch_mhc_coef(pf_part, w, h, cfg.mhc_iterations, pf_coef, M, stream);
     }
-    int run(int kind, int M, int a, int b);
+    int run(int kind, int M, int a, int b, bool upload = true);
+    // the speculative step's graph (run kind 2): the MTP draft over M pairs, then the checkpointed
+    // 2-row verify whose second token is the draft's pick, with event records around both passes
+    int build_spec(int M, int parity, hipGraphExec_t* out);
     static constexpr int kPartBlocks = 4096;  // partial-sum slots of mhc_part per token
     int part_n = 0;                           // partials currently in mhc_part (0: none)
     // GEMV with an optional fused branch-input prologue (pro: GEMV_NORM with norm weights nw, or
@@ -618,8 +633,9 @@ int snl_engine::init() {
         (rc = dalloc(&hlast, (size_t)h)) || (rc = dalloc(&mx, (size_t)M * 2 * h)) ||
         (rc = dalloc(&hn, (size_t)M * h)) || (rc = dalloc(&m_logits, (size_t)c.vocab)) ||
         (rc = dalloc(&pick_scratch, pick_scratch_floats(c.vocab, kLogitRows))) || (rc = dalloc(&d_picks, 2)) ||
-        (rc = dalloc(&d_mpick, 1)) || (rc = dalloc(&d_step, 1)) || (rc = dalloc(&d_mstep, 1)))
+        (rc = dalloc(&d_mpick, 1)) || (rc = dalloc(&d_step, 2)))
         return rc;
+    d_mstep = d_step + 1;
     // ---- sampler scratch ----
     if ((rc = dalloc(&topk_keys, topk_scratch_keys(c.vocab, kDistMax))) || (rc = dalloc(&pen_dev, (size_t)2 * c.vocab)))
         return rc;
@@ -664,6 +680,30 @@ int snl_engine::init() {
     if (hipHostMalloc((void**)&h_picks, 3 * sizeof(Pick), hipHostMallocDefault) != hipSuccess ||
         hipHostMalloc((void**)&h_step, 2 * sizeof(StepDev), hipHostMallocDefault) != hipSuccess)
         return fail(SNL_ENOMEM, "pinned host allocation failed");
+    if (hipHostGetDevicePointer((void**)&hd_picks, h_picks, 0) != hipSuccess || !hd_picks)
+        return fail(SNL_EDEVICE, "no device address for the pinned picks");
+    memset(h_picks, 0, 3 * sizeof(Pick));
+    if (hipHostMalloc((void**)&h_ring, kSpecRing * sizeof(SpecOut), hipHostMallocDefault) != hipSuccess)
+        return fail(SNL_ENOMEM, "pinned host allocation failed");
+    if (hipHostGetDevicePointer((void**)&hd_ring, h_ring, 0) != hipSuccess || !hd_ring)
+        return fail(SNL_EDEVICE, "no device address for the pinned step ring");
+    memset(h_ring, 0, kSpecRing * sizeof(SpecOut));
+    // rotary cos / sin of every text position (all three rotary components equal), as step_rope
+    // forms them, for the records the speculative step's control kernel writes
+    {
+        rope_rows = ctx + 4;
+        std::vector<float> tab((size_t)rope_rows * SNL_ROPE_MAX * 2, 0.0f);
+        StepDev tmp;
+        for (int p = 0; p < rope_rows; ++p) {
+            memset(&tmp, 0, sizeof tmp);
+            for (int k = 0; k < 3; ++k) tmp.rpos[0][k] = (uint32_t)p;
+            step_rope(tmp, 1, c.rope_theta, c.rot_dim, c.mrope_section);
+            memcpy(tab.data() + (size_t)p * SNL_ROPE_MAX * 2, tmp.rope[0], SNL_ROPE_MAX * 2 * sizeof(float));
+        }
+        if ((rc = dalloc(&rope_tab, tab.size()))) return rc;
+        if (hipMemcpy(rope_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+            return fail(SNL_EDEVICE, "rotary table upload failed");
+    }
     // zero everything a pass may read before writing (the reference's buffers start zeroed)
     if (hipMemsetAsync(x, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
         hipMemsetAsync(mx, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
@@ -688,7 +728,7 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
     int rc = 0;
     // the same launch copies hlast into hid row 0 (the hidden of the token before this step)
     if (op("embed", 0.0))
-        rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream, hlast, hid);
+        rc |= launch_embed(d_step, (const int8_t*)embed.q, embed.s, c.vocab, h, x, M, stream, hlast, hid, d_mpick);
     int fslot = 0, lslot = 0;
     const size_t kvn = (size_t)ctx * kv_dim;
     const size_t nl = std::max(n_lin, 1);
@@ -765,7 +805,7 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
     rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M, hlast);
     if (rows > 0) {
         rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
-        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
+        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream, hd_picks);
     }
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
@@ -788,10 +828,10 @@ int snl_engine::record_mtp(int M, int draft) {
                m_post_ln.p);
     rc |= gemv("gemv_mtp_down", m_down, act, c.intermediate, mx, 2 * h, M, GEMV_ADD);
     if (draft) {
-        // final norm of the last pair fused into the LM head
-        rc |= gemv("gemv_lm_head", lm_head, mx + (size_t)(M - 1) * 2 * h, 2 * h, m_logits, c.vocab, 1, GEMV_STORE, 0,
-                   GEMV_NORM, m_norm.p);
-        if (op("pick", 0.0)) rc |= launch_pick(m_logits, c.vocab, 1, pick_scratch, d_mpick, stream);
+        // final norm of the draft's pair (the record's x_off: the last real one) fused into the LM head
+        rc |= gemv("gemv_lm_head", lm_head, mx, 2 * h, m_logits, c.vocab, 1, GEMV_STORE, 0, GEMV_NORM, m_norm.p,
+                   &d_mstep->x_off);
+        if (op("pick", 0.0)) rc |= launch_pick(m_logits, c.vocab, 1, pick_scratch, d_mpick, stream, hd_picks + 2);
     }
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
@@ -864,7 +904,7 @@ int snl_engine::record_prefill(int M, int rows) {
     rc |= norm(pf_x, X2, nullptr, 0, final_norm.p, hid + h, 0, M);
     if (rows > 0) {
         rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
-        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream);
+        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream, hd_picks);
     }
     if (op("copy", 0.0)) rc |= launch_copy(hlast, hid + (size_t)M * h, h, stream);
     mark("end", 0.0);
@@ -921,13 +961,22 @@ int snl_engine::prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int 
 
 // Replay (capturing on first use) the pass (kind, M, a, b): kind 0 forward (a = rows,
 // b = ckpt), kind 1 MTP (a = draft).  The step record is copied first.
-int snl_engine::run(int kind, int M, int a, int b) {
-    StepDev* hs = h_step + kind;
-    if (hipMemcpyAsync(kind == 0 ? d_step : d_mstep, hs, sizeof(StepDev), hipMemcpyHostToDevice, stream) !=
-        hipSuccess)
+// Replays the captured pass of `kind` (0: forward of M rows, a logit rows, checkpoint b; 1: MTP
+// head over M pairs, draft a; 2: a greedy speculative step, the MTP draft over M pairs then the
+// checkpointed 2-row verify) after uploading its step records.
+int snl_engine::run(int kind, int M, int a, int b, bool upload) {
+    const int first = kind == 1 ? 1 : 0, count = kind == 2 ? 2 : 1;
+    if (upload &&
+        hipMemcpyAsync(d_step + first, h_step + first, count * sizeof(StepDev), hipMemcpyHostToDevice, stream) !=
+            hipSuccess)
         return fail(SNL_EDEVICE, "step upload failed");
     auto key = std::make_tuple(kind, M, a, b);
     auto it = graphs.find(key);
+    if (it == graphs.end() && kind == 2) {
+        hipGraphExec_t ex = nullptr;
+        if (int rc = build_spec(M, a, &ex)) return rc;
+        it = graphs.emplace(key, ex).first;
+    }
     if (it == graphs.end()) {
         hipGraph_t g = nullptr;
         if (hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
@@ -936,7 +985,8 @@ int snl_engine::run(int kind, int M, int a, int b) {
         hipError_t ce = hipStreamEndCapture(stream, &g);
         if (rc || ce != hipSuccess) {
             if (g) hipGraphDestroy(g);
-            return fail(SNL_EDEVICE, "pass capture failed (kind %d, M %d)", kind, M);
+            return fail(SNL_EDEVICE, "pass capture failed (kind %d, M %d): %s", kind, M,
+                        rc ? (err.empty() ? "a launch failed" : err.c_str()) : hipGetErrorString(ce));
         }
         hipGraphExec_t ex = nullptr;
         hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
@@ -946,6 +996,59 @@ int snl_engine::run(int kind, int M, int a, int b) {
     }
     if (hipGraphLaunch(it->second, stream) != hipSuccess) return fail(SNL_EDEVICE, "hipGraphLaunch failed");
     return SNL_OK;
+}
+
+// The two passes are captured on their own, then joined in a parent graph between event record
+// nodes (an event recorded inside a stream capture was refused here).
+int snl_engine::build_spec(int M, int parity, hipGraphExec_t* out) {
+    hipGraph_t ga = nullptr, gb = nullptr, pg = nullptr;
+    auto capture = [&](hipGraph_t* g, bool draft) -> int {
+        if (const hipError_t be = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal); be != hipSuccess) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            hipStreamIsCapturing(stream, &cs);
+            return fail(SNL_EDEVICE, "hipStreamBeginCapture failed (%s pass): %s, capture status %d",
+                        draft ? "draft" : "verify", hipGetErrorString(be), (int)cs);
+        }
+        int rc = draft ? record_mtp(M, 1) : record_forward(2, 2, 1);
+        if (!rc && !draft) {
+            SpecArgs sa{};
+            sa.vstep = d_step;
+            sa.mstep = d_mstep;
+            sa.picks = d_picks;
+            sa.draft = d_mpick;
+            sa.rope_tab = rope_tab;
+            sa.rope_rows = rope_rows;
+            sa.hid1 = hid + h;
+            sa.hlast = hlast;
+            sa.h = h;
+            sa.ring = hd_ring;
+            sa.ring_n = kSpecRing;
+            rc = launch_spec_next(sa, stream);
+        }
+        const hipError_t ce = hipStreamEndCapture(stream, g);
+        if (rc || ce != hipSuccess)
+            return fail(SNL_EDEVICE, "speculative step capture failed (%s pass): %s", draft ? "draft" : "verify",
+                        rc ? "a launch failed" : hipGetErrorString(ce));
+        return SNL_OK;
+    };
+    int rc = capture(&ga, true);
+    if (!rc) rc = capture(&gb, false);
+    hipGraphNode_t n0, na, n1, nb, n2;
+    const char* what = nullptr;
+    if (!rc) {
+        if (hipGraphCreate(&pg, 0) != hipSuccess) what = "hipGraphCreate";
+        else if (hipGraphAddEventRecordNode(&n0, pg, nullptr, 0, spec_ev[parity][0]) != hipSuccess) what = "event node";
+        else if (hipGraphAddChildGraphNode(&na, pg, &n0, 1, ga) != hipSuccess) what = "draft node";
+        else if (hipGraphAddEventRecordNode(&n1, pg, &na, 1, spec_ev[parity][1]) != hipSuccess) what = "event node";
+        else if (hipGraphAddChildGraphNode(&nb, pg, &n1, 1, gb) != hipSuccess) what = "verify node";
+        else if (hipGraphAddEventRecordNode(&n2, pg, &nb, 1, spec_ev[parity][2]) != hipSuccess) what = "event node";
+        else if (hipGraphInstantiate(out, pg, nullptr, nullptr, 0) != hipSuccess) what = "hipGraphInstantiate";
+        if (what) rc = fail(SNL_EDEVICE, "speculative step graph: %s failed", what);
+    }
+    if (pg) hipGraphDestroy(pg);
+    if (gb) hipGraphDestroy(gb);
+    if (ga) hipGraphDestroy(ga);
+    return rc;
 }
 
 extern "C" {
@@ -1148,6 +1251,10 @@ void snl_engine_destroy(snl_engine* e) {
     for (auto& kv : e->graphs) hipGraphExecDestroy(kv.second);
     e->free_gen_tmp();
     for (void* p : e->allocs) hipFree(p);
+    for (auto& evs : e->spec_ev)
+        for (hipEvent_t ev : evs)
+            if (ev) hipEventDestroy(ev);
+    if (e->h_ring) hipHostFree(e->h_ring);
     if (e->h_picks) hipHostFree(e->h_picks);
     if (e->h_step) hipHostFree(e->h_step);
     if (e->h_pstep) hipHostFree(e->h_pstep);
@@ -1227,9 +1334,8 @@ int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* po
         if (logits_out &&
             hipMemcpy(logits_out, e->logits, sizeof(float) * rows * e->cfg.vocab, hipMemcpyDeviceToHost) != hipSuccess)
             return e->fail(SNL_EDEVICE, "logits readback failed");
-        if (picks_out &&
-            hipMemcpy(picks_out, e->d_picks, sizeof(snl_pick) * rows, hipMemcpyDeviceToHost) != hipSuccess)
-            return e->fail(SNL_EDEVICE, "pick readback failed");
+        // the pick kernel also wrote them to pinned host memory, complete once the stream synchronised
+        if (picks_out) memcpy(picks_out, e->h_picks, sizeof(snl_pick) * rows);
     }
     return SNL_OK;
 }
@@ -1370,6 +1476,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
         st.pos0 = slot0 + c0;
         st.m = m;
         st.r0 = r0 + c0;
+        st.x_off = m - 1;
         for (int i = 0; i < m; ++i) {
             st.tokens[i] = tokens[c0 + i];
             for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3[(c0 + i) * 3 + k];
@@ -1380,8 +1487,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
         if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "mtp failed on device");
     }
     if (draft) {
-        if (hipMemcpy(e->h_picks + 2, e->d_mpick, sizeof(Pick), hipMemcpyDeviceToHost) != hipSuccess)
-            return e->fail(SNL_EDEVICE, "draft readback failed");
+        // written to pinned host memory by the pick kernel of the synchronised pass
         if (draft_out) *draft_out = e->h_picks[2].token;
         if (pick_out) memcpy(pick_out, e->h_picks + 2, sizeof(snl_pick));
         if (logits_out &&
@@ -1465,6 +1571,121 @@ uint64_t engine_epoch(const snl_engine* e) { return e->epoch; }
 int engine_fail(snl_engine* e, int code, const char* msg) { return e->fail(code, "%s", msg); }
 
 int engine_vocab(const snl_engine* e) { return e->cfg.vocab; }
+
+// Greedy speculative steps (src/worker.rs:197-255).  A step is the MTP draft (Engine::mtp with a
+// draft, src/engine.rs:736-774) over one or two pairs from hidden row r0 at cache slot slot0, then
+// the checkpointed 2-token verify of [tok, draft] (src/engine.rs:801-936), whose second token the
+// embedding reads from the draft's pick on the device, then spec_next_kernel, which takes the accept
+// decision, copies the rollback's carried row on a reject, posts the outcome to the pinned ring and
+// writes both records of the next step.  The three replay as one graph (two instances, so that one
+// step can be queued while the previous one runs).  The draft pass always has two rows: with one
+// pair the second is a padding row at the next position, whose cache entry the next draft
+// overwrites before any pass reads it; the draft comes from the record's row x_off.
+
+// The records of a step from the host's decode state (draft pairs mtok / mpos, verify token tok
+// at rotary positions pos3).
+int spec_prepare(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint32_t* mpos, int slot0, uint32_t tok,
+                 const uint32_t* pos3) {
+    e->err.clear();
+    if (!e->cfg.has_mtp) return e->fail(SNL_ESTATE, "this model has no MTP head");
+    if (mn < 1 || mn > kMaxM || !mtok || !mpos || !pos3 || r0 < 0 || r0 + mn > e->hid_rows + 1 || slot0 < 0 ||
+        slot0 + kMaxM > e->ctx)
+        return e->fail(SNL_EARG, "mtp: rows out of range");
+    for (int i = 0; i < mn; ++i)
+        if (mtok[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", mtok[i]);
+    if (tok >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tok);
+    if (e->pos + 2 > e->ctx) return e->fail(SNL_ECTX, "context length exceeded (%d > %d)", e->pos + 2, e->ctx);
+    StepDev& ms = e->h_step[1];
+    memset(&ms, 0, sizeof ms);
+    ms.pos0 = slot0;
+    ms.m = kMaxM;
+    ms.r0 = r0;
+    ms.x_off = mn - 1;
+    for (int i = 0; i < kMaxM; ++i) {
+        ms.tokens[i] = mtok[i < mn ? i : 0];
+        for (int k = 0; k < 3; ++k) ms.rpos[i][k] = i < mn ? mpos[i * 3 + k] : mpos[k] + (uint32_t)i;
+    }
+    step_rope(ms, kMaxM, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
+    StepDev& vs = e->h_step[0];
+    memset(&vs, 0, sizeof vs);
+    vs.pos0 = e->pos;
+    vs.m = 2;
+    vs.ckpt = 1;
+    vs.s_in = e->cur;
+    vs.s_ck = (e->cur + 1) % 3;
+    vs.s_out = (e->cur + 2) % 3;
+    vs.draft_rows = 2u;
+    vs.seq = e->spec_seq;
+    vs.tokens[0] = tok;
+    for (int i = 0; i < 2; ++i)
+        for (int k = 0; k < 3; ++k) vs.rpos[i][k] = pos3[i * 3 + k];
+    step_rope(vs, 2, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
+    return SNL_OK;
+}
+
+// Queues step `seq` (instance seq & 1): with upload, from the records spec_prepare wrote; without,
+// from the records the previous step's control kernel left on the device.
+int spec_launch(snl_engine* e, bool upload) {
+    for (auto& evs : e->spec_ev)
+        for (hipEvent_t& ev : evs)
+            if (!ev && hipEventCreate(&ev) != hipSuccess) return e->fail(SNL_EDEVICE, "event creation failed");
+    const int parity = (int)(e->spec_seq & 1u);
+    if (int rc = e->run(2, kMaxM, parity, 0, upload)) return rc;
+    ++e->spec_seq;
+    return SNL_OK;
+}
+
+// Waits for step seq and applies it to the engine's host state: the verify's slots and position,
+// then the rollback on a reject (whose carried row the control kernel copied).
+int spec_finish(snl_engine* e, uint32_t seq, SpecOut* out, float* draft_ms, float* verify_ms) {
+    hipEvent_t* ev = e->spec_ev[seq & 1u];
+    if (hipEventSynchronize(ev[2]) != hipSuccess) return e->fail(SNL_EDEVICE, "speculative step failed on device");
+    const SpecOut o = e->h_ring[seq % kSpecRing];
+    if (o.seq != seq) return e->fail(SNL_EDEVICE, "speculative step %u: outcome of step %u in the ring", seq, o.seq);
+    ++e->epoch;
+    e->ck_slot = (e->cur + 1) % 3;
+    e->cur = (e->cur + 2) % 3;
+    e->pos += 2;
+    e->hid_rows = 2;
+    e->logit_rows = 2;
+    if (!o.accepted) {
+        e->cur = e->ck_slot;
+        e->ck_slot = -1;
+        e->pos -= 1;
+        e->hid_rows = 1;
+    }
+    if (out) *out = o;
+    // (timing is informative only: a failed query reports zero and clears the error state)
+    float t0 = 0.0f, t1 = 0.0f;
+    if (hipEventElapsedTime(&t0, ev[0], ev[1]) != hipSuccess || hipEventElapsedTime(&t1, ev[1], ev[2]) != hipSuccess) {
+        (void)hipGetLastError();
+        t0 = t1 = 0.0f;
+    }
+    if (draft_ms) *draft_ms = t0;
+    if (verify_ms) *verify_ms = t1;
+    return SNL_OK;
+}
+
+// One step from the host's decode state, waited for.
+int engine_spec_step(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint32_t* mpos, int slot0,
+                     uint32_t tok, const uint32_t* pos3, SpecOut* out, float* draft_ms, float* verify_ms) {
+    if (int rc = spec_prepare(e, r0, mtok, mn, mpos, slot0, tok, pos3)) return rc;
+    const uint32_t seq = e->spec_seq;
+    if (int rc = spec_launch(e, true)) return rc;
+    return spec_finish(e, seq, out, draft_ms, verify_ms);
+}
+
+// Steps queued ahead of the host: step seq + 1 from the device's records while step seq runs.
+// Queues it when its verify stays inside the context whatever step seq decides.
+int engine_spec_ahead(snl_engine* e, bool* queued) {
+    *queued = false;
+    if (e->pos + 4 > e->ctx) return SNL_OK;
+    if (int rc = spec_launch(e, false)) return rc;
+    *queued = true;
+    return SNL_OK;
+}
+
+uint32_t engine_spec_seq(const snl_engine* e) { return e->spec_seq; }
 
 // Penalties on logits row `row` of the last forward (in place, as the reference mutates its logits),
 // then its k largest entries (value descending, index ascending on ties): k <= kDistMax on the

@@ -102,8 +102,11 @@ int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s);
 // ---------------------------------------------------------------- layers (layers.hip)
 // x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790); with carry_src, one
 // more block copies h floats from carry_src to carry_dst in the same launch
+struct Pick;
+// draft: the MTP draft's pick, the token of the rows step->draft_rows names
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
-                 hipStream_t s, const float* carry_src = nullptr, float* carry_dst = nullptr);
+                 hipStream_t s, const float* carry_src = nullptr, float* carry_dst = nullptr,
+                 const Pick* draft = nullptr);
 
 // out[r] = rmsnorm(branch input of row first+r) * (one + w) for r < count (layers.wgsl:46-73).
 // mode 1 mixes the two streams with coef[row][0..1].  Row `row` of x starts at
@@ -144,7 +147,32 @@ struct Pick {
     float top2;
     uint32_t _pad;
 };
-int launch_pick(const float* logits, int V, int rows, float* scratch, Pick* out, hipStream_t s);
+// One greedy speculative step's outcome, posted to pinned host memory by spec_next.
+struct SpecOut {
+    uint32_t seq, draft, accepted, _pad;
+    Pick picks[2];
+};
+// After a speculative step's verify (src/worker.rs:236-255, greedy): accept when the verify's first
+// pick equals the draft; on a reject, hlast <- hid row 1 (the rollback's carried row).  Rewrites the
+// verify record vstep and the draft record mstep for the next step (positions advanced by 2 or 1,
+// the state slots switched, rotary cos / sin from rope_tab) and posts the outcome to ring[seq % ring_n].
+struct SpecArgs {
+    StepDev* vstep;
+    StepDev* mstep;
+    const Pick* picks;     // the verify's 2 picks
+    const Pick* draft;     // the draft's pick
+    const float* rope_tab; // [rope_rows][SNL_ROPE_MAX][2]: cos / sin of text position p
+    int rope_rows;
+    const float* hid1;     // hid row 1
+    float* hlast;
+    int h;
+    SpecOut* ring;         // pinned host memory (device address)
+    int ring_n;
+};
+int launch_spec_next(const SpecArgs& a, hipStream_t s);
+// host_out: pinned host memory (its device address) that also receives the picks
+int launch_pick(const float* logits, int V, int rows, float* scratch, Pick* out, hipStream_t s,
+                Pick* host_out = nullptr);
 size_t pick_scratch_floats(int V, int rows);
 
 int launch_copy(float* dst, const float* src, size_t n, hipStream_t s);

@@ -17,14 +17,15 @@ namespace {
 __global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const int8_t* __restrict__ eq,
                                                      const float* __restrict__ es, int vocab, int h,
                                                      float* __restrict__ x, int M, const float* carry_src,
-                                                     float* carry_dst) {
+                                                     float* carry_dst, const Pick* draft) {
     const int m = blockIdx.x;
     if (m == M) {  // the carried row (launched only with carry_src)
         for (int i = threadIdx.x; i * 4 < h; i += 256)
             reinterpret_cast<float4*>(carry_dst)[i] = reinterpret_cast<const float4*>(carry_src)[i];
         return;
     }
-    uint32_t tok = step->tokens[m];
+    // a verify pass launched right behind the MTP draft takes the draft's token from its pick
+    uint32_t tok = draft && ((step->draft_rows >> m) & 1u) ? draft->token : step->tokens[m];
     if (tok >= (uint32_t)vocab) tok = 0;  // the host rejects out-of-range ids before launching
     const int8_t* q = eq + (size_t)tok * h;
     const float* s = es + (size_t)tok * (h / 32);
@@ -287,7 +288,7 @@ __global__ __launch_bounds__(256) void pick_partial_kernel(const float* logits, 
     }
 }
 
-__global__ __launch_bounds__(256) void pick_final_kernel(const float* scratch, int nblk, Pick* out) {
+__global__ __launch_bounds__(256) void pick_final_kernel(const float* scratch, int nblk, Pick* out, Pick* host_out) {
     const int row = blockIdx.x;
     Top2 t = {-FLT_MAX, 0xFFFFFFFFu, -FLT_MAX};
     for (int b = threadIdx.x; b < nblk; b += 256) {
@@ -296,11 +297,90 @@ __global__ __launch_bounds__(256) void pick_final_kernel(const float* scratch, i
     }
     t = top2_block(t);
     if (threadIdx.x == 0) {
-        out[row].token = t.i1 == 0xFFFFFFFFu ? 0u : t.i1;
-        out[row].top1 = t.v1;
-        out[row].top2 = t.v2;
-        out[row]._pad = 0;
+        const Pick r = {t.i1 == 0xFFFFFFFFu ? 0u : t.i1, t.v1, t.v2, 0u};
+        out[row] = r;
+        if (host_out) {  // pinned host memory: the host reads it after the stream synchronises
+            host_out[row] = r;
+            __threadfence_system();
+        }
     }
+}
+
+// One block of 256 threads.  Every thread reads what it needs of the two records before the
+// barrier; the records are rewritten after it.
+__global__ __launch_bounds__(256) void spec_next_kernel(SpecArgs a) {
+    const int tid = threadIdx.x;
+    const Pick p0 = a.picks[0], p1 = a.picks[1];
+    const uint32_t d = a.draft->token;
+    const StepDev& v = *a.vstep;
+    const int32_t pos0 = v.pos0, s_ck = v.s_ck, s_out = v.s_out;
+    const uint32_t rope = v.rpos[0][0], tok0 = v.tokens[0], seq = v.seq;
+    (void)tok0;
+    __syncthreads();
+    const bool acc = p0.token == d;
+    const int adv = acc ? 2 : 1;
+    const uint32_t nrope = rope + (uint32_t)adv;
+    auto tab = [&](uint32_t p, int f) {
+        const uint32_t r = p < (uint32_t)a.rope_rows ? p : (uint32_t)a.rope_rows - 1;
+        return *reinterpret_cast<const float2*>(a.rope_tab + ((size_t)r * SNL_ROPE_MAX + f) * 2);
+    };
+    // rotary cos / sin: threads 0-127 the verify's two rows, 128-255 the draft's two rows
+    {
+        const int row = (tid >> 6) & 1, f = tid & 63;
+        if (tid < 128) {
+            const float2 t = tab(nrope + (uint32_t)row, f);
+            a.vstep->rope[row][f][0] = t.x;
+            a.vstep->rope[row][f][1] = t.y;
+        } else {
+            const float2 t = tab(rope + (uint32_t)row, f);
+            a.mstep->rope[row][f][0] = t.x;
+            a.mstep->rope[row][f][1] = t.y;
+        }
+    }
+    if (tid == 0) {
+        StepDev& nv = *a.vstep;
+        nv.pos0 = pos0 + adv;
+        nv.m = 2;
+        nv.ckpt = 1;
+        nv.s_in = acc ? s_out : s_ck;
+        nv.s_ck = (nv.s_in + 1) % 3;
+        nv.s_out = (nv.s_in + 2) % 3;
+        nv.r0 = 0;
+        nv.x_off = 0;
+        nv.draft_rows = 2u;
+        nv.seq = seq + 1;
+        nv.tokens[0] = acc ? p1.token : p0.token;
+        nv.tokens[1] = 0u;
+        for (int i = 0; i < 2; ++i)
+            for (int k = 0; k < 4; ++k) nv.rpos[i][k] = k < 3 ? nrope + (uint32_t)i : 0u;
+        // the next draft: after an accept the pairs (d, p1) at the verify's positions, after a
+        // reject (p0) and a padding row (the same token at the next position), from hidden row 1
+        StepDev& nm = *a.mstep;
+        nm.pos0 = pos0;
+        nm.m = 2;
+        nm.ckpt = 0;
+        nm.s_in = nm.s_ck = nm.s_out = 0;
+        nm.r0 = 1;
+        nm.x_off = acc ? 1 : 0;
+        nm.draft_rows = 0u;
+        nm.seq = 0u;
+        nm.tokens[0] = acc ? d : p0.token;
+        nm.tokens[1] = acc ? p1.token : p0.token;
+        for (int i = 0; i < 2; ++i)
+            for (int k = 0; k < 4; ++k) nm.rpos[i][k] = k < 3 ? rope + (uint32_t)i : 0u;
+        SpecOut o;
+        o.seq = seq;
+        o.draft = d;
+        o.accepted = acc ? 1u : 0u;
+        o._pad = 0u;
+        o.picks[0] = p0;
+        o.picks[1] = p1;
+        a.ring[seq % (uint32_t)a.ring_n] = o;
+    }
+    // the rollback's carried row
+    if (!acc)
+        for (int i = tid; i < a.h; i += 256) a.hlast[i] = a.hid1[i];
+    if (tid == 0) __threadfence_system();
 }
 
 __global__ __launch_bounds__(256) void copy_kernel(float* dst, const float* src, size_t n) {
@@ -313,13 +393,13 @@ inline int last_error() { return hipGetLastError() == hipSuccess ? 0 : -2; }
 }  // namespace
 
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
-                 hipStream_t s, const float* carry_src, float* carry_dst) {
+                 hipStream_t s, const float* carry_src, float* carry_dst, const Pick* draft) {
     if (M < 1 || M > SNL_MAX_M || h % 32 || (reinterpret_cast<uintptr_t>(eq) & 15) ||
         (reinterpret_cast<uintptr_t>(x) & 15) || (carry_src && !carry_dst) ||
         (reinterpret_cast<uintptr_t>(carry_src) & 15) || (reinterpret_cast<uintptr_t>(carry_dst) & 15))
         return -1;
     hipLaunchKernelGGL(embed_kernel, dim3(M + (carry_src ? 1 : 0)), dim3(256), 0, s, step, eq, es, vocab, h, x, M,
-                       carry_src, carry_dst);
+                       carry_src, carry_dst, draft);
     return last_error();
 }
 
@@ -355,11 +435,19 @@ int launch_swiglu(const float* proj, float* act, int inter, int M, hipStream_t s
 
 size_t pick_scratch_floats(int V, int rows) { return (size_t)rows * ((V + kPickChunk - 1) / kPickChunk) * 3; }
 
-int launch_pick(const float* logits, int V, int rows, float* scratch, Pick* out, hipStream_t s) {
+int launch_spec_next(const SpecArgs& a, hipStream_t s) {
+    if (!a.vstep || !a.mstep || !a.picks || !a.draft || !a.rope_tab || a.rope_rows < 1 || !a.hid1 || !a.hlast ||
+        a.h < 1 || !a.ring || a.ring_n < 1)
+        return -1;
+    hipLaunchKernelGGL(spec_next_kernel, dim3(1), dim3(256), 0, s, a);
+    return last_error();
+}
+
+int launch_pick(const float* logits, int V, int rows, float* scratch, Pick* out, hipStream_t s, Pick* host_out) {
     if (rows < 1 || V < 1) return -1;
     const int nblk = (V + kPickChunk - 1) / kPickChunk;
     hipLaunchKernelGGL(pick_partial_kernel, dim3(nblk, rows), dim3(256), 0, s, logits, V, scratch, nblk);
-    hipLaunchKernelGGL(pick_final_kernel, dim3(rows), dim3(256), 0, s, scratch, nblk, out);
+    hipLaunchKernelGGL(pick_final_kernel, dim3(rows), dim3(256), 0, s, scratch, nblk, out, host_out);
     return last_error();
 }
 

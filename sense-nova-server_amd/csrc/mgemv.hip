@@ -94,8 +94,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, un
 }
 
 // Block barrier that orders LDS only: this wave's LDS operations complete before the barrier and
-// vector memory loads stay in flight across it (a full __syncthreads also waits for every
-// outstanding global load, which would drain the weight ring).
+// vector memory loads stay in flight across it.  (A full __syncthreads also orders global memory,
+// so the compiler keeps every global access on its side of it.)
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();

@@ -22,10 +22,19 @@
 #include <vector>
 
 #include "../../include/snl.h"
+#include "kernels.h"
 
 namespace snl {
 uint64_t engine_epoch(const snl_engine* e);
 int engine_fail(snl_engine* e, int code, const char* msg);
+int engine_spec_step(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint32_t* mpos, int slot0,
+                     uint32_t tok, const uint32_t* pos3, SpecOut* out, float* draft_ms, float* verify_ms);
+int engine_spec_ahead(snl_engine* e, bool* queued);
+int spec_prepare(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint32_t* mpos, int slot0, uint32_t tok,
+                 const uint32_t* pos3);
+int spec_launch(snl_engine* e, bool upload);
+int spec_finish(snl_engine* e, uint32_t seq, SpecOut* out, float* draft_ms, float* verify_ms);
+uint32_t engine_spec_seq(const snl_engine* e);
 }  // namespace snl
 
 using clk = std::chrono::steady_clock;
@@ -393,19 +402,65 @@ int snl_decoder_stats(const snl_decoder* d, snl_gen_stats* out) {
     return SNL_OK;
 }
 
+namespace {
+
+// A greedy speculative step's outcome (Sampler::verify, greedy, src/sampler.rs:63-66, :87-89) on the
+// decode state: the draft is emitted when the verify's first pick equals it; the next step's draft
+// pairs and verify token follow (src/worker.rs:236-255).  out / gaps already hold the pending token.
+void spec_apply(snl_decoder* d, const snl::SpecOut& o, float draft_ms, float verify_ms, uint32_t* out, float* gaps,
+                int* n_out) {
+    const uint32_t rope = d->rope;
+    d->st.draft_s += draft_ms * 1e-3;
+    d->st.verify_s += verify_ms * 1e-3;
+    d->st.drafted++;
+    // the verify's position, before this step: the next draft's first cache slot
+    d->mslot = snl_pos(d->e) - (o.accepted ? 2 : 1);
+    d->mr0 = 1;
+    if (o.accepted) {
+        d->st.accepted++;
+        d->st.generated++;
+        out[1] = o.draft;
+        if (gaps) gaps[1] = o.picks[0].top1 - o.picks[0].top2;
+        *n_out = 2;
+        d->tok = o.picks[1].token;
+        d->gap = o.picks[1].top1 - o.picks[1].top2;
+        d->mn = 2;
+        d->mtok[0] = o.draft;
+        d->mtok[1] = d->tok;
+        for (int k = 0; k < 3; ++k) {
+            d->mpos[k] = rope;
+            d->mpos[3 + k] = rope + 1;
+        }
+        d->rope = rope + 2;
+    } else {
+        d->tok = o.picks[0].token;
+        d->gap = o.picks[0].top1 - o.picks[0].top2;
+        d->mn = 1;
+        d->mtok[0] = d->tok;
+        for (int k = 0; k < 3; ++k) d->mpos[k] = rope;
+        d->rope = rope + 1;
+    }
+}
+
+// emit the pending token (Emit::push, src/worker.rs:346-381)
+void emit_pending(snl_decoder* d, uint32_t* out, float* gaps, int* n_out) {
+    out[0] = d->tok;
+    if (gaps) gaps[0] = d->gap;
+    *n_out = 1;
+    d->st.generated++;
+}
+
+}  // namespace
+
 int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out) {
     if (!d || !out || !n_out) return SNL_EARG;
     snl_engine* e = d->e;
     *n_out = 0;
     const auto ts = clk::now();
     int rc;
-    // emit the pending token (Emit::push, src/worker.rs:346-381)
-    out[0] = d->tok;
-    if (gaps) gaps[0] = d->gap;
-    *n_out = 1;
-    d->st.generated++;
-    snl_pick picks[2];
+    emit_pending(d, out, gaps, n_out);
     if (!d->spec) {
+        snl_pick picks[1];
         uint32_t p1[3] = {d->rope, d->rope, d->rope};
         if ((rc = snl_forward(e, &d->tok, 1, p1, 1, 0, nullptr, picks))) return rc;
         d->rope += 1;
@@ -414,50 +469,65 @@ int snl_decoder_step(snl_decoder* d, uint32_t* out, float* gaps, int* n_out) {
         d->st.decode_s += secs(ts, clk::now());
         return SNL_OK;
     }
-    uint32_t draft = 0;
-    if ((rc = snl_mtp(e, d->mr0, d->mtok, d->mn, d->mpos, d->mslot, 1, &draft, nullptr, nullptr))) return rc;
-    const auto tb = clk::now();
-    const int slot = snl_pos(e);
+    // the draft (Engine::mtp) and the verify of [tok, draft] (Engine::forward) as one step: the
+    // verify reads the draft's token on the device, the accept decision and the rollback's carried
+    // row are taken there too
     const uint32_t rope = d->rope;
-    uint32_t pair[2] = {d->tok, draft};
     uint32_t p2[6] = {rope, rope, rope, rope + 1, rope + 1, rope + 1};
-    if ((rc = snl_forward(e, pair, 2, p2, 2, 1, nullptr, picks))) return rc;
-    const auto tc = clk::now();
-    d->st.draft_s += secs(ts, tb);
-    d->st.verify_s += secs(tb, tc);
-    d->st.drafted++;
-    // Sampler::verify, greedy (src/sampler.rs:63-66, :87-89)
-    const uint32_t next = picks[0].token;
-    if (next == draft) {
-        d->st.accepted++;
-        d->st.generated++;
-        out[1] = draft;
-        if (gaps) gaps[1] = picks[0].top1 - picks[0].top2;
-        *n_out = 2;
-        d->tok = picks[1].token;
-        d->gap = picks[1].top1 - picks[1].top2;
-        d->mr0 = 1;
-        d->mn = 2;
-        d->mtok[0] = draft;
-        d->mtok[1] = d->tok;
-        for (int k = 0; k < 3; ++k) {
-            d->mpos[k] = rope;
-            d->mpos[3 + k] = rope + 1;
-        }
-        d->rope = rope + 2;
-    } else {
-        if ((rc = snl_rollback(e))) return rc;
-        d->tok = next;
-        d->gap = picks[0].top1 - picks[0].top2;
-        d->mr0 = 1;
-        d->mn = 1;
-        d->mtok[0] = d->tok;
-        for (int k = 0; k < 3; ++k) d->mpos[k] = rope;
-        d->rope = rope + 1;
-    }
-    d->mslot = slot;
+    snl::SpecOut o{};
+    float draft_ms = 0.0f, verify_ms = 0.0f;
+    if ((rc = snl::engine_spec_step(e, d->mr0, d->mtok, d->mn, d->mpos, d->mslot, d->tok, p2, &o, &draft_ms,
+                                    &verify_ms)))
+        return rc;
+    spec_apply(d, o, draft_ms, verify_ms, out, gaps, n_out);
     d->st.decode_s += secs(ts, clk::now());
     return SNL_OK;
+}
+
+int snl_decoder_steps(snl_decoder* d, int steps, uint32_t* out, float* gaps, int* n_out) {
+    if (!d || !out || !n_out || steps < 0) return SNL_EARG;
+    *n_out = 0;
+    if (!d->spec) {
+        for (int i = 0; i < steps; ++i) {
+            int n = 0;
+            if (int rc = snl_decoder_step(d, out + *n_out, gaps ? gaps + *n_out : nullptr, &n)) return rc;
+            *n_out += n;
+        }
+        return SNL_OK;
+    }
+    // step i + 1 is queued, from the records step i's control kernel writes, before the host waits
+    // for step i; every queued step is waited for before returning
+    snl_engine* e = d->e;
+    const auto ts = clk::now();
+    int rc = SNL_OK;
+    bool ahead = false;  // step i + 1 already queued
+    for (int i = 0; i < steps; ++i) {
+        uint32_t* o_out = out + *n_out;
+        float* o_gaps = gaps ? gaps + *n_out : nullptr;
+        int n = 0;
+        emit_pending(d, o_out, o_gaps, &n);
+        const uint32_t seq = snl::engine_spec_seq(e) - (ahead ? 1u : 0u);
+        if (!ahead) {
+            const uint32_t rope = d->rope;
+            uint32_t p2[6] = {rope, rope, rope, rope + 1, rope + 1, rope + 1};
+            if ((rc = snl::spec_prepare(e, d->mr0, d->mtok, d->mn, d->mpos, d->mslot, d->tok, p2)) ||
+                (rc = snl::spec_launch(e, true)))
+                break;
+        }
+        ahead = false;
+        if (i + 1 < steps && (rc = snl::engine_spec_ahead(e, &ahead))) break;
+        snl::SpecOut o{};
+        float draft_ms = 0.0f, verify_ms = 0.0f;
+        if ((rc = snl::spec_finish(e, seq, &o, &draft_ms, &verify_ms))) break;
+        spec_apply(d, o, draft_ms, verify_ms, o_out, o_gaps, &n);
+        *n_out += n;
+    }
+    if (rc && ahead) {  // leave nothing queued behind an error
+        snl::SpecOut o{};
+        (void)snl::spec_finish(e, snl::engine_spec_seq(e) - 1u, &o, nullptr, nullptr);
+    }
+    d->st.decode_s += secs(ts, clk::now());
+    return rc;
 }
 
 int snl_generate(snl_engine* e, const uint32_t* prompt, int n, int max_tokens, int spec, uint32_t* out, float* gaps,

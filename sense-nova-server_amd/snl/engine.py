@@ -121,6 +121,7 @@ def lib() -> ctypes.CDLL:
                                   ctypes.POINTER(ctypes.c_double), i32p]
         L.snl_decoder_create.argtypes = [vp, u32p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(vp)]
         L.snl_decoder_step.argtypes = [vp, u32p, f32p, i32p]
+        L.snl_decoder_steps.argtypes = [vp, ctypes.c_int, u32p, f32p, i32p]
         L.snl_decoder_stats.argtypes = [vp, ctypes.POINTER(GenStats)]
         L.snl_decoder_destroy.argtypes = [vp]
         L.snl_worker_create.argtypes = [vp, ctypes.c_int, ctypes.POINTER(vp)]
@@ -363,6 +364,14 @@ class Decoder:
         self.engine._check(lib().snl_decoder_step(self.h, _ptr(self._out, u32p), _ptr(self._gaps, f32p),
                                                   ctypes.byref(n)))
         return self._out[:n.value].tolist()
+
+    def steps(self, k: int):
+        """k steps in one native call (each queued on the device before the previous one is read);
+        returns the emitted tokens."""
+        out = np.zeros(2 * max(k, 1), np.uint32)
+        n = ctypes.c_int32()
+        self.engine._check(lib().snl_decoder_steps(self.h, int(k), _ptr(out, u32p), None, ctypes.byref(n)))
+        return out[:n.value].tolist()
 
     def stats(self) -> dict:
         st = GenStats()

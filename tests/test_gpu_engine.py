@@ -220,6 +220,63 @@ def test_forced_acceptance_matches_oracle(snl_mod, oracle, quant, tmp_path):
         o.close()
 
 
+def _decode_both(g, prompt, counts):
+    """The greedy speculative loop once through snl_decoder_step and once through
+    snl_decoder_steps (calls of `counts` steps each): tokens, stats and the engine state after."""
+    res = []
+    for many in (False, True):
+        d = g.decoder(prompt, spec=True)
+        toks = []
+        for k in counts:
+            if many:
+                toks += d.steps(k)
+            else:
+                for _ in range(k):
+                    toks += d.step()
+        st = d.stats()
+        res.append((toks, st["drafted"], st["accepted"], g.pos, g.hid_rows, g.buffer(2), g.buffer(3), g.buffer(4)))
+        d.close()
+    return res
+
+
+@pytest.mark.parametrize("quant", [0, 1], ids=["q8", "q4"])
+def test_decoder_steps_match_single_steps(snl_mod, oracle, quant, tmp_path):
+    """snl_decoder_steps queues each speculative step before the host reads the one before it, the
+    step's records being written on the device by the previous step's control kernel (accept
+    decision, state slots, positions, rotary table, the rollback's carried row).  Its tokens,
+    drafted / accepted counts and the engine state it leaves (position, hidden rows, carried hidden
+    row, recurrent and conv state of the current slot) must equal those of as many
+    snl_decoder_step calls, which the oracle tests pin: on random weights (every draft rejected), on
+    a head that confines the argmax to 5 tokens (drafts accepted), and up to the end of a short
+    context, where the loop stops queueing ahead."""
+    import snl_format as F
+
+    cfg = snl_mod.tiny_config()
+    o = oracle.Engine(cfg, seed=13, quant=quant, ctx=256, max_m=512)
+    o.zero_rows(-1, oracle.K_LM_HEAD, 4)
+    main, mtp = str(tmp_path / "model.snl"), str(tmp_path / "mtp.snl")
+    F.write_engine_files(o, cfg, quant, main, mtp)
+    o.close()
+    cases = [("random", snl_mod.Engine(cfg, seed=3, quant=quant, ctx=256), [1, 17, 23]),
+             ("forced", snl_mod.Engine.load(main, mtp, ctx=256), [2, 30, 9]),
+             ("context end", snl_mod.Engine(cfg, seed=3, quant=quant, ctx=48), [23])]
+    try:
+        for name, g, counts in cases:
+            prompt = _prompt(24, cfg.vocab, seed=5)
+            one, many = _decode_both(g, prompt, counts)
+            print(f"decoder steps quant={quant} {name}: {len(one[0])} tokens, drafted {one[1]} accepted {one[2]}, "
+                  f"pos {one[3]}", flush=True)
+            assert many[0] == one[0], name
+            assert many[1:5] == one[1:5], name
+            for a, b in zip(one[5:], many[5:]):
+                assert np.array_equal(a, b), name
+            if name == "forced":
+                assert one[2] > 0
+    finally:
+        for _, g, _ in cases:
+            g.close()
+
+
 def test_mtp_on_off_identical(pair):
     cfg, g, o = pair
     for seed in (1, 2, 3):
