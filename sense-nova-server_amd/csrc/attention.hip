@@ -106,8 +106,10 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
         const float* row = a.proj + (size_t)m * a.proj_stride;
 #pragma unroll
         for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
-        kv0[m] = mine[m] ? row[2 * q_dim + kh * HD + d] : 0.0f;
-        vv0[m] = mine[m] ? row[2 * q_dim + kv_dim + kh * HD + d] : 0.0f;
+        // this call's key / value rows where they fall in this part, zeros elsewhere, branch-free
+        // (a conditional load joined with a constant is waited for right after its issue)
+        kv0[m] = load_f32_or0(buffer_range(row + 2 * q_dim + kh * HD, HD * 4), (unsigned)d * 4u, mine[m]);
+        vv0[m] = load_f32_or0(buffer_range(row + 2 * q_dim + kv_dim + kh * HD, HD * 4), (unsigned)d * 4u, mine[m]);
     }
     const float nq = a.norms[d], nk = a.norms[HD + d];
     // the rotary cos / sin of this dim's frequency for each token, formed on the host

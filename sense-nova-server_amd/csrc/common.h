@@ -175,6 +175,24 @@ __device__ __forceinline__ float wave_max(float v) {
     return xor_max<1>(v);
 }
 
+// Raw buffer descriptor over [base, base + bytes) (gfx9 raw dword format in word 3): a load at
+// or past `bytes` returns 0 and touches no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_range(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Loads that read 0 instead of memory when `ok` is false, without a branch: the offset moves past
+// the descriptor's range.  (A load under a condition whose other side sets a constant makes the
+// compiler wait for the load where the two sides join, i.e. right after issuing it, which
+// serialises the memory round trips of the loads that follow.)
+constexpr unsigned kPastRange = 0xFFFFFF00u;
+__device__ __forceinline__ float load_f32_or0(__amdgpu_buffer_rsrc_t r, unsigned off, bool ok) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)(ok ? off : kPastRange), 0, 0));
+}
+__device__ __forceinline__ float4 load_f32x4_or0(__amdgpu_buffer_rsrc_t r, unsigned off, bool ok) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)(ok ? off : kPastRange), 0, 0));
+}
+
 // Sum over a block of NT threads (NT a multiple of 64, at most 1024); every thread gets the total.
 // The order is fixed by the thread layout, so the result does not depend on anything else.
 template <int NT>

@@ -52,16 +52,20 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     const int ch = which == 0 ? kh * DK + tid
                  : which == 1 ? key_dim + kh * DK + (tid - DK)
                               : 2 * key_dim + h * DV + cg * kCols + (tid - 2 * DK);
-    float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f}, r0 = 0.0f, r1 = 0.0f, r2 = 0.0f, cur[M];
-    if (which < 3) {
-        const float4 w = *reinterpret_cast<const float4*>(a.lw + (size_t)ch * 4);
+    // (branch-free: the other lanes read zeros through the buffer range, so no wait is forced)
+    const bool cl = which < 3;
+    const __amdgpu_buffer_rsrc_t lr = buffer_range(a.lw, (unsigned)cd * 16u);
+    const __amdgpu_buffer_rsrc_t sr = buffer_range(a.conv_state + (size_t)s_in * a.conv_slot, (unsigned)cd * 12u);
+    const __amdgpu_buffer_rsrc_t pr = buffer_range(a.proj, (unsigned)(M * a.proj_stride) * 4u);
+    float w4[4], r0, r1, r2, cur[M];
+    {
+        const float4 w = load_f32x4_or0(lr, (unsigned)ch * 16u, cl);
         w4[0] = w.x, w4[1] = w.y, w4[2] = w.z, w4[3] = w.w;
-        const float* cs = a.conv_state + (size_t)s_in * a.conv_slot;
-        r0 = cs[ch];
-        r1 = cs[cd + ch];
-        r2 = cs[2 * cd + ch];
+        r0 = load_f32_or0(sr, (unsigned)ch * 4u, cl);
+        r1 = load_f32_or0(sr, (unsigned)(cd + ch) * 4u, cl);
+        r2 = load_f32_or0(sr, (unsigned)(2 * cd + ch) * 4u, cl);
 #pragma unroll
-        for (int m = 0; m < M; ++m) cur[m] = a.proj[(size_t)m * a.proj_stride + ch];
+        for (int m = 0; m < M; ++m) cur[m] = load_f32_or0(pr, (unsigned)(m * a.proj_stride + ch) * 4u, cl);
     }
     const size_t hoff = (size_t)h * DK * DV;
     const float* S0 = a.state + (size_t)s_in * a.state_slot + hoff;
@@ -73,7 +77,7 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     float gz[M];  // silu of the output gate of column j
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-        const float z = rg == 0 ? a.proj[(size_t)m * a.proj_stride + cd + h * DV + j] : 0.0f;
+        const float z = load_f32_or0(pr, (unsigned)(m * a.proj_stride + cd + h * DV + j) * 4u, rg == 0);
         gz[m] = z / (1.0f + expf(-z));
     }
     float beta[M], decay[M];
