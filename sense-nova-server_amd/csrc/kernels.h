@@ -52,7 +52,12 @@ struct GemvArgs {
 };
 // grid size of launch_gemv over tile-order weights (the partial count a producer leaves)
 int mgemv_blocks(int quant, int N, int K, int inter);
+// Kernel-level GEMV (snl_gemv): the matrix-core path for tile-order weights, else the vector-ALU
+// fallback of gemv.hip / gemv_ksplit.hip for the reference's row-major layout at shapes the
+// matrix-core kernel does not serve (K % 128 != 0; M = 3, 4 where two token pairs overflow LDS).
+// The engine's passes never take the fallback.
 int launch_gemv(const GemvArgs& a, int quant, int M, hipStream_t s);
+// vector-ALU fallback, K split over blocks (kernel-level calls only)
 int launch_gemv_ksplit(const GemvArgs& a, int quant, int M, hipStream_t s);
 // Matrix-core path (mgemv.hip) over tile-order weights: 0 launched, 1 not served (M too large for
 // LDS at this K), < 0 error.
