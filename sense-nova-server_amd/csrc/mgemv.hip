@@ -267,8 +267,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const unsigned rin_off = ((unsigned)(reinterpret_cast<unsigned char*>(mult_s) - lds) + (unsigned)P * nss * 8 + 15u) & ~15u;
     const unsigned rin_w = rin_off + (unsigned)(wave - sw0) * kRinSlots * 1024;  // this wave's slots
     f32x4_t sb[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};  // the 8 router biases
+    // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
+    // of squares.
+    f32x4_t xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
+    auto stage_loads = [&]() {
     if constexpr (PRO == GEMV_NORM_MHC) {
-        if (stager) {
+        {
             const unsigned lds_base = (unsigned)(uintptr_t)(__attribute__((address_space(3))) void*)lds;
             // the 256-partial window may run past a shorter producer into other sums (masked when
             // added) but stays inside the partials buffer (kPartBlocks rows per sum)
@@ -292,10 +296,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             sb[1] = ld4(br, 16);
         }
     }
-    // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
-    // of squares.
-    f32x4_t xa[2 * P][UPT][2], xb[2 * P][UPT][2], nw[UPT][2], gp[2 * P][UPT];
-    if (stager) {
+    {
         const __amdgpu_buffer_rsrc_t nr = make_rsrc(a.norm_w, (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) ? (unsigned)K * 4 : 0u);
         // GNORM: the head partials [M][K/128][4]
         const __amdgpu_buffer_rsrc_t gr = make_rsrc(a.rin, PRO == GEMV_GNORM ? (unsigned)(M * (K / 128) * 16) : 0u);
@@ -320,6 +321,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             }
         }
     }
+    };
 
     // Thread tid owns output tid of the block (cnt*16*M outputs, all in streaming waves); the
     // residual it will update is read now, also ahead of the weights.
@@ -327,6 +329,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     const int e_T = tile0 + (e_r >> 4), e_j = e_r & 15;
     const int e_row = tid < cnt * 16 * M && !(EPI == GEMV_SWIGLU && e_j >= 8) ? tile_row<EPI>(a, e_T, e_j) : -1;
     float e_y0 = 0.0f, e_y1 = 0.0f;
+    float cfv = 0.0f;  // the site's token coefficients (MHC epilogue), left by its NORM_MHC launch
+    float nr0[8], nr1[8];  // router rows of the next mHC site at this output's row
+#pragma unroll
+    for (int o = 0; o < 8; ++o) nr0[o] = nr1[o] = 0.0f;
+    auto epilogue_loads = [&]() {
     if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
         if (e_row >= 0) {
             const float* yr = a.y + (size_t)e_m * a.y_stride;
@@ -334,15 +341,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             if constexpr (EPI == GEMV_MHC) e_y1 = yr[a.h + e_row];
         }
     }
-    // the site's token coefficients (MHC epilogue), left by the NORM_MHC launch of the same site
-    float cfv = 0.0f;
     if constexpr (EPI == GEMV_MHC) {
         if (tid < 8 * M) cfv = a.coef[tid];
     }
-    // router rows of the next mHC site at this output's row, when this launch leaves its partials
-    float nr0[8], nr1[8];
-#pragma unroll
-    for (int o = 0; o < 8; ++o) nr0[o] = nr1[o] = 0.0f;
     if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
         if (a.rpart && e_row >= 0)
 #pragma unroll
@@ -351,6 +352,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                 nr1[o] = a.next_w[(size_t)o * 2 * a.h + a.h + e_row];
             }
     }
+    };
 
     // ---- prologue, part 2: the staging, wave by wave ----
     float ssq[2 * P];  // this thread's sum of squares of the branch input, per token
@@ -659,15 +661,22 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     // Every wave of the block has issued its row loads before any wave issues weights, so the rows
     // are not queued behind the block's weight stream (issued after it they arrived ~6 us later).
     // The staging waves reach this barrier without waiting for any load.  The two roles run in
-    // separate branches, so a staging wave holds no weight ring and a streaming wave no token rows.
-    __builtin_amdgcn_s_barrier();
+    // separate branches from their first load on, each with its own copy of the barrier: a staging
+    // wave holds no weight ring and a streaming wave no token rows, and the compiler's wait
+    // tracking sees no join where a streaming wave might still owe a staging load.  (With the
+    // staging loads in a branch that joined the streaming path before the barrier, every streaming
+    // wave waited for its epilogue loads before issuing its second chunk.)
     if constexpr (IL == 1) {
         if (stager) {
+            stage_loads();
+            __builtin_amdgcn_s_barrier();
             stage();
             side_lds();
             lds_barrier();
             sinkhorn();
         } else {
+            epilogue_loads();
+            __builtin_amdgcn_s_barrier();
             // streaming-only waves send the whole ring at once
             issue(w0, s0, 0);
             issue(w1, s1, 1);
@@ -680,6 +689,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
         // Tile-major launches (the vocabulary head: many short blocks, several resident per CU):
         // the odd waves send their second chunk before the staging too (168 -> 163 us per
         // 248320 x 4096 Q8_0 head), the others after it.
+        stage_loads();
+        epilogue_loads();
+        __builtin_amdgcn_s_barrier();
         issue(w0, s0, 0);
         const bool early = (wave & 1) != 0;
         if (early) issue(w1, s1, 1);
