@@ -175,6 +175,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     __shared__ float cf_s[2 * P][8];                 // mHC token coefficients (MHC epilogue)
     __shared__ float raw_s[2 * P][9];                // last block: this site's router sums (NORM_MHC)
     __shared__ float pr_s[kMaxWaves * 16 / 32][2 * P][9];  // next-site router sums per 32-row group
+    __shared__ float rt_s[9 * 2 * P * 16];                 // one tile: [sum][token][row] of them
     constexpr int NI = QT == 0 ? 2 * U : U;   // 16-byte loads per lane per superstep
     constexpr int NM = QT == 0 ? 2 : 4;       // MFMAs per load
     constexpr int SSU = 16 * U;               // 8-element units per superstep
@@ -757,9 +758,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     }
     if constexpr (EPI == GEMV_ADD || EPI == GEMV_MHC) {
         if (a.rpart) {
-            // partial router sums of the next site over this block's rows: the lanes of one token
-            // add 32-row groups in a butterfly (stride M), then the groups are added in order, so
-            // the association is the same for every M
+            // partial router sums of the next site over this block's rows, in an order that is the
+            // same for every M (one tile: the rows in order; more: 32-row butterflies, then the
+            // groups in order)
             float c[9];
             if (e_row >= 0) {
                 const float4* st = reinterpret_cast<const float4*>(lds + rrow_off) + tid * 4;
@@ -773,21 +774,37 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
                 for (int o = 0; o < 8; ++o) c[o] = 0.0f;
             }
             c[8] = x0n * x0n + x1n * x1n;
-            // butterflies over the 32 rows of a token (lanes M apart), through DPP and permlane swaps
-            if (M == 2) {
-#pragma unroll
-                for (int o = 0; o < 9; ++o) c[o] = xor_sum<32>(xor_sum<16>(xor_sum<8>(xor_sum<4>(xor_sum<2>(c[o])))));
-            } else {
-#pragma unroll
-                for (int o = 0; o < 9; ++o) c[o] = xor_sum<16>(xor_sum<8>(xor_sum<4>(xor_sum<2>(xor_sum<1>(c[o])))));
-            }
             const int groups = (cnt * 16 + 31) / 32;
             if (groups == 1) {
-                // every output of the block sits in wave 0: lane m holds token m's sums
-                if (tid < M)
+                // one tile: every output sits in wave 0 (lane r*M + m: row r, token m).  The rows'
+                // values go through LDS and lane o*M + m adds sum o of token m over the 16 rows in
+                // row order (16 pipelined reads instead of 9 butterflies of 5 dependent swaps)
+                if (tid < 64) {
+                    if (tid < 16 * M)
 #pragma unroll
-                    for (int o = 0; o < 9; ++o) a.rpart[(size_t)(tid * 9 + o) * gridDim.x + blockIdx.x] = 0.0f + c[o];
+                        for (int o = 0; o < 9; ++o) rt_s[(o * 2 * P + e_m) * 16 + e_r] = c[o];
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+                    if (tid < 9 * M) {
+                        const int m = tid % M, o = tid / M;
+                        const float* rv = rt_s + (o * 2 * P + m) * 16;
+                        float t = rv[0];
+#pragma unroll
+                        for (int r = 1; r < 16; ++r) t = t + rv[r];
+                        a.rpart[(size_t)(m * 9 + o) * gridDim.x + blockIdx.x] = t;
+                    }
+                }
             } else {
+                // butterflies over the 32 rows of a token (lanes M apart), through DPP and permlane
+                // swaps, then the 32-row groups in order
+                if (M == 2) {
+#pragma unroll
+                    for (int o = 0; o < 9; ++o) c[o] = xor_sum<32>(xor_sum<16>(xor_sum<8>(xor_sum<4>(xor_sum<2>(c[o])))));
+                } else {
+#pragma unroll
+                    for (int o = 0; o < 9; ++o) c[o] = xor_sum<16>(xor_sum<8>(xor_sum<4>(xor_sum<2>(xor_sum<1>(c[o])))));
+                }
                 if (((tid / M) & 31) == 0 && tid < cnt * 16 * M)
 #pragma unroll
                     for (int o = 0; o < 9; ++o) pr_s[(tid / M) >> 5][tid % M][o] = c[o];
