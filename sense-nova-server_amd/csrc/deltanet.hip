@@ -67,19 +67,23 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
 #pragma unroll
         for (int m = 0; m < M; ++m) cur[m] = load_f32_or0(pr, (unsigned)(m * a.proj_stride + ch) * 4u, cl);
     }
+    const float* lwp = a.lw + (size_t)cd * 4;
+    const float a_log = lwp[h], dt_bias = lwp[a.n_v + h], norm_w = lwp[2 * a.n_v + j];
+    float zr[M];  // the output gate of column j
+#pragma unroll
+    for (int m = 0; m < M; ++m) zr[m] = load_f32_or0(pr, (unsigned)(m * a.proj_stride + cd + h * DV + j) * 4u, rg == 0);
+    // the state slice last: vector loads return in issue order, so the conv waits only for its
+    // own inputs and runs while the state is in flight
+    __builtin_amdgcn_sched_barrier(0);
     const size_t hoff = (size_t)h * DK * DV;
     const float* S0 = a.state + (size_t)s_in * a.state_slot + hoff;
     float s[kRows];
 #pragma unroll
     for (int r = 0; r < kRows; ++r) s[r] = S0[(size_t)(kRows * rg + r) * DV + j];
-    const float* lwp = a.lw + (size_t)cd * 4;
-    const float a_log = lwp[h], dt_bias = lwp[a.n_v + h], norm_w = lwp[2 * a.n_v + j];
-    float gz[M];  // silu of the output gate of column j
+    __builtin_amdgcn_sched_barrier(0);
+    float gz[M];  // silu of the output gate
 #pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const float z = load_f32_or0(pr, (unsigned)(m * a.proj_stride + cd + h * DV + j) * 4u, rg == 0);
-        gz[m] = z / (1.0f + expf(-z));
-    }
+    for (int m = 0; m < M; ++m) gz[m] = zr[m] / (1.0f + expf(-zr[m]));
     float beta[M], decay[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {  // linear.wgsl:113-117
