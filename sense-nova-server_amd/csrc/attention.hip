@@ -75,13 +75,35 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     static_assert((2 * G * M + M) * HD * 4 <= kPart * VROW * 2, "prep staging fits the value tile");
     const int kh = blockIdx.x, p = blockIdx.y;
     const StepDev* st = a.step;
+    const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // ---- loads that do not need the position go out first: the position is a scalar load that
+    // depends on another (the step record's address), and nothing else waits behind it ----
+    // attention.wgsl:59-127 for the group's 4 query heads and this call's new key / value rows:
+    // thread d holds dim d of each row
+    const int d = tid;
+    float qv0[G][M], kr0[M], vr0[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float* row = a.proj + (size_t)m * a.proj_stride;
+#pragma unroll
+        for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
+        kr0[m] = row[2 * q_dim + kh * HD + d];
+        vr0[m] = row[2 * q_dim + kv_dim + kh * HD + d];
+    }
+    const float nq = a.norms[d], nk = a.norms[HD + d];
+    // the rotary cos / sin of this dim's frequency for each token, formed on the host (every dim
+    // reads an entry; the dims past rot_dim drop it below)
+    const int half = a.rot_dim / 2;
+    float2 rt[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) rt[m] = *reinterpret_cast<const float2*>(st->rope[m][half > 0 ? d % half : 0]);
+    __builtin_amdgcn_sched_barrier(0);
     const int pos0 = st->pos0;
     const int kstart = p * kPart;
     const int total_max = pos0 + M;  // keys of the last token
     if (kstart >= total_max) return;
     const int nkeys = min(kPart, total_max - kstart);
-    const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
-    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n = lane & 15, g = lane >> 4;  // MFMA column (combination) and k-group of this lane
     int cm = -1;                             // the token of column n, if any
 #pragma unroll
@@ -92,41 +114,13 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
     for (int m = 0; m < M; ++m) mine[m] = pos0 + m >= kstart && pos0 + m < kstart + kPart;
 
-    // ---- loads: this call's rows, then the part's values (for the LDS tile) and this wave's keys
-    // (both straight from the cache, which the rows of this call's positions patch below) ----
+    // ---- then the part's values (for the LDS tile) and this wave's keys, straight from the cache
+    // (the rows of this call's positions patch them below) ----
     const unsigned row_bytes = (unsigned)kv_dim * 2;
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.kcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.vcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
-    // attention.wgsl:59-127 for the group's 4 query heads and this part's new key / value rows:
-    // thread d holds dim d of each row
-    const int d = tid;
-    float qv0[G][M], kv0[M], vv0[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const float* row = a.proj + (size_t)m * a.proj_stride;
-#pragma unroll
-        for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
-        // this call's key / value rows where they fall in this part, zeros elsewhere, branch-free
-        // (a conditional load joined with a constant is waited for right after its issue)
-        kv0[m] = load_f32_or0(buffer_range(row + 2 * q_dim + kh * HD, HD * 4), (unsigned)d * 4u, mine[m]);
-        vv0[m] = load_f32_or0(buffer_range(row + 2 * q_dim + kv_dim + kh * HD, HD * 4), (unsigned)d * 4u, mine[m]);
-    }
-    const float nq = a.norms[d], nk = a.norms[HD + d];
-    // the rotary cos / sin of this dim's frequency for each token, formed on the host
-    const int half = a.rot_dim / 2;
-    float rcs[M], rsn[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        rcs[m] = 1.0f;
-        rsn[m] = 0.0f;
-        if (d < a.rot_dim) {
-            const float2 t = *reinterpret_cast<const float2*>(st->rope[m][d % half]);
-            rcs[m] = t.x;
-            rsn[m] = t.y;
-        }
-    }
-    // then the cache loads: vector loads complete in issue order, so the waits for this call's rows
-    // above do not include them (issued first, they held the row prep back ~1 us)
+    // (vector loads complete in issue order, so the waits for this call's rows do not include
+    // the cache loads; issued first, they held the row prep back ~1 us)
     u32x4_t vv[kPart / 8];
 #pragma unroll
     for (int i = 0; i < kPart / 8; ++i)  // thread: keys tid / 32 + 8i, 16-byte segment tid % 32
@@ -135,6 +129,16 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
 #pragma unroll
     for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
         kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // this call's key / value rows where they fall in this part, zeros elsewhere
+    float kv0[M], vv0[M], rcs[M], rsn[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        kv0[m] = mine[m] ? kr0[m] : 0.0f;
+        vv0[m] = mine[m] ? vr0[m] : 0.0f;
+        rcs[m] = d < a.rot_dim ? rt[m].x : 1.0f;
+        rsn[m] = d < a.rot_dim ? rt[m].y : 0.0f;
+    }
     // RMSNorm (1 + w) over each row's 256 dims: wave sums, then the 4 waves in order
     float ss[NS];
 #pragma unroll

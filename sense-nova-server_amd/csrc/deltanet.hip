@@ -37,7 +37,6 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     __shared__ float ored[kWaves][M];                      // sums of o^2 per wave
 
     const StepDev* st = a.step;
-    const int s_in = st->s_in, s_out = st->s_out, s_ck = st->s_ck, ckpt = st->ckpt;
     const int h = blockIdx.x / kCG, cg = blockIdx.x - (blockIdx.x / kCG) * kCG;
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 3, rg = lane >> 2;
@@ -46,7 +45,9 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     const int key_dim = a.n_k * DK, cd = a.conv_dim;
     const int b_off = cd + a.n_v * DV, a_off = b_off + a.n_v;
 
-    // ---- every load up front: conv inputs, the state slice, per-token scalars ----
+    // ---- every load up front: first those that do not need the step record (the slots: a scalar
+    // load that depends on another), the conv state of all three slots among them, then the state
+    // slice ----
     // conv lanes: tid < 128 q channel, < 256 k channel, < 288 v channel of this column group
     const int which = tid < DK ? 0 : tid < 2 * DK ? 1 : tid < 2 * DK + kCols ? 2 : 3;
     const int ch = which == 0 ? kh * DK + tid
@@ -55,15 +56,11 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     // (branch-free: the other lanes read zeros through the buffer range, so no wait is forced)
     const bool cl = which < 3;
     const __amdgpu_buffer_rsrc_t lr = buffer_range(a.lw, (unsigned)cd * 16u);
-    const __amdgpu_buffer_rsrc_t sr = buffer_range(a.conv_state + (size_t)s_in * a.conv_slot, (unsigned)cd * 12u);
     const __amdgpu_buffer_rsrc_t pr = buffer_range(a.proj, (unsigned)(M * a.proj_stride) * 4u);
-    float w4[4], r0, r1, r2, cur[M];
+    float w4[4], cur[M];
     {
         const float4 w = load_f32x4_or0(lr, (unsigned)ch * 16u, cl);
         w4[0] = w.x, w4[1] = w.y, w4[2] = w.z, w4[3] = w.w;
-        r0 = load_f32_or0(sr, (unsigned)ch * 4u, cl);
-        r1 = load_f32_or0(sr, (unsigned)(cd + ch) * 4u, cl);
-        r2 = load_f32_or0(sr, (unsigned)(2 * cd + ch) * 4u, cl);
 #pragma unroll
         for (int m = 0; m < M; ++m) cur[m] = load_f32_or0(pr, (unsigned)(m * a.proj_stride + ch) * 4u, cl);
     }
@@ -72,6 +69,15 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
     float zr[M];  // the output gate of column j
 #pragma unroll
     for (int m = 0; m < M; ++m) zr[m] = load_f32_or0(pr, (unsigned)(m * a.proj_stride + cd + h * DV + j) * 4u, rg == 0);
+    float rs[3][3];  // conv state row i of slot k
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const __amdgpu_buffer_rsrc_t sr = buffer_range(a.conv_state + (size_t)k * a.conv_slot, (unsigned)cd * 12u);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) rs[k][i] = load_f32_or0(sr, (unsigned)(i * cd + ch) * 4u, cl);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int s_in = st->s_in, s_out = st->s_out, s_ck = st->s_ck, ckpt = st->ckpt;
     // the state slice last: vector loads return in issue order, so the conv waits only for its
     // own inputs and runs while the state is in flight
     __builtin_amdgcn_sched_barrier(0);
@@ -81,6 +87,9 @@ __global__ __launch_bounds__(kThreads) void deltanet_kernel(DeltaArgs a) {
 #pragma unroll
     for (int r = 0; r < kRows; ++r) s[r] = S0[(size_t)(kRows * rg + r) * DV + j];
     __builtin_amdgcn_sched_barrier(0);
+    float r0 = s_in == 0 ? rs[0][0] : s_in == 1 ? rs[1][0] : rs[2][0];
+    float r1 = s_in == 0 ? rs[0][1] : s_in == 1 ? rs[1][1] : rs[2][1];
+    float r2 = s_in == 0 ? rs[0][2] : s_in == 1 ? rs[1][2] : rs[2][2];
     float gz[M];  // silu of the output gate
 #pragma unroll
     for (int m = 0; m < M; ++m) gz[m] = zr[m] / (1.0f + expf(-zr[m]));
