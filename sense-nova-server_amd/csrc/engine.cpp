@@ -1826,6 +1826,8 @@ int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s) {
             hipMemcpy(hs.data(), sp, g.s_floats * 4, hipMemcpyDeviceToHost) != hipSuccess)
             return SNL_EDEVICE;
         uint8_t* qo = static_cast<uint8_t*>(q);
+        if (w->quant == 0)  // packed Q8 bytes carry the offset-binary flip of packing.h
+            for (uint8_t& b : hq) b ^= 0x80u;
         for (int T = 0; T < g.tiles; ++T)
             for (int S = 0; S < g.nss; ++S)
                 for (int lane = 0; lane < 64; ++lane) {

@@ -9,9 +9,10 @@
 // The dot products run on v_mfma_f32_16x16x32_f16, which takes the place of the per-element
 // convert-and-FMA of a vector-ALU GEMV (that costs ~3.5 VALU lane-ops per weight byte at M=2,
 // close to the whole VALU budget at full HBM rate).  Both operands are exact:
-//   * quants become f16 exactly: Q8 bytes are xor-ed with 0x80, v_perm pairs each byte with 0x64
-//     (the f16 1024 + byte), and one packed f16 subtract of 1152 leaves q; Q4 nibbles are masked
-//     into the same f16 pattern and 1032 is subtracted;
+//   * quants become f16 exactly: Q8 bytes, stored in offset binary (q + 128), are paired with 0x64
+//     by v_perm (the f16 1024 + byte) and one packed f16 subtract of 1152 leaves q; Q4 nibbles are
+//     masked into the same f16 pattern in place (then 1032 is subtracted) or from the upper half
+//     of their byte (1024 + 16n, then times 1/16 minus 72);
 //   * each token row x (f32) is split into two f16 parts, hi = f16(x) and lo = f16(x - hi), whose
 //     sum carries 22 significant bits; a power of two per token and superstep scales the part's
 //     largest |x| into [2^13, 2^14), so hi cannot overflow and small rows keep their bits.
@@ -119,12 +120,17 @@ __device__ __forceinline__ void opaque(f32x4_t& v) { asm volatile("" : "+v"(v));
 
 // 8 weights of one 16-byte load as exact f16: MFMA i (0..NM-1) of the load.
 // Q8 order: elements 8i..8i+7.  Q4 order (word i): elements 8i + {0, 4, 1, 5, 2, 6, 3, 7}.
+// Q8: the packed bytes are offset binary (q + 128, packing.h); v_perm pairs each with 0x64, the f16
+// 1024 + byte, and one packed subtract of 1152 leaves q.  Q4: nibble pairs (i, i + 4) are masked
+// into the f16 pattern in place, 0x6400 | n = 1024 + n (subtract 1032), or from the upper half of
+// their byte, 0x6400 | 16n = 1024 + 16n (times 1/16 minus 72, one packed fma, exact): 9 vector
+// instructions per 8 weights.
 template <int QT>
 __device__ __forceinline__ half8_t dequant8(const uint4& w, int i) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
     if constexpr (QT == 0) {
         const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-        const uint32_t u0 = wd[2 * i] ^ 0x80808080u, u1 = wd[2 * i + 1] ^ 0x80808080u;
+        const uint32_t u0 = wd[2 * i], u1 = wd[2 * i + 1];
         const half2_t p0 = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04010400u)) - bias;
         const half2_t p1 = as_h2(__builtin_amdgcn_perm(0x64646464u, u0, 0x04030402u)) - bias;
         const half2_t p2 = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04010400u)) - bias;
@@ -132,11 +138,12 @@ __device__ __forceinline__ half8_t dequant8(const uint4& w, int i) {
         return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     } else {
         const half2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-        const uint32_t v = wd[i];
+        const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f}, b72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+        const uint32_t v = wd[i], v8 = v >> 8;
         const half2_t p0 = as_h2((v & 0x000F000Fu) | 0x64006400u) - bias;
-        const half2_t p1 = as_h2(((v >> 4) & 0x000F000Fu) | 0x64006400u) - bias;
-        const half2_t p2 = as_h2(((v >> 8) & 0x000F000Fu) | 0x64006400u) - bias;
-        const half2_t p3 = as_h2(((v >> 12) & 0x000F000Fu) | 0x64006400u) - bias;
+        const half2_t p1 = __builtin_elementwise_fma(as_h2((v & 0x00F000F0u) | 0x64006400u), s16, b72);
+        const half2_t p2 = as_h2((v8 & 0x000F000Fu) | 0x64006400u) - bias;
+        const half2_t p3 = __builtin_elementwise_fma(as_h2((v8 & 0x00F000F0u) | 0x64006400u), s16, b72);
         return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     }
 }
@@ -889,6 +896,12 @@ __global__ __launch_bounds__(256) void pack_q_kernel(PackGeom g, const uint8_t* 
     const int row = pack_row(g, T, lane & 15);
     uint4 val = make_uint4(0u, 0u, 0u, 0u);
     if (row >= 0) val = *reinterpret_cast<const uint4*>(q + (size_t)row * g.row_bytes + pack_row_offset(g, S, v, lane >> 4));
+    if (g.quant == 0) {  // Q8 in offset binary
+        val.x ^= 0x80808080u;
+        val.y ^= 0x80808080u;
+        val.z ^= 0x80808080u;
+        val.w ^= 0x80808080u;
+    }
     *reinterpret_cast<uint4*>(qp + pack_piece(g, T, S, v, lane)) = val;
 }
 

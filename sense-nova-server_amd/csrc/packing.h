@@ -29,6 +29,8 @@
 // with vv the load inside the chunk and the scales of chunk (q, i) at ((q*items + i)*64 + l)*CS.
 // Sizes: tiles*16*K (Q8) or tiles*8*K (Q4) bytes and tiles*16*K/32 scales, the reference's
 // sizes whenever the tile count divides the rows.
+// Q8 bytes are stored in offset binary (the int8 value plus 128, i.e. the byte xor 0x80), the
+// form the GEMV turns into an exact f16 with one byte permute; padding rows hold 0x80 (zero).
 #pragma once
 
 #include <stddef.h>
