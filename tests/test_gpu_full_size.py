@@ -125,12 +125,17 @@ def test_nine_b_matches_oracle(big, oracle):
 
 
 def test_mtp_on_off_identical_full_size(big):
+    """The 9B workload itself: a 1024-token prompt (two prefill chunks), 512 greedy tokens with the
+    MTP head drafting and without it, byte-identical."""
     cfg, e, _ = big
-    prompt = _prompt(600, cfg.vocab, seed=4)
-    a = e.generate(prompt, 24, False)
-    b = e.generate(prompt, 24, True)
+    prompt = _prompt(1024, cfg.vocab, seed=4)
+    a = e.generate(prompt, 512, False)
+    b = e.generate(prompt, 512, True)
+    # (an end-of-sequence pick would stop both runs at the same token)
+    assert 0 < len(a["tokens"]) == len(b["tokens"]) <= 512
     assert a["tokens"] == b["tokens"]
-    assert b["drafted"] > 0
+    assert b["drafted"] > 0 and 0 <= b["accepted"] <= b["drafted"]
+    print(f"9B 1024 + {len(b['tokens'])}: drafted {b['drafted']} accepted {b['accepted']}", flush=True)
 
 
 def test_verify_rows_equal_single_token_feeds_full_size(big):
