@@ -66,6 +66,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMaxWaves = 16;
+constexpr int kRing4Waves = 12;           // largest block of the four-chunk ring
 constexpr int kCUs = 256;                 // MI355X compute units
 constexpr int kLdsLimit = 150 * 1024;     // dynamic LDS per block
 constexpr int kZeroBytes = 64;            // zero A fragment read by the lanes outside their slot
@@ -172,10 +173,15 @@ __device__ __forceinline__ int a_pos(int e) {
 // 1/rms of the branch input is applied to the dot products in the epilogue, from the staging
 // waves' sums of squares; the mHC pre-mix coefficients come from the router sums, which every
 // staging wave adds up itself from the producer's partials.
+//
+// IL 2 is chunk-major with a four-chunk ring, for blocks of at most 12 waves (a wave may then hold
+// 170 registers): the deeper ring keeps the memory pipe fed while the staging of a normed or mHC
+// branch input is still running.
 template <int QT, int P, int EPI, int PRO, int U, int UPT, int IL>
-__global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M, int KS, int base, int extra,
-                                                               int nss_w, int tiles, int sw0) {
-    constexpr int il = IL;
+__global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void mgemv_kernel(
+    GemvArgs a, int M, int KS, int base, int extra, int nss_w, int tiles, int sw0) {
+    constexpr int il = IL ? 1 : 0;
+    constexpr int RING = IL == 2 ? 4 : 3;
     extern __shared__ __align__(16) unsigned char lds[];
     __shared__ float red_s[kMaxWaves * 16 * 2 * P];  // [wave][row j][token]
     __shared__ float ssq_s[kMaxWaves][2 * P];        // staging waves' sums of squares, per token
@@ -213,8 +219,8 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     constexpr int CL = U == 4 ? NI / 2 : NI;  // loads per chunk
     constexpr int CPS = NI / CL;              // chunks per superstep
     constexpr int CS = U / CPS;               // scales per chunk
-    uint4 w0[CL], w1[CL], w2[CL];
-    float s0[CS], s1[CS], s2[CS];
+    uint4 w0[CL], w1[CL], w2[CL], w3[CL];
+    float s0[CS], s1[CS], s2[CS], s3[CS];
     const int nch = nss_w * CPS;
     const size_t item = (size_t)Tl * KS + ks;
     const size_t items = (size_t)tiles * KS;
@@ -643,10 +649,34 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             }
         };
 
-        // Steady state: compute a chunk, issue the one three ahead.  The last five chunks or fewer run
-        // as a straight-line tail that issues nothing past the slice.
+        // Steady state: compute a chunk, issue the one RING ahead.  The last 2 RING - 1 chunks or fewer
+        // run as a straight-line tail that issues nothing past the slice.
         const int nrun = active ? nch : 0;
         int q = 0;
+        if constexpr (RING == 4) {
+            for (; q + 7 < nrun; q += 4) {
+                compute(w0, s0, q);
+                issue(w0, s0, q + 4);
+                compute(w1, s1, q + 1);
+                issue(w1, s1, q + 5);
+                compute(w2, s2, q + 2);
+                issue(w2, s2, q + 6);
+                compute(w3, s3, q + 3);
+                issue(w3, s3, q + 7);
+            }
+            const int rem = nrun - q;  // 0 (idle wave) .. 7
+            if (rem >= 1) compute(w0, s0, q);
+            if (rem >= 5) issue(w0, s0, q + 4);
+            if (rem >= 2) compute(w1, s1, q + 1);
+            if (rem >= 6) issue(w1, s1, q + 5);
+            if (rem >= 3) compute(w2, s2, q + 2);
+            if (rem >= 7) issue(w2, s2, q + 6);
+            if (rem >= 4) compute(w3, s3, q + 3);
+            if (rem >= 5) compute(w0, s0, q + 4);
+            if (rem >= 6) compute(w1, s1, q + 5);
+            if (rem >= 7) compute(w2, s2, q + 6);
+            return;
+        }
         for (; q + 5 < nrun; q += 3) {
             compute(w0, s0, q);
             issue(w0, s0, q + 3);
@@ -674,7 +704,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
     // tracking sees no join where a streaming wave might still owe a staging load.  (With the
     // staging loads in a branch that joined the streaming path before the barrier, every streaming
     // wave waited for its epilogue loads before issuing its second chunk.)
-    if constexpr (IL == 1) {
+    if constexpr (IL >= 1) {
         if (stager) {
             stage_loads();
             __builtin_amdgcn_s_barrier();
@@ -689,6 +719,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void mgemv_kernel(GemvArgs a, int M
             issue(w0, s0, 0);
             issue(w1, s1, 1);
             issue(w2, s2, 2);
+            if constexpr (RING == 4) issue(w3, s3, 3);
             side_lds();
             lds_barrier();
             main_loop();
@@ -831,8 +862,9 @@ using KernelFn = void (*)(GemvArgs, int, int, int, int, int, int, int);
 
 template <int QT, int U, int UPT>
 KernelFn pick_fn(int P, int epi, int pro, int il) {
-#define SNL_G(E, PR) \
-    if (epi == E && pro == PR) return &mgemv_kernel<QT, 1, E, PR, U, UPT, 1>;
+#define SNL_G(E, PR)                                                                   \
+    if (epi == E && pro == PR)                                                         \
+        return il == 2 ? &mgemv_kernel<QT, 1, E, PR, U, UPT, 2> : &mgemv_kernel<QT, 1, E, PR, U, UPT, 1>;
     if (il == 0) {
         // tile-major (the vocabulary head, the draft's with its final norm): the plain store
         if constexpr (UPT <= 2) {
@@ -865,7 +897,8 @@ KernelFn pick_fn(int P, int epi, int pro, int il) {
     // two token pairs: the plain product with at most 2 units per staging thread (kernel-level
     // calls with M = 3, 4)
     if constexpr (UPT <= 2)
-        if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN) return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U, UPT, 1>;
+        if (P == 2 && epi == GEMV_STORE && pro == GEMV_PLAIN && il == 1)
+            return &mgemv_kernel<QT, 2, GEMV_STORE, GEMV_PLAIN, U, UPT, 1>;
     return nullptr;
 }
 
@@ -934,7 +967,7 @@ int mgemv_init() {
                 for (int P = 1; P <= 2; ++P)
                     for (int e = 0; e < 4; ++e)
                         for (int p = 0; p < 4; ++p)
-                            for (int il = 0; il < 2; ++il) {
+                            for (int il = 0; il < 3; ++il) {
                                 KernelFn f = pick(q, U, upt, P, e, p, il);
                                 if (f && hipFuncSetAttribute(reinterpret_cast<const void*>(f),
                                                              hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1040,7 +1073,11 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     if (a.epi == GEMV_MHC && !a.coef) return -1;
     if (a.rpart && (!a.next_w || (a.epi != GEMV_ADD && a.epi != GEMV_MHC) || (M & (M - 1)))) return -1;
     if (a.epi == GEMV_ADD && a.rpart && !a.expand) return -1;  // an ADD producer starts the mHC range
-    KernelFn f = pick(quant, g.U, sh.upt, P, a.epi, a.pro, g.il);
+    // a chunk-major block of at most 12 waves with more than three chunks per wave streams through
+    // the four-chunk ring (same arithmetic, same order)
+    KernelFn f = nullptr;
+    if (g.il == 1 && sh.waves <= kRing4Waves && sh.nss_w * g.CPS > 3) f = pick(quant, g.U, sh.upt, P, a.epi, a.pro, 2);
+    if (!f) f = pick(quant, g.U, sh.upt, P, a.epi, a.pro, g.il);
     if (!f) return 1;
     hipLaunchKernelGGL(f, dim3(sh.blocks), dim3(sh.waves * 64), lds, s, a, M, sh.KS, sh.base, sh.extra, sh.nss_w,
                        g.tiles, sh.sw0);
