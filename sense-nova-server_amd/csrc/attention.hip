@@ -43,6 +43,80 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
+// attention.wgsl:59-127 once per KV head, for contexts past kSplitPrepCtx: block kv head, thread d
+// holds dim d of the group's 4 query rows and of this call's new key and value rows, per token.
+// RMSNorm (1 + w), then rotate-half RoPE on the first rot_dim dims: the rotated queries go to qbuf,
+// the new keys and values to the f16 cache.  The same operations as the fused prep of
+// attend_kernel, so either path gives the same bits.
+constexpr int kSplitPrepCtx = 8192;
+
+template <int M>
+__global__ __launch_bounds__(256) void prep_kernel(AttnArgs a) {
+    constexpr int NS = G * M + M;
+    __shared__ float qs[G * M][HD], ks[M][HD];
+    __shared__ float red[4][NS];
+    const int kh = blockIdx.x, d = threadIdx.x, lane = d & 63, w = d >> 6;
+    const StepDev* st = a.step;
+    const int q_dim = a.n_heads * HD, kv_dim = a.n_kv * HD;
+    float qv0[G][M], kr0[M], vr0[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float* row = a.proj + (size_t)m * a.proj_stride;
+#pragma unroll
+        for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
+        kr0[m] = row[2 * q_dim + kh * HD + d];
+        vr0[m] = row[2 * q_dim + kv_dim + kh * HD + d];
+    }
+    const float nq = a.norms[d], nk = a.norms[HD + d];
+    const int half = a.rot_dim / 2;
+    float rcs[M], rsn[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float2 rt = *reinterpret_cast<const float2*>(st->rope[m][half > 0 ? d % half : 0]);
+        rcs[m] = d < a.rot_dim ? rt.x : 1.0f;
+        rsn[m] = d < a.rot_dim ? rt.y : 0.0f;
+    }
+    const int pos0 = st->pos0;
+    float ss[NS];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) ss[j * M + m] = qv0[j][m] * qv0[j][m];
+        ss[G * M + m] = kr0[m] * kr0[m];
+    }
+    wave_sum_n(ss);
+    if (lane == 0)
+#pragma unroll
+        for (int i = 0; i < NS; ++i) red[w][i] = ss[i];
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const int i = j * M + m;
+            const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
+            qs[i][d] = (qv0[j][m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nq);
+        }
+        const int i = G * M + m;
+        const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
+        ks[m][d] = (kr0[m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nk);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float cs = rcs[m], sn = rsn[m];
+        auto rot = [&](const float* v) {
+            if (d >= a.rot_dim) return v[d];
+            return d < half ? v[d] * cs - v[d + half] * sn : v[d] * cs + v[d - half] * sn;
+        };
+#pragma unroll
+        for (int j = 0; j < G; ++j) a.qbuf[(size_t)m * q_dim + (kh * G + j) * HD + d] = rot(qs[j * M + m]);
+        const size_t c = (size_t)(pos0 + m) * kv_dim + kh * HD + d;
+        a.kcache[c] = __builtin_bit_cast(uint16_t, (_Float16)rot(ks[m]));
+        a.vcache[c] = __builtin_bit_cast(uint16_t, (_Float16)vr0[m]);
+    }
+}
+
 // Block (kv head, part of kPart keys) for all M tokens and the 4 query heads of the GQA group,
 // 256 threads = 4 waves, on v_mfma_f32_16x16x32_f16.  The 16 MFMA columns hold the head-token
 // combinations: token m's 4 heads take columns 4 * ((pos0 + m) & 1) + head, so a token sits in the
@@ -57,8 +131,14 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 //  values:  O^T = V^T P^T: the part's values pass through LDS (64 keys x 256 dims, f16, rows past
 //           the last key zero) and each lane gathers the 8 keys of its A fragment for one dim;
 //           B = the probabilities as f16 hi + lo; wave w takes dims [64w, 64w+64).
-template <int M>
-__global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
+//
+// FUSED: the block also forms its queries and this call's new keys (norms, RoPE: prep above) and
+// writes the new cache rows, which suits short contexts where the key parts are few.  Otherwise
+// (contexts past kSplitPrepCtx, hundreds of parts) prep_kernel has done that once per KV head and
+// the block reads the rotated queries from qbuf and every key from the cache; the results are
+// bitwise the same.
+template <int M, bool FUSED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attend_kernel(AttnArgs a) {
     constexpr int NC = G * M;
     static_assert(NC == 4 || NC == 8, "M = 1 or 2");
     constexpr int VROW = HD + 16;  // V tile row in halfs (544 bytes: a transposed read's 4 rows on distinct banks)
@@ -83,21 +163,24 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     // thread d holds dim d of each row
     const int d = tid;
     float qv0[G][M], kr0[M], vr0[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const float* row = a.proj + (size_t)m * a.proj_stride;
-#pragma unroll
-        for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
-        kr0[m] = row[2 * q_dim + kh * HD + d];
-        vr0[m] = row[2 * q_dim + kv_dim + kh * HD + d];
-    }
-    const float nq = a.norms[d], nk = a.norms[HD + d];
-    // the rotary cos / sin of this dim's frequency for each token, formed on the host (every dim
-    // reads an entry; the dims past rot_dim drop it below)
+    float nq = 0.0f, nk = 0.0f;
     const int half = a.rot_dim / 2;
     float2 rt[M];
+    if constexpr (FUSED) {
 #pragma unroll
-    for (int m = 0; m < M; ++m) rt[m] = *reinterpret_cast<const float2*>(st->rope[m][half > 0 ? d % half : 0]);
+        for (int m = 0; m < M; ++m) {
+            const float* row = a.proj + (size_t)m * a.proj_stride;
+#pragma unroll
+            for (int j = 0; j < G; ++j) qv0[j][m] = row[(kh * G + j) * 2 * HD + d];
+            kr0[m] = row[2 * q_dim + kh * HD + d];
+            vr0[m] = row[2 * q_dim + kv_dim + kh * HD + d];
+        }
+        nq = a.norms[d], nk = a.norms[HD + d];
+        // the rotary cos / sin of this dim's frequency for each token, formed on the host (every
+        // dim reads an entry; the dims past rot_dim drop it below)
+#pragma unroll
+        for (int m = 0; m < M; ++m) rt[m] = *reinterpret_cast<const float2*>(st->rope[m][half > 0 ? d % half : 0]);
+    }
     __builtin_amdgcn_sched_barrier(0);
     const int pos0 = st->pos0;
     const int kstart = p * kPart;
@@ -115,104 +198,144 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     for (int m = 0; m < M; ++m) mine[m] = pos0 + m >= kstart && pos0 + m < kstart + kPart;
 
     // ---- then the part's values (for the LDS tile) and this wave's keys, straight from the cache
-    // (the rows of this call's positions patch them below) ----
+    // (FUSED: the rows of this call's positions patch them below) ----
     const unsigned row_bytes = (unsigned)kv_dim * 2;
     const __amdgpu_buffer_rsrc_t kr = make_rsrc(a.kcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
     const __amdgpu_buffer_rsrc_t vr = make_rsrc(a.vcache + (size_t)kstart * kv_dim, (unsigned)nkeys * row_bytes);
-    // (vector loads complete in issue order, so the waits for this call's rows do not include
-    // the cache loads; issued first, they held the row prep back ~1 us)
+    // not FUSED: the group's rotated queries first (vector loads complete in issue order, so they
+    // are not waited for behind the keys and values), thread d taking dim d of each row, once per
+    // block; they reach the lanes' fragments through LDS
+    float qd[G][M];
+    if constexpr (!FUSED) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int j = 0; j < G; ++j) qd[j][m] = a.qbuf[(size_t)m * q_dim + (kh * G + j) * HD + d];
+    }
+    // FUSED: (vector loads complete in issue order, so the waits for this call's rows do not
+    // include the cache loads; issued first, they held the row prep back ~1 us)
     u32x4_t vv[kPart / 8];
-#pragma unroll
-    for (int i = 0; i < kPart / 8; ++i)  // thread: keys tid / 32 + 8i, 16-byte segment tid % 32
-        vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((tid >> 5) + 8 * i) * (int)row_bytes + kh * HD * 2 + (tid & 31) * 16, 0, 0);
     u32x4_t kf[HD / 32];
+    if constexpr (FUSED) {
 #pragma unroll
-    for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
-        kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
+        for (int i = 0; i < kPart / 8; ++i)  // thread: keys tid / 32 + 8i, 16-byte segment tid % 32
+            vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((tid >> 5) + 8 * i) * (int)row_bytes + kh * HD * 2 + (tid & 31) * 16, 0, 0);
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)  // key 16w + n, dims 32s + 8g .. + 7
+            kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
+    } else {
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s)
+            kf[s] = __builtin_amdgcn_raw_buffer_load_b128(kr, (16 * w + n) * (int)row_bytes + (kh * HD + 32 * s + 8 * g) * 2, 0, 0);
+#pragma unroll
+        for (int i = 0; i < kPart / 8; ++i)
+            vv[i] = __builtin_amdgcn_raw_buffer_load_b128(vr, ((tid >> 5) + 8 * i) * (int)row_bytes + kh * HD * 2 + (tid & 31) * 16, 0, 0);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    // this call's key / value rows where they fall in this part, zeros elsewhere
-    float kv0[M], vv0[M], rcs[M], rsn[M];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        kv0[m] = mine[m] ? kr0[m] : 0.0f;
-        vv0[m] = mine[m] ? vr0[m] : 0.0f;
-        rcs[m] = d < a.rot_dim ? rt[m].x : 1.0f;
-        rsn[m] = d < a.rot_dim ? rt[m].y : 0.0f;
-    }
-    // RMSNorm (1 + w) over each row's 256 dims: wave sums, then the 4 waves in order
-    float ss[NS];
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-#pragma unroll
-        for (int j = 0; j < G; ++j) ss[j * M + m] = qv0[j][m] * qv0[j][m];
-        ss[G * M + m] = kv0[m] * kv0[m];
-    }
-    wave_sum_n(ss);
-    if (lane == 0)
-#pragma unroll
-        for (int i = 0; i < NS; ++i) red[w][i] = ss[i];
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const int i = j * M + m;
-            const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
-            qs[i * HD + d] = (qv0[j][m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nq);
-        }
-        if (mine[m]) {
-            const int i = G * M + m;
-            const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
-            ks[m * HD + d] = (kv0[m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nk);
-        }
-    }
-    __syncthreads();
-    // rotate-half RoPE on the first rot_dim dims; the new keys and values go to the cache
-#pragma unroll
-    for (int m = 0; m < M; ++m) {
-        const float cs = rcs[m], sn = rsn[m];
-        auto rot = [&](const float* v) {
-            if (d >= a.rot_dim) return v[d];
-            return d < half ? v[d] * cs - v[d + half] * sn : v[d] * cs + v[d - half] * sn;
-        };
-#pragma unroll
-        for (int j = 0; j < G; ++j) {
-            const float q = rot(qs + (j * M + m) * HD);
-            qr[(j * M + m) * HD + d] = q;
-            if (p == 0) a.qbuf[(size_t)m * q_dim + (kh * G + j) * HD + d] = q;
-        }
-        if (mine[m]) {
-            const _Float16 kq = (_Float16)rot(ks + m * HD), vq = (_Float16)vv0[m];
-            knew[m][d] = kq;
-            vnew[m][d] = vq;
-            const size_t c = (size_t)(pos0 + m) * kv_dim + kh * HD + d;
-            a.kcache[c] = __builtin_bit_cast(uint16_t, kq);
-            a.vcache[c] = __builtin_bit_cast(uint16_t, vq);
-        }
-    }
-    __syncthreads();
-    // the query fragments: lane (column n, k-group g) takes dims 32s + 8g .. + 7 of its column
     float qv[HD / 32][8];
     float amax = 0.0f;
+    if constexpr (FUSED) {
+        // this call's key / value rows where they fall in this part, zeros elsewhere
+        float kv0[M], vv0[M], rcs[M], rsn[M];
 #pragma unroll
-    for (int s = 0; s < HD / 32; ++s) {
-        float4 u0 = make_float4(0.f, 0.f, 0.f, 0.f), u1 = u0;
-        if (cm >= 0) {
-            const float4* qp = reinterpret_cast<const float4*>(qr + (chh * M + cm) * HD + 32 * s + 8 * g);
-            u0 = qp[0];
-            u1 = qp[1];
+        for (int m = 0; m < M; ++m) {
+            kv0[m] = mine[m] ? kr0[m] : 0.0f;
+            vv0[m] = mine[m] ? vr0[m] : 0.0f;
+            rcs[m] = d < a.rot_dim ? rt[m].x : 1.0f;
+            rsn[m] = d < a.rot_dim ? rt[m].y : 0.0f;
         }
-        qv[s][0] = u0.x, qv[s][1] = u0.y, qv[s][2] = u0.z, qv[s][3] = u0.w;
-        qv[s][4] = u1.x, qv[s][5] = u1.y, qv[s][6] = u1.z, qv[s][7] = u1.w;
+        // RMSNorm (1 + w) over each row's 256 dims: wave sums, then the 4 waves in order
+        float ss[NS];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[s][e]));
+        for (int m = 0; m < M; ++m) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) ss[j * M + m] = qv0[j][m] * qv0[j][m];
+            ss[G * M + m] = kv0[m] * kv0[m];
+        }
+        wave_sum_n(ss);
+        if (lane == 0)
+#pragma unroll
+            for (int i = 0; i < NS; ++i) red[w][i] = ss[i];
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const int i = j * M + m;
+                const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
+                qs[i * HD + d] = (qv0[j][m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nq);
+            }
+            if (mine[m]) {
+                const int i = G * M + m;
+                const float total = (((0.0f + red[0][i]) + red[1][i]) + red[2][i]) + red[3][i];
+                ks[m * HD + d] = (kv0[m] * (1.0f / sqrtf(total / (float)HD + a.eps))) * (1.0f + nk);
+            }
+        }
+        __syncthreads();
+        // rotate-half RoPE on the first rot_dim dims; the new keys and values go to the cache
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const float cs = rcs[m], sn = rsn[m];
+            auto rot = [&](const float* v) {
+                if (d >= a.rot_dim) return v[d];
+                return d < half ? v[d] * cs - v[d + half] * sn : v[d] * cs + v[d - half] * sn;
+            };
+#pragma unroll
+            for (int j = 0; j < G; ++j) {
+                const float q = rot(qs + (j * M + m) * HD);
+                qr[(j * M + m) * HD + d] = q;
+                if (p == 0) a.qbuf[(size_t)m * q_dim + (kh * G + j) * HD + d] = q;
+            }
+            if (mine[m]) {
+                const _Float16 kq = (_Float16)rot(ks + m * HD), vq = (_Float16)vv0[m];
+                knew[m][d] = kq;
+                vnew[m][d] = vq;
+                const size_t c = (size_t)(pos0 + m) * kv_dim + kh * HD + d;
+                a.kcache[c] = __builtin_bit_cast(uint16_t, kq);
+                a.vcache[c] = __builtin_bit_cast(uint16_t, vq);
+            }
+        }
+        __syncthreads();
+        // the query fragments: lane (column n, k-group g) takes dims 32s + 8g .. + 7 of its column
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s) {
+            float4 u0 = make_float4(0.f, 0.f, 0.f, 0.f), u1 = u0;
+            if (cm >= 0) {
+                const float4* qp = reinterpret_cast<const float4*>(qr + (chh * M + cm) * HD + 32 * s + 8 * g);
+                u0 = qp[0];
+                u1 = qp[1];
+            }
+            qv[s][0] = u0.x, qv[s][1] = u0.y, qv[s][2] = u0.z, qv[s][3] = u0.w;
+            qv[s][4] = u1.x, qv[s][5] = u1.y, qv[s][6] = u1.z, qv[s][7] = u1.w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[s][e]));
+        }
+        // the key rows of this call's positions come from knew, not from the cache loads above
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+            if (mine[m] && kstart + 16 * w + n == pos0 + m)
+#pragma unroll
+                for (int s = 0; s < HD / 32; ++s) kf[s] = *reinterpret_cast<const u32x4_t*>(&knew[m][32 * s + 8 * g]);
+    } else {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+            for (int j = 0; j < G; ++j) qr[(j * M + m) * HD + d] = qd[j][m];
+        lds_barrier();
+#pragma unroll
+        for (int s = 0; s < HD / 32; ++s) {
+            float4 u0 = make_float4(0.f, 0.f, 0.f, 0.f), u1 = u0;
+            if (cm >= 0) {
+                const float4* qp = reinterpret_cast<const float4*>(qr + (chh * M + cm) * HD + 32 * s + 8 * g);
+                u0 = qp[0];
+                u1 = qp[1];
+            }
+            qv[s][0] = u0.x, qv[s][1] = u0.y, qv[s][2] = u0.z, qv[s][3] = u0.w;
+            qv[s][4] = u1.x, qv[s][5] = u1.y, qv[s][6] = u1.z, qv[s][7] = u1.w;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[s][e]));
+        }
     }
-    // the key rows of this call's positions come from knew, not from the cache loads above
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-        if (mine[m] && kstart + 16 * w + n == pos0 + m)
-#pragma unroll
-            for (int s = 0; s < HD / 32; ++s) kf[s] = *reinterpret_cast<const u32x4_t*>(&knew[m][32 * s + 8 * g]);
     amax = xor_max<32>(xor_max<16>(amax));  // the 4 lanes of column n
     const int ex = amax > 0.0f ? max(ilogbf(amax) - 14, -110) : 0;
     const float down = ldexpf(1.0f, -ex), up = ldexpf(1.0f, ex) * a.scale;
@@ -231,9 +354,10 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     for (int i = 0; i < kPart / 8; ++i) {
         const int r = (tid >> 5) + 8 * i;
         u32x4_t val = vv[i];
+        if constexpr (FUSED)
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-            if (mine[m] && kstart + r == pos0 + m) val = *reinterpret_cast<const u32x4_t*>(&vnew[m][(tid & 31) * 8]);
+            for (int m = 0; m < M; ++m)
+                if (mine[m] && kstart + r == pos0 + m) val = *reinterpret_cast<const u32x4_t*>(&vnew[m][(tid & 31) * 8]);
         *reinterpret_cast<u32x4_t*>(vt + r * VROW + (tid & 31) * 8) = val;
     }
 
@@ -313,13 +437,13 @@ __global__ __launch_bounds__(256) void attend_kernel(AttnArgs a) {
     }
 }
 
-// attention.wgsl:248-269: merge the token's parts, then the sigmoid gate.  Block (head, token, 64
-// dims) of 1024 threads: every part's scale e^(max_p - max) goes to LDS once, then thread (d, q)
+// attention.wgsl:248-269: merge the token's parts, then the sigmoid gate.  Block (head, token, 32
+// dims) of 512 threads: every part's scale e^(max_p - max) goes to LDS once, then thread (d, q)
 // adds the parts q, q+16, ... of dim d and the 16 groups are added in order.  Many short chains
-// keep a long context's partials (512 parts at 32K keys) in flight at once.  Past 1024 parts
-// (64K keys) thread t also takes the parts t + 1024, t + 2048, ... for the maximum and the weights;
+// keep a long context's partials (512 parts at 32K keys) in flight at once.  Past 512 parts
+// (32K keys) thread t also takes the parts t + 512, t + 1024, ... for the maximum and the weights;
 // the order of every sum depends on the token's part count alone.
-constexpr int kCombThreads = 1024, kCombDims = 64, kCombGroups = kCombThreads / kCombDims;
+constexpr int kCombThreads = 512, kCombDims = 32, kCombGroups = kCombThreads / kCombDims;
 
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(AttnArgs a) {
     __shared__ float fs[kAttnMaxParts];
@@ -382,10 +506,19 @@ int launch_attention(const AttnArgs& a, int M, hipStream_t s) {
     if (a.ctx > kMaxCtx) return -1;
     const int parts_max = (a.ctx + kPart - 1) / kPart;
     dim3 grid(a.n_kv, parts_max);
-    switch (M) {
-        case 1: hipLaunchKernelGGL(attend_kernel<1>, grid, dim3(256), 0, s, a); break;
-        case 2: hipLaunchKernelGGL(attend_kernel<2>, grid, dim3(256), 0, s, a); break;
-        default: return -1;
+    // the context the engine was sized for (not the position) picks the path, so a captured pass
+    // keeps one launch sequence
+    const bool split = a.ctx > kSplitPrepCtx;
+    if (split) {
+        if (M == 1) hipLaunchKernelGGL(prep_kernel<1>, dim3(a.n_kv), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL(prep_kernel<2>, dim3(a.n_kv), dim3(256), 0, s, a);
+    }
+    if (M == 1) {
+        if (split) hipLaunchKernelGGL((attend_kernel<1, false>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attend_kernel<1, true>), grid, dim3(256), 0, s, a);
+    } else {
+        if (split) hipLaunchKernelGGL((attend_kernel<2, false>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((attend_kernel<2, true>), grid, dim3(256), 0, s, a);
     }
     hipLaunchKernelGGL(combine_kernel, dim3(a.n_heads, M, HD / kCombDims), dim3(kCombThreads), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -2;
