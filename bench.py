@@ -276,10 +276,17 @@ def summarize_decode_pmc(d: str) -> str:
         cnt = (sum(float(r["Counter_Value"]) for r in fa) / len(fa) * ff +
                sum(float(r["Counter_Value"]) for r in wa) / len(wa) * wf) * 1024.0
         us = sum((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in ta) / len(ta)
+        kname = _short(ta[0]["Kernel_Name"]) if ta else "attend_kernel"
         alg = (p0 + 2) * 1024 * 2 * 2
         gbs = alg / (us * 1e-6) / 1e9
-        out.append(f"| attention at {p0} keys (kernel-level) | `attend_kernel<2>` | - | {alg / 1e6:.2f} | "
+        out.append(f"| attention at {p0} keys (kernel-level) | `{kname}` | - | {alg / 1e6:.2f} | "
                    f"{cnt / 1e6:.2f} | {cnt / alg:.3f} | {us:.2f} | {gbs:.0f} | {gbs / HBM_PEAK_GBS:.3f} |")
+        # contexts past 8K positions form the queries once per KV head in their own launch
+        tp = [r for r in _csv_rows(os.path.join(d, "at_kernel_trace.csv")) if "prep_kernel" in r["Kernel_Name"]]
+        if tp:
+            pus = sum((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in tp) / len(tp)
+            out.append(f"| attention at {p0} keys (kernel-level) | `{_short(tp[0]['Kernel_Name'])}` | - | - | - | - | "
+                       f"{pus:.2f} | - | - |")
     return "\n".join(out) + "\n"
 
 
