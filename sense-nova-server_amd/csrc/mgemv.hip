@@ -33,9 +33,10 @@
 // [b*base + min(b, extra), +base + (b < extra)) (chunk-major shapes use extra = 0: base tiles per
 // block, the last block the rest), its streaming wave w the item (tile w / KS, slice w % KS), so
 // every active wave streams the same bytes, and pack_stage_waves(K) more waves stage the token
-// rows.  Taller matrices (the vocabulary head) run many short blocks of 4
-// slices x 2 tiles whose waves do both.  The split depends on the matrix shape alone, never on M.
-// Weights stream through a three-chunk register ring (half supersteps).  Slices are added in
+// rows.  Taller matrices (the vocabulary head) run many short blocks of 4 slices x 2 tiles
+// (Q4: 2 x 4) whose waves do both.  The split depends on the matrix shape and quant type alone,
+// never on M.  Weights stream through a three-chunk register ring (half supersteps; four chunks
+// in blocks of at most 12 waves).  Slices are added in
 // slice order through LDS, so a token's result does not depend on M, on its index or on timing
 // (greedy output is then byte-identical with and without speculative drafting).
 //
