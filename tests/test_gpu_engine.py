@@ -4,7 +4,7 @@ hidden 256, FFN 768, vocab 4096, 8 layers (DeltaNet : attention = 3 : 1), layers
 twice, 2-stream mHC over the loop, 1-layer MTP head; seeded Q8_0 / Q4_0 weights drawn on the
 device and, independently, by the oracle on the CPU.
 
-Bars (north star): weights bit-exact; token ids and acceptance decisions bit-exact except at
+Bars: weights bit-exact; token ids and acceptance decisions bit-exact except at
 argmax near-ties (top-2 gap < 1e-3 in the oracle's logits); logits and DeltaNet state within
 1e-2 relative; greedy output byte-identical with and without MTP.
 """

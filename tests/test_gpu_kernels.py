@@ -1,6 +1,6 @@
 """Kernel-level parity of the HIP library (through the C ABI) against the CPU oracle.
 
-Tolerances: the north star asks for fp32-accumulation agreement within 1e-2 relative on
+Tolerances: the path is required to agree within 1e-2 relative (fp32 accumulation) on
 logits and DeltaNet state; the kernels here are held to much tighter bounds (GEMV 1e-5 of
 the sum of |terms|), since the oracle and the GPU only differ in summation order.
 Integer/index work (greedy pick) is bit-exact.
@@ -197,7 +197,7 @@ def test_deltanet_matches_oracle(torch_cuda, K, oracle, nk, nv, m):
     if ckpt:
         assert np.allclose(got_ss[1], st_ck, rtol=1e-4, atol=1e-5)
         assert np.allclose(got_cs[1], conv_ck, rtol=1e-6, atol=1e-6)
-    # relative error of the state within the north-star bound
+    # relative error of the state within the 1e-2 bound
     rel = np.abs(got_ss[2] - st_ref).max() / np.abs(st_ref).max()
     assert rel < 1e-2
 
