@@ -4,7 +4,7 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the shipped library links, loads or
  * calls this file: only tests/, __graft_entry__.smoke() and bench.py's CPU
- * baseline use it, and only as the checker (or as the timed CPU baseline).
+ * baseline use it, and only as the reference results (or as the timed CPU baseline).
  *
  * Every kernel below follows one WGSL entry point of the reference, in the
  * same arithmetic order where the WGSL fixes it (explicit loops, tree
@@ -34,7 +34,7 @@
  *   mtp, rollback,       never run, snapshot/restore, MTP on == off.  The op order
  *   snapshot, generate)  itself (src/engine.rs:383-570) is a restatement with no
  *                        independent check: parity unpinned.
- *   twin RNG, weights    this build's own convention (no reference counterpart);
+ *   twin RNG, weights    the engine's own convention (no reference counterpart);
  *                        moments and determinism only.
  */
 #include <math.h>

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/snl_oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/snl_oracle.c) before the GPU results are compared with it.
 
 The reference ships no golden vectors or tests for this path, so each oracle
 function is pinned here by what the mathematics fixes: fp64 restatements of
