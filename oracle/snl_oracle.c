@@ -30,10 +30,14 @@
  *   attn_prep, attend,   float64 RMSNorm + RoPE, transformers rotate-half, brute-force
  *   combine              softmax attention over the f16 cache, split-K invariance
  *   argmax               brute force, first index on ties
- *   engine (forward,     self-consistency only: stepwise == batched, rollback ==
- *   mtp, rollback,       never run, snapshot/restore, MTP on == off.  The op order
- *   snapshot, generate)  itself (src/engine.rs:383-570) is a restatement with no
- *                        independent check: parity unpinned.
+ *   engine (forward,     the op order (src/engine.rs:383-570) against an independent
+ *   mtp, rollback,       composition of transformers' Qwen3.5 modules over the same
+ *   snapshot, generate)  weights (stored logits, tests/golden/composition.npz): plain,
+ *                        looped and mHC models, Q8_0 and Q4_0, prefill chunks, verify,
+ *                        MTP catch-up and drafts; the mHC router by a zero-router closed
+ *                        form; planted mistakes rejected.  Plus self-consistency:
+ *                        stepwise == batched, rollback == never run, snapshot/restore,
+ *                        MTP on == off.
  *   twin RNG, weights    the engine's own convention (no reference counterpart);
  *                        moments and determinism only.
  */
