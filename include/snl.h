@@ -266,6 +266,11 @@ int snl_worker_run_sampled(snl_worker* w, const uint32_t* prompt, int n, int sna
 int snl_tensor_info(const snl_engine* e, int layer, int kind, int* rows, int* cols);
 /* Copy a tensor to host memory: q (quants or f32 values) and s (scales; NULL for vectors). */
 int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s);
+/* Set the block scales of rows first.. of a quantised matrix to zero, so those rows dequantise to
+ * exactly 0 (every copy the engine keeps of it).  No counterpart in the reference: on random
+ * weights no draft is ever accepted, so tests and the bench confine the LM head's argmax to its
+ * first rows this way to drive the accept branch of the decode loop.  Drops cached state. */
+int snl_tensor_zero_rows(snl_engine* e, int layer, int kind, int first);
 /* Copy an engine buffer to host: 0 x [2, 2H], 1 hid [3, H], 2 hlast [H], 3 DeltaNet state
  * (current slot, all visits), 4 conv state (current slot), 5 MTP residual [2, 2H]. */
 int snl_buffer_read(snl_engine* e, int id, void* out, size_t bytes);
@@ -318,14 +323,14 @@ int snl_attention(const float* proj, int proj_stride, float* qbuf, uint16_t* kca
                   float rope_theta, float eps, const int32_t* mrope_section, int ctx, int M, int pos0,
                   const uint32_t* rpos, void* stream);
 
-/* Greedy pick of `rows` device logits rows of length V into device picks_out. */
+/* Greedy pick of `rows` device logits rows of length V into device picks_out; 1 <= rows <= 64. */
 int snl_pick_rows(const float* logits, int V, int rows, snl_pick* picks_out, void* stream);
 
 /* snl_pick_rows without any device allocation.  No counterpart in the reference: it is for callers
  * that cannot allocate (code under HIP graph capture, serving loops or harnesses that forbid
  * hipMalloc).  The block partials live in a static 48 KiB device array, one per GPU, held until
  * the process ends, so rows * ceil(V / 2048) may be at most 4096 (e.g. 33 rows of a 248320-entry
- * vocabulary; SNL_EARG beyond).  The call only enqueues work on `stream`, a stream of the current
+ * vocabulary), and rows at most 64 as for snl_pick_rows; SNL_EARG beyond either limit.  The call only enqueues work on `stream`, a stream of the current
  * device, and returns; picks_out is ready when the stream reaches it.  Calls that overlap on one
  * GPU share the array and race. */
 int snl_pick_rows_noalloc(const float* logits, int V, int rows, snl_pick* picks_out, void* stream);

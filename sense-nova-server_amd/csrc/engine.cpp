@@ -56,6 +56,9 @@ constexpr int kLogitRows = 2;
 constexpr int kDistMax = 1024;  // largest k the device top-k serves (SNL_DIST_MAX)
 // Token rows per captured pass.  The kernels take up to SNL_MAX_M; passes use 1 or 2.
 constexpr int kMaxM = 2;
+// Hidden rows: row 0 carries the token before a pass, rows 1..M a pass's final-normed rows (up to
+// SNL_PF_M), and one more row for the padding row a two-row draft over r0 = SNL_PF_M reads.
+constexpr int kHidRows = SNL_PF_M + kMaxM;
 constexpr int kSpecRing = 4;  // speculative step outcomes held in pinned memory
 
 // Tensor kinds of the seeded initialiser: stream id = ((layer + 1) << 8) | kind for layer
@@ -216,7 +219,11 @@ struct snl_engine {
     // Counts the calls that change the caches, the recurrent state or a snapshot slot, so that a
     // holder of cache bookkeeping (the worker) can tell whether someone else has moved the engine.
     uint64_t epoch = 0;
-    std::map<std::tuple<int, int, int, int>, hipGraphExec_t> graphs;
+    std::map<std::tuple<int, int, int, int, int>, hipGraphExec_t> graphs;
+    // Keys the decode attention launches of a captured pass cover (its grid, part count and
+    // query-prep path): the context bucket of the positions the pass may reach, so the cost of a
+    // decode pass follows the position, not the allocated context.  0 outside recording.
+    int span = 0;
     std::string err;
 
     // Per-op timing of an eagerly launched pass (the reference's SENSENOVA_PROFILE mode,
@@ -434,10 +441,20 @@ struct snl_engine {
         return launch_mhc(pf_x, w, pf_part, h, M, stream) |
                launch_mhc_coef(pf_part, w, h, cfg.mhc_iterations, pf_coef, M, stream);
     }
-    int run(int kind, int M, int a, int b, bool upload = true);
+    int run(int kind, int M, int a, int b, int keys, bool upload = true);
+    // The context bucket serving passes over up to `keys` cache positions: 2048 * 2^k, capped at
+    // the allocated context.  Results do not depend on it (blocks past the live keys return, and
+    // both query-prep paths give the same bits); only the launch shape does.
+    int span_for(int keys) const {
+        int b = 2048;
+        while (b < keys && b < ctx) b *= 2;
+        return std::min(b, ctx);
+    }
+    int ensure_rope_tab();
+    int build_spec_pair(int keys);
     // the speculative step's graph (run kind 2): the MTP draft over M pairs, then the checkpointed
     // 2-row verify whose second token is the draft's pick, with event records around both passes
-    int build_spec(int M, int parity, hipGraphExec_t* out);
+    int build_spec(int M, int parity, int sp, hipGraphExec_t* out);
     static constexpr int kPartBlocks = 4096;  // partial-sum slots of mhc_part per token
     int part_n = 0;                           // partials currently in mhc_part (0: none)
     // GEMV with an optional fused branch-input prologue (pro: GEMV_NORM with norm weights nw, or
@@ -518,7 +535,7 @@ struct snl_engine {
         a.eps = cfg.eps;
         a.scale = 1.0f / sqrtf((float)cfg.head_dim);
         a.mrope = ((uint32_t)(3 * cfg.mrope_section[1]) << 16) | (uint32_t)(3 * cfg.mrope_section[2]);
-        a.ctx = ctx;
+        a.ctx = span > 0 ? span : ctx;
         a.step = st;
         return a;
     }
@@ -629,7 +646,7 @@ int snl_engine::init() {
         (rc = dalloc(&dn_ssq, (size_t)M * std::max(c.lin_v_heads, 1) * kDeltaGroups)) ||
         (rc = dalloc(&mhc_part, (size_t)kPartBlocks * M * 9)) ||
         (rc = dalloc(&partial, (size_t)M * c.n_heads * parts_max * (c.head_dim + 2))) ||
-        (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)(SNL_PF_M + 1) * h)) ||
+        (rc = dalloc(&logits, (size_t)kLogitRows * c.vocab)) || (rc = dalloc(&hid, (size_t)kHidRows * h)) ||
         (rc = dalloc(&hlast, (size_t)h)) || (rc = dalloc(&mx, (size_t)M * 2 * h)) ||
         (rc = dalloc(&hn, (size_t)M * h)) || (rc = dalloc(&m_logits, (size_t)c.vocab)) ||
         (rc = dalloc(&pick_scratch, pick_scratch_floats(c.vocab, kLogitRows))) || (rc = dalloc(&d_picks, 2)) ||
@@ -688,26 +705,10 @@ int snl_engine::init() {
     if (hipHostGetDevicePointer((void**)&hd_ring, h_ring, 0) != hipSuccess || !hd_ring)
         return fail(SNL_EDEVICE, "no device address for the pinned step ring");
     memset(h_ring, 0, kSpecRing * sizeof(SpecOut));
-    // rotary cos / sin of every text position (all three rotary components equal), as step_rope
-    // forms them, for the records the speculative step's control kernel writes
-    {
-        rope_rows = ctx + 4;
-        std::vector<float> tab((size_t)rope_rows * SNL_ROPE_MAX * 2, 0.0f);
-        StepDev tmp;
-        for (int p = 0; p < rope_rows; ++p) {
-            memset(&tmp, 0, sizeof tmp);
-            for (int k = 0; k < 3; ++k) tmp.rpos[0][k] = (uint32_t)p;
-            step_rope(tmp, 1, c.rope_theta, c.rot_dim, c.mrope_section);
-            memcpy(tab.data() + (size_t)p * SNL_ROPE_MAX * 2, tmp.rope[0], SNL_ROPE_MAX * 2 * sizeof(float));
-        }
-        if ((rc = dalloc(&rope_tab, tab.size()))) return rc;
-        if (hipMemcpy(rope_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
-            return fail(SNL_EDEVICE, "rotary table upload failed");
-    }
     // zero everything a pass may read before writing (the reference's buffers start zeroed)
     if (hipMemsetAsync(x, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
         hipMemsetAsync(mx, 0, sizeof(float) * M * 2 * h, stream) != hipSuccess ||
-        hipMemsetAsync(hid, 0, sizeof(float) * (SNL_PF_M + 1) * h, stream) != hipSuccess ||
+        hipMemsetAsync(hid, 0, sizeof(float) * kHidRows * h, stream) != hipSuccess ||
         hipMemsetAsync(hlast, 0, sizeof(float) * h, stream) != hipSuccess ||
         hipMemsetAsync(lin_state, 0, sizeof(float) * 3 * nl * state_floats, stream) != hipSuccess ||
         hipMemsetAsync(conv_state, 0, sizeof(float) * 3 * nl * conv_floats, stream) != hipSuccess ||
@@ -964,24 +965,27 @@ int snl_engine::prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int 
 // Replays the captured pass of `kind` (0: forward of M rows, a logit rows, checkpoint b; 1: MTP
 // head over M pairs, draft a; 2: a greedy speculative step, the MTP draft over M pairs then the
 // checkpointed 2-row verify) after uploading its step records.
-int snl_engine::run(int kind, int M, int a, int b, bool upload) {
+int snl_engine::run(int kind, int M, int a, int b, int keys, bool upload) {
     const int first = kind == 1 ? 1 : 0, count = kind == 2 ? 2 : 1;
     if (upload &&
         hipMemcpyAsync(d_step + first, h_step + first, count * sizeof(StepDev), hipMemcpyHostToDevice, stream) !=
             hipSuccess)
         return fail(SNL_EDEVICE, "step upload failed");
-    auto key = std::make_tuple(kind, M, a, b);
+    const int sp = span_for(keys);
+    auto key = std::make_tuple(kind, M, a, b, sp);
     auto it = graphs.find(key);
     if (it == graphs.end() && kind == 2) {
         hipGraphExec_t ex = nullptr;
-        if (int rc = build_spec(M, a, &ex)) return rc;
+        if (int rc = build_spec(M, a, sp, &ex)) return rc;
         it = graphs.emplace(key, ex).first;
     }
     if (it == graphs.end()) {
         hipGraph_t g = nullptr;
         if (hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
             return fail(SNL_EDEVICE, "hipStreamBeginCapture failed");
+        span = sp;
         int rc = kind == 0 ? record_forward(M, a, b) : record_mtp(M, a);
+        span = 0;
         hipError_t ce = hipStreamEndCapture(stream, &g);
         if (rc || ce != hipSuccess) {
             if (g) hipGraphDestroy(g);
@@ -998,9 +1002,53 @@ int snl_engine::run(int kind, int M, int a, int b, bool upload) {
     return SNL_OK;
 }
 
+// The rotary cos / sin of every text position (the three rotary components equal, as decode
+// positions are), bitwise as step_rope forms them, for the records the speculative step's control
+// kernel writes.  Built on the first speculative step, so engines that never draft hold none.
+int snl_engine::ensure_rope_tab() {
+    if (rope_tab) return SNL_OK;
+    const int rows = ctx + 4, half = cfg.rot_dim / 2;
+    std::vector<float> tab((size_t)rows * SNL_ROPE_MAX * 2, 0.0f);
+    float inv_freq[SNL_ROPE_MAX];
+    for (int f = 0; f < half && f < SNL_ROPE_MAX; ++f)
+        inv_freq[f] = powf(cfg.rope_theta, -(float)(2 * f) / (float)cfg.rot_dim);
+    for (int p = 0; p < rows; ++p)
+        for (int f = 0; f < half && f < SNL_ROPE_MAX; ++f) {
+            const float ang = (float)p * inv_freq[f];
+            tab[((size_t)p * SNL_ROPE_MAX + f) * 2] = cosf(ang);
+            tab[((size_t)p * SNL_ROPE_MAX + f) * 2 + 1] = sinf(ang);
+        }
+    float* d = nullptr;
+    if (int rc = dalloc(&d, tab.size())) return rc;
+    if (hipMemcpy(d, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess)
+        return fail(SNL_EDEVICE, "rotary table upload failed");  // (d stays in allocs, freed with the engine)
+    rope_tab = d;
+    rope_rows = rows;
+    return SNL_OK;
+}
+
+// Both instances of the speculative step graph (steps alternate between them).
+int snl_engine::build_spec_pair(int keys) {
+    const int sp = span_for(keys);
+    for (int parity = 0; parity < 2; ++parity) {
+        const auto key = std::make_tuple(2, kMaxM, parity, 0, sp);
+        if (graphs.count(key)) continue;
+        hipGraphExec_t ex = nullptr;
+        if (int rc = build_spec(kMaxM, parity, sp, &ex)) return rc;
+        graphs.emplace(key, ex);
+    }
+    return SNL_OK;
+}
+
 // The two passes are captured on their own, then joined in a parent graph between event record
 // nodes (an event recorded inside a stream capture was refused here).
-int snl_engine::build_spec(int M, int parity, hipGraphExec_t* out) {
+int snl_engine::build_spec(int M, int parity, int sp, hipGraphExec_t* out) {
+    if (int rc = ensure_rope_tab()) return rc;
+    struct SpanScope {  // the span of this capture, cleared on every return
+        int& s;
+        SpanScope(int& v, int x) : s(v) { s = x; }
+        ~SpanScope() { s = 0; }
+    } scope(span, sp);
     hipGraph_t ga = nullptr, gb = nullptr, pg = nullptr;
     auto capture = [&](hipGraph_t* g, bool draft) -> int {
         if (const hipError_t be = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal); be != hipSuccess) {
@@ -1320,7 +1368,7 @@ int snl_forward(snl_engine* e, const uint32_t* tokens, int n, const uint32_t* po
             st.rpos[i][3] = 0;
         }
         step_rope(st, n, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
-        int rc = e->run(0, n, rows, ckpt ? 1 : 0);
+        int rc = e->run(0, n, rows, ckpt ? 1 : 0, e->pos + n);
         if (rc) return rc;
         // the step record is reused by the next call: wait for this one
         if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "forward failed on device");
@@ -1370,7 +1418,9 @@ int snl_forward_profiled(snl_engine* e, const uint32_t* tokens, int n, const uin
     std::vector<snl_engine::Mark> marks;
     marks.reserve(2048);
     e->marks = &marks;
+    e->span = e->span_for(e->pos + n);
     int rc = e->record_forward(n, rows, ckpt ? 1 : 0);
+    e->span = 0;
     e->marks = nullptr;
     hipError_t se = hipStreamSynchronize(e->stream);
     int k = 0;
@@ -1426,6 +1476,7 @@ int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch
     e->only = name;
     e->only_launches = 0;
     e->only_bytes = 0.0;
+    e->span = e->span_for(e->pos + 2);
     int rc = e->record_forward(2, 2, 1);  // warm-up pass
     const int per_pass = e->only_launches;
     const double bytes = per_pass ? e->only_bytes / per_pass : 0.0;
@@ -1433,6 +1484,7 @@ int snl_time_op(snl_engine* e, const char* name, int reps, double* ms_per_launch
     for (int r = 0; r < reps && !rc; ++r) rc |= e->record_forward(2, 2, 1);
     hipEventRecord(t1, e->stream);
     e->only = nullptr;
+    e->span = 0;
     float ms = 0.0f;
     const hipError_t se = hipEventSynchronize(t1);
     hipEventElapsedTime(&ms, t0, t1);
@@ -1482,7 +1534,7 @@ int snl_mtp(snl_engine* e, int r0, const uint32_t* tokens, int n, const uint32_t
             for (int k = 0; k < 3; ++k) st.rpos[i][k] = pos3[(c0 + i) * 3 + k];
         }
         step_rope(st, m, e->cfg.rope_theta, e->cfg.rot_dim, e->cfg.mrope_section);
-        int rc = e->run(1, m, last && draft ? 1 : 0, 0);
+        int rc = e->run(1, m, last && draft ? 1 : 0, 0, slot0 + c0 + m);
         if (rc) return rc;
         if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "mtp failed on device");
     }
@@ -1591,6 +1643,8 @@ int spec_prepare(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint
     if (mn < 1 || mn > kMaxM || !mtok || !mpos || !pos3 || r0 < 0 || r0 + mn > e->hid_rows + 1 || slot0 < 0 ||
         slot0 + kMaxM > e->ctx)
         return e->fail(SNL_EARG, "mtp: rows out of range");
+    // the draft pass reads kMaxM hidden rows from r0, padding included
+    if (r0 + kMaxM > kHidRows) return e->fail(SNL_EARG, "mtp: hidden rows %d..%d past the buffer", r0, r0 + kMaxM - 1);
     for (int i = 0; i < mn; ++i)
         if (mtok[i] >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", mtok[i]);
     if (tok >= (uint32_t)e->cfg.vocab) return e->fail(SNL_ETOKEN, "token id %u out of range", tok);
@@ -1630,7 +1684,12 @@ int spec_launch(snl_engine* e, bool upload) {
         for (hipEvent_t& ev : evs)
             if (!ev && hipEventCreate(&ev) != hipSuccess) return e->fail(SNL_EDEVICE, "event creation failed");
     const int parity = (int)(e->spec_seq & 1u);
-    if (int rc = e->run(2, kMaxM, parity, 0, upload)) return rc;
+    // Keys: step seq's verify reaches pos + 2 (host position) and a step queued ahead of it pos + 4;
+    // both instances of that context bucket are built before the first launch, so queueing a step
+    // ahead never captures.
+    const int keys = e->pos + 4;
+    if (int rc = e->build_spec_pair(keys)) return rc;
+    if (int rc = e->run(2, kMaxM, parity, 0, keys, upload)) return rc;
     ++e->spec_seq;
     return SNL_OK;
 }
@@ -1642,6 +1701,8 @@ int spec_finish(snl_engine* e, uint32_t seq, SpecOut* out, float* draft_ms, floa
     if (hipEventSynchronize(ev[2]) != hipSuccess) return e->fail(SNL_EDEVICE, "speculative step failed on device");
     const SpecOut o = e->h_ring[seq % kSpecRing];
     if (o.seq != seq) return e->fail(SNL_EDEVICE, "speculative step %u: outcome of step %u in the ring", seq, o.seq);
+    if (o.flags & kSpecRopeRange)
+        return e->fail(SNL_ECTX, "speculative step %u: rotary position past the context's table", seq);
     ++e->epoch;
     e->ck_slot = (e->cur + 1) % 3;
     e->cur = (e->cur + 2) % 3;
@@ -1846,6 +1907,59 @@ int snl_tensor_read(snl_engine* e, int layer, int kind, void* q, float* s) {
     const size_t qb = type == 0 ? n : (type == 1 ? n / 2 : n * 4);
     if (hipMemcpy(q, qp, qb, hipMemcpyDeviceToHost) != hipSuccess) return SNL_EDEVICE;
     if (type != 2 && s && hipMemcpy(s, sp, n / 32 * 4, hipMemcpyDeviceToHost) != hipSuccess) return SNL_EDEVICE;
+    return SNL_OK;
+}
+
+int snl_tensor_zero_rows(snl_engine* e, int layer, int kind, int first) {
+    if (!e) return SNL_EARG;
+    e->err.clear();
+    int type, rows, cols;
+    const float* sp;
+    const QW* cw = nullptr;
+    const void* qp = find_tensor(e, layer, kind, &type, &rows, &cols, &sp, &cw);
+    if (!qp || !cw || type == 2 || first < 0 || first > rows) return e->fail(SNL_EARG, "zero_rows: bad tensor or row");
+    QW& w = const_cast<QW&>(*cw);
+    ++e->epoch;
+    if (hipStreamSynchronize(e->stream) != hipSuccess) return e->fail(SNL_EDEVICE, "zero_rows: device error");
+    const size_t nb = (size_t)cols / 32;
+    if (!w.packed) {  // row-major scales
+        if (first < rows && hipMemset(w.s + (size_t)first * nb, 0, (size_t)(rows - first) * nb * 4) != hipSuccess)
+            return e->fail(SNL_EDEVICE, "zero_rows: memset failed");
+        return SNL_OK;
+    }
+    PackGeom g;
+    if (!pack_geom(w.quant, rows, cols, w.inter, &g)) return e->fail(SNL_EDEVICE, "zero_rows: no tile order");
+    std::vector<float> hs(g.s_floats);
+    if (hipMemcpy(hs.data(), w.s, g.s_floats * 4, hipMemcpyDeviceToHost) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "zero_rows: scale readback failed");
+    for (int T = 0; T < g.tiles; ++T)
+        for (int S = 0; S < g.nss; ++S)
+            for (int lane = 0; lane < 64; ++lane) {
+                const int row = pack_row(g, T, lane & 15);
+                if (row >= first)
+                    for (int u = 0; u < g.U; ++u) hs[pack_scale(g, T, S, lane, u)] = 0.0f;
+            }
+    if (hipMemcpy(w.s, hs.data(), g.s_floats * 4, hipMemcpyHostToDevice) != hipSuccess)
+        return e->fail(SNL_EDEVICE, "zero_rows: scale upload failed");
+    if (w.pq) {  // the prefill GEMM's panel copy, packed again from the reference layout
+        const size_t n = (size_t)rows * cols, qn = w.quant == 0 ? n : n / 2;
+        std::vector<uint8_t> hq(qn);
+        std::vector<float> rs(n / 32);
+        if (int rc = snl_tensor_read(e, layer, kind, hq.data(), rs.data())) return e->fail(rc, "zero_rows: readback failed");
+        void* tq = nullptr;
+        float* ts = nullptr;
+        int rc = SNL_OK;
+        if (hipMalloc(&tq, qn) != hipSuccess || hipMalloc((void**)&ts, n / 32 * 4) != hipSuccess)
+            rc = e->fail(SNL_ENOMEM, "zero_rows: staging allocation failed");
+        else if (hipMemcpy(tq, hq.data(), qn, hipMemcpyHostToDevice) != hipSuccess ||
+                 hipMemcpy(ts, rs.data(), n / 32 * 4, hipMemcpyHostToDevice) != hipSuccess ||
+                 launch_panel_pack(w.quant, rows, cols, tq, ts, w.pq, w.ps, e->stream) ||
+                 hipStreamSynchronize(e->stream) != hipSuccess)
+            rc = e->fail(SNL_EDEVICE, "zero_rows: panel repack failed");
+        hipFree(tq);
+        hipFree(ts);
+        return rc;
+    }
     return SNL_OK;
 }
 

@@ -153,8 +153,9 @@ struct Pick {
     uint32_t _pad;
 };
 // One greedy speculative step's outcome, posted to pinned host memory by spec_next.
+constexpr uint32_t kSpecRopeRange = 1u;
 struct SpecOut {
-    uint32_t seq, draft, accepted, _pad;
+    uint32_t seq, draft, accepted, flags;  // flags: kSpecRopeRange when a position ran past rope_tab
     Pick picks[2];
 };
 // After a speculative step's verify (src/worker.rs:236-255, greedy): accept when the verify's first

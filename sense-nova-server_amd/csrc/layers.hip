@@ -320,10 +320,13 @@ __global__ __launch_bounds__(256) void spec_next_kernel(SpecArgs a) {
     const bool acc = p0.token == d;
     const int adv = acc ? 2 : 1;
     const uint32_t nrope = rope + (uint32_t)adv;
+    // a position past the table (it holds ctx + 4 rows, and decode positions stay below the
+    // context) reads the last row and is reported through the outcome's flags
     auto tab = [&](uint32_t p, int f) {
         const uint32_t r = p < (uint32_t)a.rope_rows ? p : (uint32_t)a.rope_rows - 1;
         return *reinterpret_cast<const float2*>(a.rope_tab + ((size_t)r * SNL_ROPE_MAX + f) * 2);
     };
+    const bool rope_out = nrope + 1u >= (uint32_t)a.rope_rows;
     // rotary cos / sin: threads 0-127 the verify's two rows, 128-255 the draft's two rows
     {
         const int row = (tid >> 6) & 1, f = tid & 63;
@@ -372,7 +375,7 @@ __global__ __launch_bounds__(256) void spec_next_kernel(SpecArgs a) {
         o.seq = seq;
         o.draft = d;
         o.accepted = acc ? 1u : 0u;
-        o._pad = 0u;
+        o.flags = rope_out ? kSpecRopeRange : 0u;
         o.picks[0] = p0;
         o.picks[1] = p1;
         a.ring[seq % (uint32_t)a.ring_n] = o;

@@ -515,14 +515,19 @@ int snl_decoder_steps(snl_decoder* d, int steps, uint32_t* out, float* gaps, int
                 break;
         }
         ahead = false;
-        if (i + 1 < steps && (rc = snl::engine_spec_ahead(e, &ahead))) break;
+        // a failure to queue step i + 1 still waits for and applies step i, so every queued step
+        // has completed and the decoder's state follows the device's before the error returns
+        const int ahead_rc = i + 1 < steps ? snl::engine_spec_ahead(e, &ahead) : SNL_OK;
         snl::SpecOut o{};
         float draft_ms = 0.0f, verify_ms = 0.0f;
         if ((rc = snl::spec_finish(e, seq, &o, &draft_ms, &verify_ms))) break;
         spec_apply(d, o, draft_ms, verify_ms, o_out, o_gaps, &n);
         *n_out += n;
+        if ((rc = ahead_rc)) break;
     }
-    if (rc && ahead) {  // leave nothing queued behind an error
+    if (rc && ahead) {
+        // step i failed on the device with step i + 1 queued behind it: wait for that one too, so
+        // nothing stays queued; the engine then needs snl_reset, as after any device error
         snl::SpecOut o{};
         (void)snl::spec_finish(e, snl::engine_spec_seq(e) - 1u, &o, nullptr, nullptr);
     }

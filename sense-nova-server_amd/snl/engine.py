@@ -154,6 +154,7 @@ def lib() -> ctypes.CDLL:
         L.snl_sampler_distribution.argtypes = [vp, ctypes.c_int, u32p, f32p, ctypes.c_int, i32p]
         L.snl_tensor_info.argtypes = [vp, ctypes.c_int, ctypes.c_int, i32p, i32p]
         L.snl_tensor_read.argtypes = [vp, ctypes.c_int, ctypes.c_int, vp, f32p]
+        L.snl_tensor_zero_rows.argtypes = [vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.snl_buffer_read.argtypes = [vp, ctypes.c_int, vp, ctypes.c_size_t]
         L.snl_buffer_size.restype = ctypes.c_size_t
         L.snl_buffer_size.argtypes = [vp, ctypes.c_int]
@@ -338,6 +339,11 @@ class Engine:
         s = np.zeros(r * c // 32, np.float32)
         self._check(lib().snl_tensor_read(self.h, layer, kind, q.ctypes.data, _ptr(s, f32p)))
         return qt, q.reshape(r, -1), s.reshape(r, -1)
+
+    def zero_rows(self, layer: int, kind: int, first: int) -> None:
+        """Zero the block scales of rows first.. of a quantised matrix (those rows dequantise to 0):
+        a head whose argmax is confined to its first rows, as the oracle's zero_rows."""
+        self._check(lib().snl_tensor_zero_rows(self.h, layer, kind, first))
 
     def buffer(self, bid: int) -> np.ndarray:
         n = lib().snl_buffer_size(self.h, bid)

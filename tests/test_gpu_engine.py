@@ -443,3 +443,53 @@ def test_long_prefill_matches_decode_feed(snl_mod):
         assert np.abs(st_a - st_b).max() / np.abs(st_b).max() < 1e-2
     finally:
         e.close()
+
+
+@pytest.mark.parametrize("n", [512, 1024])
+def test_draft_after_full_prefill_chunk(snl_mod, oracle, n):
+    """A prompt whose last prefill pass is a full 512 rows leaves the first draft at hidden row 512;
+    the two-row draft pass then also reads row 513 (its padding row), which the hidden buffer holds.
+    The speculative stream must equal the oracle's and the stream without MTP."""
+    cfg = snl_mod.tiny_config()
+    print(f"draft after a full chunk: prompt {n}", flush=True)
+    g = snl_mod.Engine(cfg, seed=29, quant=0, ctx=n + 80)
+    o = oracle.Engine(cfg, seed=29, quant=0, ctx=n + 80, max_m=g.prefill_chunk)
+    try:
+        prompt = _prompt(n, cfg.vocab, seed=n)
+        rg = g.generate(prompt, 24, True)
+        off = g.generate(prompt, 24, False)
+        ro = o.generate(prompt, 24, True)
+        assert rg["tokens"] == off["tokens"]
+        matched = _compare_streams(rg["tokens"], ro["tokens"], ro["gaps"])
+        if matched == 24:
+            assert (rg["drafted"], rg["accepted"]) == (ro["drafted"], ro["accepted"])
+    finally:
+        g.close()
+        o.close()
+
+
+def test_decode_cost_follows_position(snl_mod):
+    """Decode passes size their attention launches by the context bucket of the live position
+    (2048 * 2^k keys, capped at the allocated context), not by the allocated context.  An engine
+    sized for 16384 positions and one sized for 2200 must give bitwise the same tokens, counts,
+    logits and recurrent state across the 2048-key bucket edge (2048 -> 4096 keys on one, 2048 ->
+    2200 on the other), with MTP on."""
+    cfg = snl_mod.tiny_config()
+    n = 2030
+    prompt = _prompt(n, cfg.vocab, seed=43)
+    res = []
+    for ctx in (16384, 2200):
+        print(f"position-sized attention: ctx {ctx}", flush=True)
+        e = snl_mod.Engine(cfg, seed=31, quant=0, ctx=ctx)
+        try:
+            r = e.generate(prompt, 40, True)
+            pos = e.pos
+            lg, _ = e.forward([5, 6], [[pos] * 3, [pos + 1] * 3], logit_rows=2)
+            res.append((r["tokens"], r["drafted"], r["accepted"], pos, lg, e.buffer(3)))
+        finally:
+            e.close()
+    a, b = res
+    assert a[3] > 2048 + 4
+    assert a[0] == b[0] and a[1:4] == b[1:4]
+    assert np.array_equal(a[4], b[4])
+    assert np.array_equal(a[5], b[5])

@@ -124,6 +124,67 @@ def test_nine_b_matches_oracle(big, oracle):
         o.close()
 
 
+@pytest.mark.parametrize("quant", [0, 1], ids=["q8", "q4"])
+def test_nine_b_accept_branch_matches_oracle(snl_mod, oracle, quant):
+    """The accept branch of the decode loop at 9B (src/worker.rs:236-246).  Random weights never
+    accept a draft, so the LM head (shared by the main model and the MTP head) is confined to its
+    first rows on both sides: block scales zeroed from row 4 on, so those logits are exactly 0 and
+    the first of them wins whenever rows 0-3 are all negative.  Greedy speculative decoding through
+    the captured step graph (its device-side accept decision, the 2-pair draft over the verify's
+    hidden rows, the rotary and slot bookkeeping), once step by step and once with every step
+    queued ahead from the records the previous step wrote on the device: tokens, drafted and
+    accepted counts and the DeltaNet state after equal the oracle's (ties aside)."""
+    cfg = snl_mod.nine_b_config()
+    print(f"9B accept branch quant={quant}", flush=True)
+    g = snl_mod.Engine(cfg, seed=17, quant=quant, ctx=256)
+    o = oracle.Engine(cfg, seed=17, quant=quant, ctx=256, max_m=64)
+    try:
+        g.zero_rows(-1, snl_mod.engine.K_LM_HEAD, 4)
+        o.zero_rows(-1, oracle.K_LM_HEAD, 4)
+        n, steps = 40, 12
+        prompt = _prompt(n, cfg.vocab, seed=19)
+        ro = o.generate(prompt, steps, True)
+        st_o = o.buf(3, g.buffer(3).size)
+        print(f"9B accept oracle: {ro['tokens']} drafted {ro['drafted']} accepted {ro['accepted']}", flush=True)
+        assert ro["accepted"] > 0
+        rg = g.generate(prompt, steps, True)
+        st_g = g.buffer(3)
+        print(f"9B accept gpu: {rg['tokens']} drafted {rg['drafted']} accepted {rg['accepted']}", flush=True)
+        matched = n_match = min(len(rg["tokens"]), len(ro["tokens"]))
+        for i in range(n_match):
+            if rg["tokens"][i] != ro["tokens"][i]:
+                assert ro["gaps"][i] < TIE, f"divergence at {i} with oracle gap {ro['gaps'][i]}"
+                matched = i
+                break
+        if matched == n_match:
+            assert len(rg["tokens"]) == len(ro["tokens"])
+            assert (rg["drafted"], rg["accepted"]) == (ro["drafted"], ro["accepted"])
+            assert _rel(st_g, st_o) < 1e-2
+        assert rg["accepted"] > 0
+        # the same loop with every step queued ahead equals single steps: tokens, counts, state
+        res = []
+        for many in (False, True):
+            d = g.decoder(prompt, spec=True)
+            toks = []
+            for k in (1, 4, 3):
+                if many:
+                    toks += d.steps(k)
+                else:
+                    for _ in range(k):
+                        toks += d.step()
+            st = d.stats()
+            res.append((toks, st["drafted"], st["accepted"], g.pos, g.buffer(2), g.buffer(3)))
+            d.close()
+        one, queued = res
+        print(f"9B accept steps: {one[0]} drafted {one[1]} accepted {one[2]}", flush=True)
+        assert one[2] > 0
+        assert queued[:4] == one[:4]
+        assert np.array_equal(queued[4], one[4]) and np.array_equal(queued[5], one[5])
+    finally:
+        g.close()
+        o.close()
+
+
 def test_mtp_on_off_identical_full_size(big):
     """The 9B workload itself: a 1024-token prompt (two prefill chunks), 512 greedy tokens with the
     MTP head drafting and without it, byte-identical."""
