@@ -7,9 +7,15 @@ weights drawn on the device, batch 1, a 1024-token random prompt, then greedy MT
 A step is one speculative decode step: MTP draft + 2-token verify through the weights + greedy
 acceptance (rollback on reject).  W untimed warmup steps, then exactly K timed steps between two
 device synchronisations; value = tokens emitted in those K steps / their wall time.  The steps run
-through the decoder's native multi-step call (snl_decoder_steps, 100 steps a call): each step is
+through the decoder's native multi-step call (snl_decoder_steps, 20 steps a call): each step is
 queued on the device, its records written there by the previous step's accept decision, before
-the host reads the previous step's outcome.
+the host reads the previous step's outcome.  ms_per_step_median is the median over those calls.
+
+The headline engine is allocated for 32768 positions, the reference's default context; decode
+passes size their attention by the live position, so config.sized_engine (the same run on an
+engine allocated for the run's own positions) should agree with it.  Random weights never accept
+a draft, so config.accept_leg repeats the run with the LM head confined to its first rows (block
+scales zeroed from row 4): drafts are then accepted, and tokens per step = 1 + acceptance.
 
 roofline: the dominant kernel is the verify pass's gate_up GEMV (Q8_0, M=2, N=24576, K=4096 with
 the fused mHC/RMSNorm prologue and SwiGLU epilogue, 43% of the pass's weight bytes).  After the
@@ -43,6 +49,8 @@ sys.path.insert(0, os.path.join(REPO, "sense-nova-server_amd"))
 METRIC = "9B Q8_0 MTP greedy decode tok/s (1 GPU); Q8 GEMV GB/s vs HBM peak"
 HBM_PEAK_GBS = 8000.0
 PROMPT = 1024
+REF_CTX = 32768  # sensenova-loop --ctx default (src/main.rs:178-180)
+STEP_CHUNK = 20  # timed steps per native decoder call
 ROOFLINE_KERNEL = "mgemv_kernel<0, 1, 3, 2, 4, 2, 1>"  # Q8_0, one token pair, SwiGLU epilogue, mHC input, U=4, UPT=2, chunk-major
 # HBM traffic of the roofline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs (see summarize_pmc);
 # reported only while the kernel sources hash to the value recorded with it.
@@ -410,6 +418,51 @@ def long_context(snl, np) -> int:
     return 0
 
 
+def decode_leg(snl, cfg, prompt, ctx: int, warmup: int, steps: int, name: str, confine_head: bool = False):
+    """Create the 9B Q8_0 engine (seed 1) for `ctx` positions, prefill the prompt, run `warmup`
+    untimed steps, then `steps` timed greedy MTP steps between device synchronisations, in native
+    calls of up to STEP_CHUNK steps; the median is over those calls' ms per step.  Returns the open
+    engine and the leg's figures."""
+    import torch
+
+    t0 = time.perf_counter()
+    eng = snl.Engine(cfg, seed=1, quant=0, ctx=ctx)
+    if confine_head:
+        eng.zero_rows(-1, snl.engine.K_LM_HEAD, 4)
+    log(f"[{name}] engine created in {time.perf_counter() - t0:.1f}s (ctx {ctx})")
+    t0 = time.perf_counter()
+    dec = eng.decoder(prompt, spec=True)
+    prefill_s = time.perf_counter() - t0
+    log(f"[{name}] prefill of {len(prompt)} tokens (+ MTP catch-up) in {prefill_s:.3f}s")
+    dec.steps(warmup)
+    st0 = dec.stats()
+    torch.cuda.synchronize()
+    emitted, per = 0, []
+    t0 = time.perf_counter()
+    for i0 in range(0, steps, STEP_CHUNK):
+        k = min(STEP_CHUNK, steps - i0)
+        tc = time.perf_counter()
+        emitted += len(dec.steps(k))
+        per.append((time.perf_counter() - tc) / k * 1e3)
+        if (i0 + k) % 100 == 0 or i0 + k == steps:
+            log(f"[{name}] step {i0 + k}/{steps}")
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    st1 = dec.stats()
+    dec.close()
+    drafted = st1["drafted"] - st0["drafted"]
+    accepted = st1["accepted"] - st0["accepted"]
+    per.sort()
+    median = per[len(per) // 2] if len(per) % 2 else 0.5 * (per[len(per) // 2 - 1] + per[len(per) // 2])
+    res = {"emitted": emitted, "dt": dt, "drafted": drafted, "accepted": accepted, "prefill_s": prefill_s,
+           "draft_ms": (st1["draft_s"] - st0["draft_s"]) / max(drafted, 1) * 1e3,
+           "verify_ms": (st1["verify_s"] - st0["verify_s"]) / max(drafted, 1) * 1e3, "median_ms": median}
+    log(f"[{name}] {steps} steps: {emitted} tokens in {dt:.3f}s ({emitted / dt:.1f} tok/s), acceptance "
+        f"{accepted}/{drafted}, {dt / steps * 1e3:.4f} ms/step (median {median:.4f}), verify "
+        f"{res['verify_ms']:.3f} ms")
+    return eng, res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -468,36 +521,14 @@ def main() -> int:
             json.dump({"pos": int(args.pmc_attention[0])}, fh)
         return pmc_attention(snl, np, int(args.pmc_attention[0]))
     cfg = snl.nine_b_config()
-    ctx = PROMPT + 2 * (args.warmup + args.steps) + args.profile_passes + 64
-    t0 = time.perf_counter()
-    eng = snl.Engine(cfg, seed=1, quant=0, ctx=ctx)
-    log(f"engine created in {time.perf_counter() - t0:.1f}s (ctx {ctx})")
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, PROMPT).tolist()
-    t0 = time.perf_counter()
-    dec = eng.decoder(prompt, spec=True)
-    prefill_s = time.perf_counter() - t0
-    log(f"prefill of {PROMPT} tokens (+ MTP catch-up) in {prefill_s:.3f}s")
-
-    dec.steps(args.warmup)
-    st0 = dec.stats()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    emitted = 0
-    # native loop: each step queued on the device before the previous one is read
-    for i0 in range(0, args.steps, 100):
-        k = min(100, args.steps - i0)
-        emitted += len(dec.steps(k))
-        log(f"step {i0 + k}/{args.steps}")
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    st1 = dec.stats()
-    drafted = st1["drafted"] - st0["drafted"]
-    accepted = st1["accepted"] - st0["accepted"]
-    draft_ms = (st1["draft_s"] - st0["draft_s"]) / max(drafted, 1) * 1e3
-    verify_ms = (st1["verify_s"] - st0["verify_s"]) / max(drafted, 1) * 1e3
-    log(f"timed {args.steps} steps: {emitted} tokens in {dt:.3f}s, acceptance {accepted}/{drafted}, "
-        f"draft {draft_ms:.3f} ms, verify {verify_ms:.3f} ms")
-    dec.close()
+    # headline: the engine sized as the reference sizes it by default (--ctx 32768)
+    eng, lg = decode_leg(snl, cfg, prompt, REF_CTX, args.warmup, args.steps, "headline")
+    emitted, dt, steps = lg["emitted"], lg["dt"], args.steps
+    drafted, accepted = lg["drafted"], lg["accepted"]
+    draft_ms, verify_ms, prefill_s = lg["draft_ms"], lg["verify_ms"], lg["prefill_s"]
+    log(f"timed {steps} steps: {emitted} tokens in {dt:.3f}s, acceptance {accepted}/{drafted}, "
+        f"draft {draft_ms:.3f} ms, verify {verify_ms:.3f} ms, median step {lg['median_ms']:.4f} ms")
 
     # live per-kernel timing: verify passes launched op by op (HIP events on the engine stream)
     per_op = {}
@@ -545,6 +576,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "ms_per_step_median": round(lg["median_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -552,7 +584,9 @@ def main() -> int:
         "data": "synthetic (random-init weights, uniform random prompt ids)",
         "config": {
             "workload": "SenseNova-Loop-9B shape, Q8_0 (f32 block scales), batch 1, 1024-token prompt, "
-                        "greedy MTP decode (draft 1 + verify 2)",
+                        "greedy MTP decode (draft 1 + verify 2), engine sized for the reference's default "
+                        "context (32768)",
+            "ctx": REF_CTX,
             "prompt_tokens": PROMPT,
             "tokens_emitted": emitted,
             "acceptance": round(accepted / max(drafted, 1), 4),
@@ -579,6 +613,22 @@ def main() -> int:
         "cpu_baseline": None,
     }
     eng.close()
+    # the same workload on an engine sized for the run alone (decode cost follows the position)
+    sized_ctx = PROMPT + 2 * (args.warmup + args.steps) + 64
+    e2, sz = decode_leg(snl, cfg, prompt, sized_ctx, args.warmup, args.steps, "sized")
+    e2.close()
+    result["config"]["sized_engine"] = {"ctx": sized_ctx, "ms_per_step": round(sz["dt"] / args.steps * 1e3, 4),
+                                        "ms_per_step_median": round(sz["median_ms"], 4),
+                                        "verify_ms": round(sz["verify_ms"], 4)}
+    # the accept branch: the LM head confined to its first rows (block scales zeroed from row 4),
+    # so drafts are accepted; tokens per step = 1 + acceptance
+    e3, acc = decode_leg(snl, cfg, prompt, REF_CTX, args.warmup, args.steps, "accept", confine_head=True)
+    e3.close()
+    result["config"]["accept_leg"] = {
+        "head": "LM head rows 4.. zeroed (argmax confined to 5 tokens)",
+        "acceptance": round(acc["accepted"] / max(acc["drafted"], 1), 4),
+        "tok_s": round(acc["emitted"] / acc["dt"], 3), "ms_per_step": round(acc["dt"] / args.steps * 1e3, 4),
+        "draft_ms": round(acc["draft_ms"], 4), "verify_ms": round(acc["verify_ms"], 4)}
     if args.gemv_reps > 0:
         result["config"]["gemv_microbench"] = gemv_microbench(snl, args.gemv_reps)
     if not args.no_cpu_baseline:

@@ -272,11 +272,11 @@ def _attention_vs_oracle(torch_cuda, K, oracle, n_heads, n_kv, m, pos0, ctx):
     K.attention(_dev(torch, proj), stride, qbuf, dk, dv, _dev(torch, norms), out, partial, n_heads, n_kv, 64, 1e7,
                 1e-6, (11, 11, 10), ctx, m, pos0, rpos[:, :3])
     torch.cuda.synchronize()
-    # RoPE angles are pos * powf(theta, -2i/64): a 1-ulp difference of powf between the GPU and
-    # libm moves an angle by up to pos * 2^-24 radians, so q/k and the output are held to
-    # max(1e-3, 2 * pos * 2^-24) of their largest value (8.3e-3 at position 70000; the bound for
-    # logits and state is 1e-2).
-    tol = max(1e-3, 2.0 * (pos0 + m) * 2.0 ** -24)
+    # The rotary cos / sin come with the step record, formed on the host with the same libm calls
+    # as the oracle, so q / k differ only by the order of the norm's sum (measured 1e-7 relative
+    # up to position 70000; one f16 key word may round the other way) and the output by the
+    # order of the softmax sums (measured 8e-7).  Held to 1e-3 of the largest value.
+    tol = 1e-3
 
     def rel(a, b):
         return float(np.abs(a - b).max() / np.abs(b).max())
