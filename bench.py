@@ -115,12 +115,13 @@ OP_KERNELS = {"attention": ["attend_kernel<2>", "combine_kernel"],
               "pick": ["pick_partial_kernel", "pick_final_kernel"]}
 
 
-def pmc_decode(snl, np, ops_out: str, passes: int = 3) -> int:
-    """Counter workload: the bench's 9B Q8_0 engine and 1024-token prompt, 6 graph-launched MTP
-    steps, then `passes` verify passes launched op by op (rolled back).  The op sequence of those
-    passes goes to ops_out, so the per-dispatch counters and trace can be labelled by op."""
+def pmc_decode(snl, np, ops_out: str, passes: int = 3, quant: int = 0) -> int:
+    """Counter workload: the bench's 9B engine (Q8_0, or Q4_0 with quant 1) and 1024-token prompt, 6
+    graph-launched MTP steps, then `passes` verify passes launched op by op (rolled back).  The op
+    sequence of those passes goes to ops_out, so the per-dispatch counters and trace can be labelled
+    by op."""
     cfg = snl.nine_b_config()
-    eng = snl.Engine(cfg, seed=1, quant=0, ctx=PROMPT + 64)
+    eng = snl.Engine(cfg, seed=1, quant=quant, ctx=PROMPT + 64)
     prompt = np.random.default_rng(1).integers(0, cfg.vocab, PROMPT).tolist()
     dec = eng.decoder(prompt, spec=True)
     for _ in range(6):
@@ -484,6 +485,11 @@ def main() -> int:
                     help="counter workload: a few decode steps and op-by-op verify passes; writes the op sequence")
     ap.add_argument("--pmc-attention", nargs=2, metavar=("POS", "INFO_JSON"),
                     help="counter workload: decode attention alone at cache position POS")
+    ap.add_argument("--quant", type=int, default=0, choices=(0, 1),
+                    help="weights of the --pmc-decode workload: 0 Q8_0, 1 Q4_0")
+    ap.add_argument("--gemm-probe", type=int, metavar="QUANT", default=-1,
+                    help="counter workload: the prefill GEMM alone on the gate_up shape (M 512, N 24576, "
+                         "K 4096), Q8_0 (0) or Q4_0 (1), 20 launches")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only copy a buffer of this many MiB 4 times on the GPU and exit: the known-size "
                          "kernel that HBM byte counters are calibrated against")
@@ -515,7 +521,13 @@ def main() -> int:
     if args.long_context:
         return long_context(snl, np)
     if args.pmc_decode:
-        return pmc_decode(snl, np, args.pmc_decode)
+        return pmc_decode(snl, np, args.pmc_decode, quant=args.quant)
+    if args.gemm_probe >= 0:
+        cfg = snl.nine_b_config()
+        ms = snl.kernels.gemm_time(args.gemm_probe, 2 * cfg.intermediate, cfg.hidden, 512, reps=20)
+        log(f"prefill GEMM {'Q8_0' if args.gemm_probe == 0 else 'Q4_0'} 512 x {2 * cfg.intermediate} x "
+            f"{cfg.hidden}: {ms * 1e3:.1f} us per launch")
+        return 0
     if args.pmc_attention:
         with open(args.pmc_attention[1], "w") as fh:
             json.dump({"pos": int(args.pmc_attention[0])}, fh)

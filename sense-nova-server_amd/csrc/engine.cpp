@@ -467,6 +467,8 @@ struct snl_engine {
             if (n < 1 || n > kPartBlocks) return SNL_EDEVICE;
             part_n = n;
         }
+        float *no = norm_out, *nl = norm_last;  // (cleared whether or not this call launches)
+        norm_out = norm_last = nullptr;
         if (!op(name, gemv_bytes(w, M, epi, cfg.intermediate))) return 0;
         GemvArgs g{};
         g.packed = w.packed ? 1 : 0;
@@ -495,9 +497,12 @@ struct snl_engine {
         g.next_w = mr.next;
         g.rpart = mr.next ? mhc_part : nullptr;
         g.expand = mr.expand;
+        g.norm_out = no;
+        g.norm_last = nl;
         return launch_gemv(g, w.quant, M, stream);
     }
     int consumed_n = 0;  // partial count a NORM_MHC launch adds up
+    float *norm_out = nullptr, *norm_last = nullptr;  // the next gemv() call's normed-row outputs
     int norm(const float* xin, int x_stride, const int32_t* row_base, int mode, const float* w, float* out,
              int first, int count, float* last_copy = nullptr) {
         NormArgs a{};
@@ -802,12 +807,19 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
                    GEMV_PLAIN, nullptr, nullptr,
                    MhcRole{mhc ? L.mhc_ffn.p : nullptr, leave ? layers[ln].mhc_attn.p : nullptr, next_start ? 1 : 0});
     }
-    // the last row's output also lands in hlast (the hidden carried to the next pass)
-    rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M, hlast);
-    if (rows > 0) {
-        rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
-        if (op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream, hd_picks);
+    // the final norm into hid rows 1..M, the last row's output also into hlast (the hidden carried
+    // to the next pass): with logits for every row, in the LM head's prologue (its block 0 stores
+    // the normed rows), else on its own
+    if (rows == M) {
+        norm_out = hid + h;
+        norm_last = hlast;
+        rc |= gemv("gemv_lm_head", lm_head, x, 2 * h, logits, c.vocab, rows, GEMV_STORE, 0, GEMV_NORM, final_norm.p);
+    } else {
+        rc |= norm(x, 2 * h, nullptr, 0, final_norm.p, hid + h, 0, M, hlast);
+        if (rows > 0)
+            rc |= gemv("gemv_lm_head", lm_head, hid + (size_t)(M - rows + 1) * h, h, logits, c.vocab, rows, GEMV_STORE);
     }
+    if (rows > 0 && op("pick", 0.0)) rc |= launch_pick(logits, c.vocab, rows, pick_scratch, d_picks, stream, hd_picks);
     mark("end", 0.0);
     return rc ? SNL_EDEVICE : SNL_OK;
 }
@@ -816,10 +828,12 @@ int snl_engine::record_forward(int M, int rows, int ckpt) {
 int snl_engine::record_mtp(int M, int draft) {
     const snl_config& c = cfg;
     int rc = 0;
-    if (op("embed", 0.0)) rc |= launch_embed(d_mstep, (const int8_t*)embed.q, embed.s, c.vocab, h, mx, M, stream);
-    // x = fc_e(norm_e(emb)) + fc_h(norm_h(hid[r0..])); fc_e reads xn, since it writes mx
-    rc |= norm(mx, 2 * h, nullptr, 0, norm_e.p, xn, 0, M);
-    rc |= gemv("gemv_fc_e", fc_e, xn, h, mx, 2 * h, M, GEMV_STORE);
+    // x = fc_e(norm_e(emb)) + fc_h(norm_h(hid[r0..])): the embedding rows go to xn (fc_e writes mx),
+    // and norm_e is fc_e's prologue
+    if (op("embed", 0.0))
+        rc |= launch_embed(d_mstep, (const int8_t*)embed.q, embed.s, c.vocab, h, xn, M, stream, nullptr, nullptr,
+                           nullptr, true);
+    rc |= gemv("gemv_fc_e", fc_e, xn, h, mx, 2 * h, M, GEMV_STORE, 0, GEMV_NORM, norm_e.p);
     rc |= gemv("gemv_fc_h", fc_h, hid, h, mx, 2 * h, M, GEMV_ADD, 0, GEMV_NORM, norm_h.p, &d_mstep->r0);
     rc |= gemv("gemv_mtp_qkv", m_qkv, mx, 2 * h, proj, attn_proj_rows, M, GEMV_STORE, 0, GEMV_NORM, m_in_ln.p);
     AttnArgs a = attn_args(d_mstep, m_kc, m_vc, m_qk_norm.p);

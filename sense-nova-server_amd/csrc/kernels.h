@@ -49,6 +49,10 @@ struct GemvArgs {
     const float* next_w; // ADD / MHC epilogue: router of the next site, whose partials this launch
     float* rpart;        //   writes to rpart[M][9][gridDim.x] (null: none)
     int expand;          //   and, at the start of the mHC range, stream 1 := stream 0 first
+    // NORM prologue of a tile-major launch (the vocabulary head): block 0 also stores the normed
+    // token rows, RMSNorm(x) * (1 + w), to norm_out [M][K] and the last of them to norm_last
+    float* norm_out;
+    float* norm_last;
 };
 // grid size of launch_gemv over tile-order weights (the partial count a producer leaves)
 int mgemv_blocks(int quant, int N, int K, int inter);
@@ -106,12 +110,13 @@ int launch_mgemm(const GemmArgs& a, int quant, hipStream_t s);
 
 // ---------------------------------------------------------------- layers (layers.hip)
 // x[m, 0:h] = dequant(embed[tokens[m]]), x[m, h:2h] = 0 (src/engine.rs:777-790); with carry_src, one
-// more block copies h floats from carry_src to carry_dst in the same launch
+// more block copies h floats from carry_src to carry_dst in the same launch.  one_stream: rows of h
+// floats (x[m*h ..]) and no second stream.
 struct Pick;
 // draft: the MTP draft's pick, the token of the rows step->draft_rows names
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
                  hipStream_t s, const float* carry_src = nullptr, float* carry_dst = nullptr,
-                 const Pick* draft = nullptr);
+                 const Pick* draft = nullptr, bool one_stream = false);
 
 // out[r] = rmsnorm(branch input of row first+r) * (one + w) for r < count (layers.wgsl:46-73).
 // mode 1 mixes the two streams with coef[row][0..1].  Row `row` of x starts at

@@ -17,7 +17,7 @@ namespace {
 __global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const int8_t* __restrict__ eq,
                                                      const float* __restrict__ es, int vocab, int h,
                                                      float* __restrict__ x, int M, const float* carry_src,
-                                                     float* carry_dst, const Pick* draft) {
+                                                     float* carry_dst, const Pick* draft, int one_stream) {
     const int m = blockIdx.x;
     if (m == M) {  // the carried row (launched only with carry_src)
         for (int i = threadIdx.x; i * 4 < h; i += 256)
@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const i
     if (tok >= (uint32_t)vocab) tok = 0;  // the host rejects out-of-range ids before launching
     const int8_t* q = eq + (size_t)tok * h;
     const float* s = es + (size_t)tok * (h / 32);
-    float* xr = x + (size_t)m * 2 * h;
+    float* xr = x + (size_t)m * (one_stream ? 1 : 2) * h;
     // piece p: 16 consecutive quants (half of quant block p / 2), one 16-byte load and its scale,
     // both issued before any store
     for (int p = threadIdx.x; p * 16 < h; p += 256) {
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const StepDev* step, const i
             const uint32_t v = wd[k];
             o[k] = make_float4((float)(int8_t)(v & 0xffu) * sc, (float)(int8_t)((v >> 8) & 0xffu) * sc,
                                (float)(int8_t)((v >> 16) & 0xffu) * sc, (float)(int8_t)(v >> 24) * sc);
-            z[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (!one_stream) z[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     }
 }
@@ -396,13 +396,13 @@ inline int last_error() { return hipGetLastError() == hipSuccess ? 0 : -2; }
 }  // namespace
 
 int launch_embed(const StepDev* step, const int8_t* eq, const float* es, int vocab, int h, float* x, int M,
-                 hipStream_t s, const float* carry_src, float* carry_dst, const Pick* draft) {
+                 hipStream_t s, const float* carry_src, float* carry_dst, const Pick* draft, bool one_stream) {
     if (M < 1 || M > SNL_MAX_M || h % 32 || (reinterpret_cast<uintptr_t>(eq) & 15) ||
         (reinterpret_cast<uintptr_t>(x) & 15) || (carry_src && !carry_dst) ||
         (reinterpret_cast<uintptr_t>(carry_src) & 15) || (reinterpret_cast<uintptr_t>(carry_dst) & 15))
         return -1;
     hipLaunchKernelGGL(embed_kernel, dim3(M + (carry_src ? 1 : 0)), dim3(256), 0, s, step, eq, es, vocab, h, x, M,
-                       carry_src, carry_dst, draft);
+                       carry_src, carry_dst, draft, one_stream ? 1 : 0);
     return last_error();
 }
 

@@ -586,6 +586,35 @@ __global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void m
 
     };
 
+    // NORM prologue with norm_out: block 0's staging threads store the normed rows themselves (the
+    // final norm of a decode pass, layers.wgsl:46-73), from their staged values and the sums of
+    // squares of every staging wave, added in wave order
+    auto store_norm_rows = [&]() {
+        if constexpr (PRO == GEMV_NORM) {
+            if (a.norm_out && blockIdx.x == 0 && stager) {
+#pragma unroll
+                for (int m = 0; m < 2 * P; ++m) {
+                    if (m >= M) continue;
+                    float ss = 0.0f;
+                    for (int w = sw0; w < nwv; ++w) ss = ss + ssq_s[w][m];
+                    const float of = 1.0f / sqrtf(ss / (float)K + a.eps);
+#pragma unroll
+                    for (int u = 0; u < UPT; ++u) {
+                        const int k8 = ts + u * nst;
+                        if (k8 >= K8) continue;
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const f32x4_t t = xa[m][u][hh];
+                            const float4 o = make_float4(t.x * of, t.y * of, t.z * of, t.w * of);
+                            reinterpret_cast<float4*>(a.norm_out + (size_t)m * K + k8 * 8)[hh] = o;
+                            if (a.norm_last && m == M - 1) reinterpret_cast<float4*>(a.norm_last + k8 * 8)[hh] = o;
+                        }
+                    }
+                }
+            }
+        }
+    };
+
     // ---- main loop ----
     f32x4_t acc[P];
 #pragma unroll
@@ -713,6 +742,7 @@ __global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void m
             side_lds();
             lds_barrier();
             sinkhorn();
+            store_norm_rows();
         } else {
             epilogue_loads();
             __builtin_amdgcn_s_barrier();
@@ -741,6 +771,7 @@ __global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void m
         issue(w2, s2, 2);
         lds_barrier();
         sinkhorn();
+        store_norm_rows();
         main_loop();
     }
 
@@ -1071,6 +1102,9 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
         return -1;
     if (a.pro == GEMV_NORM_MHC && (!a.site_w || !a.raw || !a.coef || !a.rin || a.rin_n < 1 || M > 2)) return -1;
     if (a.pro == GEMV_GNORM && (!a.rin || a.rin_n != kDeltaGroups || a.K % 128)) return -1;
+    if (a.norm_out && (a.pro != GEMV_NORM || (reinterpret_cast<uintptr_t>(a.norm_out) & 15) ||
+                       (reinterpret_cast<uintptr_t>(a.norm_last) & 15)))
+        return -1;
     if (a.epi == GEMV_MHC && !a.coef) return -1;
     if (a.rpart && (!a.next_w || (a.epi != GEMV_ADD && a.epi != GEMV_MHC) || (M & (M - 1)))) return -1;
     if (a.epi == GEMV_ADD && a.rpart && !a.expand) return -1;  // an ADD producer starts the mHC range
