@@ -11,8 +11,9 @@
 // close to the whole VALU budget at full HBM rate).  Both operands are exact:
 //   * quants become f16 exactly: Q8 bytes, stored in offset binary (q + 128), are paired with 0x64
 //     by v_perm (the f16 1024 + byte) and one packed f16 subtract of 1152 leaves q; Q4 nibbles are
-//     masked into the same f16 pattern in place (then 1032 is subtracted) or from the upper half
-//     of their byte (1024 + 16n, then times 1/16 minus 72);
+//     only masked, and read as f16 subnormals n * 2^-24 (low nibble of a byte) or 16n * 2^-24 (high
+//     nibble, whose token values are staged divided by 16); the offset 8 comes back per block as
+//     -8 * (the block's sum of staged token values), formed by the staging, after the MFMAs;
 //   * each token row x (f32) is split into two f16 parts, hi = f16(x) and lo = f16(x - hi), whose
 //     sum carries 22 significant bits; a power of two per token and superstep scales the part's
 //     largest |x| into [2^13, 2^14), so hi cannot overflow and small rows keep their bits.
@@ -124,9 +125,10 @@ __device__ __forceinline__ void opaque(f32x4_t& v) { asm volatile("" : "+v"(v));
 // Q8 order: elements 8i..8i+7.  Q4 order (word i): elements 8i + {0, 4, 1, 5, 2, 6, 3, 7}.
 // Q8: the packed bytes are offset binary (q + 128, packing.h); v_perm pairs each with 0x64, the f16
 // 1024 + byte, and one packed subtract of 1152 leaves q.  Q4: nibble pairs (i, i + 4) are masked
-// into the f16 pattern in place, 0x6400 | n = 1024 + n (subtract 1032), or from the upper half of
-// their byte, 0x6400 | 16n = 1024 + 16n (times 1/16 minus 72, one packed fma, exact): 9 vector
-// instructions per 8 weights.
+// in place (element i in the low half of a 16-bit lane, i + 4 in the high half), n from the low
+// nibble of a byte and 16n from the high one, and taken as they are, f16 subnormals n * 2^-24 and
+// 16n * 2^-24 (exact): 5 vector instructions per 8 weights.  The offset of 8 and the 2^24 are
+// applied per block after the MFMAs (Q4 block correction, stage and compute).
 template <int QT>
 __device__ __forceinline__ half8_t dequant8(const uint4& w, int i) {
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
@@ -139,13 +141,12 @@ __device__ __forceinline__ half8_t dequant8(const uint4& w, int i) {
         const half2_t p3 = as_h2(__builtin_amdgcn_perm(0x64646464u, u1, 0x04030402u)) - bias;
         return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     } else {
-        const half2_t bias = {(_Float16)1032.0f, (_Float16)1032.0f};
-        const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f}, b72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+        // the nibbles as they lie, read as f16 subnormals: n * 2^-24 for the low nibble of a byte, 16n *
+        // 2^-24 for the high one (whose token values are staged divided by 16); the MFMA's sum of n * x
+        // then becomes the block dot with 2^24 and the block's -8 * sum(x) (compute, below)
         const uint32_t v = wd[i], v8 = v >> 8;
-        const half2_t p0 = as_h2((v & 0x000F000Fu) | 0x64006400u) - bias;
-        const half2_t p1 = __builtin_elementwise_fma(as_h2((v & 0x00F000F0u) | 0x64006400u), s16, b72);
-        const half2_t p2 = as_h2((v8 & 0x000F000Fu) | 0x64006400u) - bias;
-        const half2_t p3 = __builtin_elementwise_fma(as_h2((v8 & 0x00F000F0u) | 0x64006400u), s16, b72);
+        const half2_t p0 = as_h2(v & 0x000F000Fu), p1 = as_h2(v & 0x00F000F0u);
+        const half2_t p2 = as_h2(v8 & 0x000F000Fu), p3 = as_h2(v8 & 0x00F000F0u);
         return half8_t{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
     }
 }
@@ -281,6 +282,10 @@ __global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void m
     constexpr int kRinSlots = 2 * P * 3 + kXtra;     // 1 KiB LDS slots per staging wave
     const unsigned rin_off = ((unsigned)(reinterpret_cast<unsigned char*>(mult_s) - lds) + (unsigned)P * nss * 8 + 15u) & ~15u;
     const unsigned rin_w = rin_off + (unsigned)(wave - sw0) * kRinSlots * 1024;  // this wave's slots
+    // Q4: the block corrections [P][nb][4 combos], -8 * (sum of the block's staged values, high-nibble
+    // ones times 16), after the router partial slots
+    float* const corr_s = reinterpret_cast<float*>(
+        lds + rin_off + (PRO == GEMV_NORM_MHC ? (unsigned)(nwv - sw0) * kRinSlots * 1024 : 0u));
     f32x4_t sb[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};  // the 8 router biases
     // NORM_MHC: xb is stream 1 of the row.  GNORM: gp holds the head's column-group partial sums
     // of squares.
@@ -520,18 +525,36 @@ __global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void m
                     const float v[8] = {xa[m][u][0].x, xa[m][u][0].y, xa[m][u][0].z, xa[m][u][0].w,
                                         xa[m][u][1].x, xa[m][u][1].y, xa[m][u][1].z, xa[m][u][1].w};
                     half8_t hi, lo;
+                    float shi = 0.0f, slo = 0.0f;  // Q4: the unit's staged values, high-nibble ones times 16
 #pragma unroll
                     for (int e8 = 0; e8 < 8; ++e8) {
-                        const float y = v[e8] * f;
+                        // Q4: an odd element (the high nibble of its byte) meets 16n, so it is staged / 16
+                        const float y = QT == 1 && (e8 & 1) ? v[e8] * f * 0.0625f : v[e8] * f;
                         const _Float16 hv = (_Float16)y;
+                        const _Float16 lv = (_Float16)(y - (float)hv);
                         const int pidx = a_pos<QT>(e8);
                         hi[pidx] = hv;
-                        lo[pidx] = (_Float16)(y - (float)hv);
+                        lo[pidx] = lv;
+                        if constexpr (QT == 1) {
+                            const float w = (e8 & 1) ? 16.0f : 1.0f;
+                            shi = shi + (float)hv * w;
+                            slo = slo + (float)lv * w;
+                        }
                     }
                     unsigned char* bp =
                         lds + ((size_t)(m >> 1) * nb + (k8 >> 2)) * 256 + (m & 1) * 128 + (k8 & 3) * 16;
                     *reinterpret_cast<half8_t*>(bp) = hi;
                     *reinterpret_cast<half8_t*>(bp + 64) = lo;
+                    if constexpr (QT == 1) {
+                        // the block's four units are four neighbouring lanes (all staged or none)
+                        shi = xor_sum<2>(xor_sum<1>(shi));
+                        slo = xor_sum<2>(xor_sum<1>(slo));
+                        if ((k8 & 3) == 0) {
+                            const float c = -8.0f;  // (exact: the sums are exact in f32)
+                            *reinterpret_cast<float2*>(corr_s + (((m >> 1) * nb + (k8 >> 2)) * 4 + (m & 1) * 2)) =
+                                make_float2(shi * c, slo * c);
+                        }
+                    }
                 }
             }
             if constexpr (PRO == GEMV_NORM || PRO == GEMV_NORM_MHC) {
@@ -666,6 +689,18 @@ __global__ __launch_bounds__(IL == 2 ? kRing4Waves * 64 : kMaxWaves * 64) void m
                     for (int p = 0; p < P; ++p) d[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i0][i][p], b, d[p], 0, 0, 0);
                 }
                 const float scale = sc[QT == 0 ? (i0 >> 1) : i0];
+                if constexpr (QT == 1) {
+                    // the block dot from the MFMAs' sum of n * x (times 2^-24): times 2^24, minus 8 * sum(x)
+                    const int blk = S * 4 * U + U * g + (q % CPS) * CL + i0;
+#pragma unroll
+                    for (int p = 0; p < P; ++p) {
+                        const float4 cr = *reinterpret_cast<const float4*>(corr_s + (p * nb + blk) * 4);
+                        d[p][0] = fmaf(d[p][0], 0x1p24f, cr.x);
+                        d[p][1] = fmaf(d[p][1], 0x1p24f, cr.y);
+                        d[p][2] = fmaf(d[p][2], 0x1p24f, cr.z);
+                        d[p][3] = fmaf(d[p][3], 0x1p24f, cr.w);
+                    }
+                }
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
                     // combos 0, 1: token 0 hi, lo; combos 2, 3: token 1
@@ -1063,10 +1098,12 @@ bool mgemv_shape(const PackGeom& g, Shape* sh) {
 
 // dynamic LDS: token fragments, the zero fragment, the next site's router rows, the multipliers,
 // and (NORM_MHC) the staging waves' router partial slots, 9 KiB each
-size_t lds_bytes(int M, int K, int U, size_t rrow_bytes, int rin_waves = 0) {
+size_t lds_bytes(int M, int K, int U, size_t rrow_bytes, int rin_waves = 0, int quant = 0) {
     const int P = M <= 2 ? 1 : 2;
     const size_t b = (size_t)P * (K / 32) * 256 + kZeroBytes + rrow_bytes + (size_t)P * (K / (128 * U)) * 8;
-    return rin_waves ? ((b + 15) & ~(size_t)15) + (size_t)rin_waves * 9 * 1024 : b;
+    const size_t r = rin_waves ? ((b + 15) & ~(size_t)15) + (size_t)rin_waves * 9 * 1024 : b;
+    // Q4: the block corrections, 16 bytes per (token pair, block)
+    return quant == 1 ? ((r + 15) & ~(size_t)15) + (size_t)P * (K / 32) * 16 : r;
 }
 }  // namespace
 
@@ -1081,7 +1118,7 @@ bool mgemv_fits(int M, int K) {
     PackGeom g;
     Shape sh;
     if (!pack_geom(0, 16, K, 0, &g) || !mgemv_shape(g, &sh)) return false;
-    return (M <= 2 || sh.upt <= 2) && lds_bytes(M, K, g.U, 0) <= (size_t)kLdsLimit;
+    return (M <= 2 || sh.upt <= 2) && lds_bytes(M, K, g.U, 0, 0, 1) <= (size_t)kLdsLimit;
 }
 
 // 0: launched; 1: this call is not served (M too large for LDS at this K); < 0 error.
@@ -1094,7 +1131,7 @@ int launch_mgemv(const GemvArgs& a, int quant, int M, hipStream_t s) {
     const int P = M <= 2 ? 1 : 2;
     const int tw_max = sh.base + (sh.extra ? 1 : 0);
     const size_t need = lds_bytes(M, a.K, g.U, a.rpart ? (size_t)tw_max * 16 * M * 64 : 0,
-                                  a.pro == GEMV_NORM_MHC ? sh.waves - sh.sw0 : 0);
+                                  a.pro == GEMV_NORM_MHC ? sh.waves - sh.sw0 : 0, quant);
     if (need > (size_t)kLdsLimit || (P == 2 && sh.upt > 2)) return 1;
     const size_t lds = need > sh.lds_floor ? need : sh.lds_floor;
     if ((reinterpret_cast<uintptr_t>(a.wq) & 15) || (reinterpret_cast<uintptr_t>(a.ws) & 15) ||
