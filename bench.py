@@ -299,6 +299,40 @@ def summarize_decode_pmc(d: str) -> str:
     return "\n".join(out) + "\n"
 
 
+SQ_COUNTERS = ["SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_ACTIVE_INST_VALU", "SQ_VALU_MFMA_BUSY_CYCLES",
+               "SQ_INSTS_VMEM_RD", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE"]
+
+
+def summarize_sq(path: str, kernels: dict, cus: int = 256, simds: int = 1024, xccs: int = 8) -> str:
+    """Instruction and busy counters per dispatch of the named kernels (one rocprofv3 --pmc run of
+    SQ_COUNTERS): VALU and MFMA instructions per dispatch, per KiB of weights when given (a wave load
+    is 1 KiB), VALU busy = SQ_ACTIVE_INST_VALU (quad-cycles, summed over the SIMDs) / (CUs x active
+    cycles) and MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x active cycles), as rocprofv3's
+    VALUBusy and MfmaUtil define them; the active cycles are GRBM_GUI_ACTIVE, which the CSV sums over
+    the XCDs.  kernels: {label: (kernel name part, weight bytes per dispatch or 0)}."""
+    import collections
+    import csv
+
+    rows = list(csv.DictReader(open(path)))
+    out = ["| kernel | dispatches | VALU instr | MFMA instr | VALU instr per KiB | VMEM reads | active us | VALU busy | "
+           "MFMA busy |", "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for label, (part, wbytes) in kernels.items():
+        per = collections.defaultdict(dict)  # dispatch -> counter -> value
+        for r in rows:
+            if part in r["Kernel_Name"]:
+                per[r["Dispatch_Id"]][r["Counter_Name"]] = float(r["Counter_Value"])
+        if not per:
+            continue
+        mean = {c: sum(d.get(c, 0.0) for d in per.values()) / len(per) for c in SQ_COUNTERS}
+        gui = max(mean["GRBM_GUI_ACTIVE"] / xccs, 1.0)
+        kib = wbytes / 1024.0 if wbytes else 0.0
+        vk = f"{mean['SQ_INSTS_VALU'] / kib:.1f}" if kib else "-"
+        out.append(f"| {label} | {len(per)} | {mean['SQ_INSTS_VALU']:.0f} | {mean['SQ_INSTS_MFMA']:.0f} | {vk} | "
+                   f"{mean['SQ_INSTS_VMEM_RD']:.0f} | {gui / 2.4e3:.1f} | {100 * mean['SQ_ACTIVE_INST_VALU'] / cus / gui:.1f}% | "
+                   f"{100 * mean['SQ_VALU_MFMA_BUSY_CYCLES'] / simds / gui:.1f}% |")
+    return "\n".join(out) + "\n"
+
+
 def gemv_microbench(snl, reps: int) -> list:
     """The skinny GEMV alone at the shapes of the Q8 GEMV microbench: M in {1, 2} (decode, MTP
     verify) x K = 4096 x N in {4096, 12288, 248320}, Q8_0 and Q4_0 with f32 block scales, each shape's
@@ -485,6 +519,9 @@ def main() -> int:
                     help="counter workload: a few decode steps and op-by-op verify passes; writes the op sequence")
     ap.add_argument("--pmc-attention", nargs=2, metavar=("POS", "INFO_JSON"),
                     help="counter workload: decode attention alone at cache position POS")
+    ap.add_argument("--summarize-sq", nargs=2, metavar=("CSV", "WHICH"),
+                    help="print the instruction / busy counters of one SQ_COUNTERS run: WHICH = decode-q8, "
+                         "decode-q4 or gemm")
     ap.add_argument("--quant", type=int, default=0, choices=(0, 1),
                     help="weights of the --pmc-decode workload: 0 Q8_0, 1 Q4_0")
     ap.add_argument("--gemm-probe", type=int, metavar="QUANT", default=-1,
@@ -498,6 +535,18 @@ def main() -> int:
         print(json.dumps(summarize_pmc(args.summarize_pmc, args.copy_probe_mb or 256), indent=1))
         if os.path.exists(os.path.join(args.summarize_pmc, "ops.json")):
             print(summarize_decode_pmc(args.summarize_pmc))
+        return 0
+    if args.summarize_sq:
+        csv_path, which = args.summarize_sq
+        qt = 1 if which == "decode-q4" else 0
+        wq = 24576 * 4096 * (1.0 if qt == 0 else 0.5) + 24576 * 128 * 4  # gate_up quants + f32 scales
+        if which.startswith("decode"):
+            ks = {f"gate_up ({which[-2:].upper()})": (f"mgemv_kernel<{qt}, 1, 3, 2, 4, 2, 1>", wq),
+                  "down": (f"mgemv_kernel<{qt}, 1, 2, 0, 4, 3, 1>", 4096 * 12288 * (1.0 if qt == 0 else 0.5) + 4096 * 384 * 4),
+                  "deltanet": ("deltanet_kernel<2>", 0), "attend": ("attend_kernel<2, true>", 0)}
+        else:
+            ks = {"prefill GEMM Q8_0": ("mgemm_kernel<0", 0), "prefill GEMM Q4_0": ("mgemm_kernel<1", 0)}
+        print(summarize_sq(csv_path, ks))
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode step runs on a single MI355X (multi-GPU sharding is a "
