@@ -95,19 +95,37 @@ def summarize_pmc(d: str, copy_mb: int) -> dict:
     rec = {"kernel": ROOFLINE_KERNEL, "fetch_kib": fetch, "write_kib": write, "fetch_factor": ff,
            "write_factor": wf, "traffic_bytes": (fetch * ff + write * wf) * 1024.0,
            "kernel_sources_sha256": kernel_source_hash()}
+    # the kernel's mean duration inside graph-launched verify passes (kernel trace of the same
+    # workload: its dispatches before the first op-by-op pass, which starts at the last embed
+    # launches of the trace)
+    kt = os.path.join(d, "kt_kernel_trace.csv")
+    if os.path.exists(kt):
+        rows = _csv_rows(kt)
+        info = json.load(open(os.path.join(d, "ops.json")))
+        starts = [i for i, r in enumerate(rows) if _short(r["Kernel_Name"]).startswith("embed_kernel")]
+        first_eager = starts[-info["passes"]]
+        us = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows[:first_eager]
+              if _short(r["Kernel_Name"]) == ROOFLINE_KERNEL]
+        if us:
+            rec["inpass_us"] = sum(us) / len(us)
+            rec["inpass_launches"] = len(us)
     with open(TRAFFIC_FILE, "w") as fh:
         json.dump(rec, fh, indent=1)
     return rec
 
 
-def measured_traffic():
+def traffic_record():
+    """The roofline kernel's counter record, while the kernel sources hash to the recorded value."""
     try:
         rec = json.load(open(TRAFFIC_FILE))
     except (OSError, ValueError):
         return None
-    if rec.get("kernel_sources_sha256") != kernel_source_hash():
-        return None
-    return round(rec["traffic_bytes"])
+    return rec if rec.get("kernel_sources_sha256") == kernel_source_hash() else None
+
+
+def measured_traffic():
+    rec = traffic_record()
+    return round(rec["traffic_bytes"]) if rec else None
 
 
 # kernels launched by each op of a verify pass, in launch order
@@ -674,6 +692,12 @@ def main() -> int:
         "cpu_baseline": None,
     }
     eng.close()
+    # beside the live back-to-back figure: the kernel's mean inside graph-launched verify passes, from
+    # the kernel trace recorded with its counters (profiles/), while the kernel sources match
+    rec = traffic_record()
+    if rec and rec.get("inpass_us"):
+        result["roofline"]["inpass_trace_us"] = round(rec["inpass_us"], 3)
+        result["roofline"]["frac_inpass_trace"] = round(gu_bytes / (rec["inpass_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     # the same workload on an engine sized for the run alone (decode cost follows the position)
     sized_ctx = PROMPT + 2 * (args.warmup + args.steps) + 64
     e2, sz = decode_leg(snl, cfg, prompt, sized_ctx, args.warmup, args.steps, "sized")
