@@ -156,6 +156,9 @@ struct snl_engine {
     const SnlFile* src = nullptr;
     const SnlFile* msrc = nullptr;
     hipStream_t stream = nullptr;
+    // Passes are captured on a stream of their own, idle whatever the engine's stream still runs
+    // (graphs do not depend on the stream they were captured on).
+    hipStream_t cap_stream = nullptr;
     std::vector<void*> allocs;
     // reference-layout staging of one matrix while the weights are drawn and packed (init only)
     uint8_t* gen_tmp_q = nullptr;
@@ -452,6 +455,9 @@ struct snl_engine {
     }
     int ensure_rope_tab();
     int build_spec_pair(int keys);
+    // Keys of the speculative steps that follow a prompt: the next prefill chunk builds their
+    // graphs (and the rotary table) on the host while its passes run, instead of the first step.
+    int spec_prebuild = 0;
     // the speculative step's graph (run kind 2): the MTP draft over M pairs, then the checkpointed
     // 2-row verify whose second token is the draft's pick, with event records around both passes
     int build_spec(int M, int parity, int sp, hipGraphExec_t* out);
@@ -590,7 +596,8 @@ int snl_engine::init() {
     for (int i = c.loop_end; i < c.n_layers; ++i) plan.push_back(i);
     for (int l : plan) (c.full_attention[l] ? n_full : n_lin)++;
 
-    if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess)
+    if (hipStreamCreateWithFlags(&stream, hipStreamNonBlocking) != hipSuccess ||
+        hipStreamCreateWithFlags(&cap_stream, hipStreamNonBlocking) != hipSuccess)
         return fail(SNL_EDEVICE, "hipStreamCreate failed");
     if (gemv_init()) return fail(SNL_EDEVICE, "GEMV LDS configuration failed");
     int rc;
@@ -970,6 +977,12 @@ int snl_engine::prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int 
         return fail(SNL_EDEVICE, "prefill step upload failed");
     int rc = mtp ? record_mtp_prefill(m, r0) : record_prefill(m, rows);
     if (rc) return fail(SNL_EDEVICE, "prefill launch failed (M %d)", m);
+    if (spec_prebuild > 0) {  // host work while the chunk runs
+        const int keys = spec_prebuild;
+        spec_prebuild = 0;
+        // (on failure the first step builds them again and reports why)
+        if (build_spec_pair(keys)) err.clear();
+    }
     if (hipStreamSynchronize(stream) != hipSuccess) return fail(SNL_EDEVICE, "prefill failed on device");
     return SNL_OK;
 }
@@ -979,6 +992,14 @@ int snl_engine::prefill_chunk(const uint32_t* tokens, const uint32_t* pos3, int 
 // Replays the captured pass of `kind` (0: forward of M rows, a logit rows, checkpoint b; 1: MTP
 // head over M pairs, draft a; 2: a greedy speculative step, the MTP draft over M pairs then the
 // checkpointed 2-row verify) after uploading its step records.
+// Points the engine's launch stream at its capture stream for the life of a capture.
+struct CaptureScope {
+    hipStream_t& s;
+    const hipStream_t keep;
+    CaptureScope(hipStream_t& v, hipStream_t cap) : s(v), keep(v) { s = cap; }
+    ~CaptureScope() { s = keep; }
+};
+
 int snl_engine::run(int kind, int M, int a, int b, int keys, bool upload) {
     const int first = kind == 1 ? 1 : 0, count = kind == 2 ? 2 : 1;
     if (upload &&
@@ -994,6 +1015,7 @@ int snl_engine::run(int kind, int M, int a, int b, int keys, bool upload) {
         it = graphs.emplace(key, ex).first;
     }
     if (it == graphs.end()) {
+        CaptureScope capture(stream, cap_stream);
         hipGraph_t g = nullptr;
         if (hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal) != hipSuccess)
             return fail(SNL_EDEVICE, "hipStreamBeginCapture failed");
@@ -1058,11 +1080,15 @@ int snl_engine::build_spec_pair(int keys) {
 // nodes (an event recorded inside a stream capture was refused here).
 int snl_engine::build_spec(int M, int parity, int sp, hipGraphExec_t* out) {
     if (int rc = ensure_rope_tab()) return rc;
+    for (auto& evs : spec_ev)  // (the graphs' event nodes record these)
+        for (hipEvent_t& ev : evs)
+            if (!ev && hipEventCreate(&ev) != hipSuccess) return fail(SNL_EDEVICE, "event creation failed");
     struct SpanScope {  // the span of this capture, cleared on every return
         int& s;
         SpanScope(int& v, int x) : s(v) { s = x; }
         ~SpanScope() { s = 0; }
     } scope(span, sp);
+    CaptureScope on_cap(stream, cap_stream);
     hipGraph_t ga = nullptr, gb = nullptr, pg = nullptr;
     auto capture = [&](hipGraph_t* g, bool draft) -> int {
         if (const hipError_t be = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal); be != hipSuccess) {
@@ -1322,6 +1348,7 @@ void snl_engine_destroy(snl_engine* e) {
     if (e->h_pstep) hipHostFree(e->h_pstep);
     if (e->topk_host) hipHostFree(e->topk_host);
     if (e->stream) hipStreamDestroy(e->stream);
+    if (e->cap_stream) hipStreamDestroy(e->cap_stream);
     delete e;
 }
 
@@ -1694,9 +1721,6 @@ int spec_prepare(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint
 // Queues step `seq` (instance seq & 1): with upload, from the records spec_prepare wrote; without,
 // from the records the previous step's control kernel left on the device.
 int spec_launch(snl_engine* e, bool upload) {
-    for (auto& evs : e->spec_ev)
-        for (hipEvent_t& ev : evs)
-            if (!ev && hipEventCreate(&ev) != hipSuccess) return e->fail(SNL_EDEVICE, "event creation failed");
     const int parity = (int)(e->spec_seq & 1u);
     // Keys: step seq's verify reaches pos + 2 (host position) and a step queued ahead of it pos + 4;
     // both instances of that context bucket are built before the first launch, so queueing a step
@@ -1761,6 +1785,10 @@ int engine_spec_ahead(snl_engine* e, bool* queued) {
 }
 
 uint32_t engine_spec_seq(const snl_engine* e) { return e->spec_seq; }
+
+// Asks the next prefill chunk to build the speculative step graphs for `keys` cache positions
+// while its passes run (0 withdraws the request).
+void engine_prebuild_spec(snl_engine* e, int keys) { e->spec_prebuild = keys > 0 ? keys : 0; }
 
 // Penalties on logits row `row` of the last forward (in place, as the reference mutates its logits),
 // then its k largest entries (value descending, index ascending on ties): k <= kDistMax on the

@@ -35,6 +35,7 @@ int spec_prepare(snl_engine* e, int r0, const uint32_t* mtok, int mn, const uint
 int spec_launch(snl_engine* e, bool upload);
 int spec_finish(snl_engine* e, uint32_t seq, SpecOut* out, float* draft_ms, float* verify_ms);
 uint32_t engine_spec_seq(const snl_engine* e);
+void engine_prebuild_spec(snl_engine* e, int keys);
 }  // namespace snl
 
 using clk = std::chrono::steady_clock;
@@ -82,11 +83,18 @@ constexpr int kSpecPause = 20;
 // sampled one) waits.  With want, *pick receives the pick of the last token's logits.
 int feed(snl_engine* e, const uint32_t* prompt, int from, int to, bool spec, bool want, snl_pick* pick) {
     const int chunk = snl_prefill_chunk(e);
+    struct Withdraw {  // an unused graph request does not outlive this call
+        snl_engine* e;
+        ~Withdraw() { snl::engine_prebuild_spec(e, 0); }
+    } withdraw{e};
     std::vector<uint32_t> pos3((size_t)to * 3);
     for (int i = 0; i < to; ++i) pos3[(size_t)i * 3] = pos3[(size_t)i * 3 + 1] = pos3[(size_t)i * 3 + 2] = (uint32_t)i;
     snl_pick picks[2];
     for (int c0 = from; c0 < to; c0 += chunk) {
         const int c1 = std::min(c0 + chunk, to);
+        // the first decode step's graphs (its verify reaches position to + 4) are built while the
+        // prompt's last chunk runs
+        if (spec && c1 == to) snl::engine_prebuild_spec(e, to + 4);
         int rc = snl_forward(e, prompt + c0, c1 - c0, pos3.data() + (size_t)c0 * 3, want && c1 == to ? 1 : 0, 0,
                              nullptr, picks);
         if (rc) return rc;

@@ -493,3 +493,22 @@ def test_decode_cost_follows_position(snl_mod):
     assert a[0] == b[0] and a[1:4] == b[1:4]
     assert np.array_equal(a[4], b[4])
     assert np.array_equal(a[5], b[5])
+
+
+def test_decoder_steps_across_a_context_bucket(snl_mod):
+    """Steps queued ahead of the host across the 2048-key bucket edge: the next bucket's step graphs
+    are captured while a step is still queued.  Tokens, counts and the engine state after equal
+    those of single steps."""
+    cfg = snl_mod.tiny_config()
+    e = snl_mod.Engine(cfg, seed=37, quant=0, ctx=4200)
+    try:
+        prompt = _prompt(2030, cfg.vocab, seed=47)
+        one, many = _decode_both(e, prompt, [3, 25, 12])
+        print(f"queued across the bucket edge: {len(one[0])} tokens, pos {one[3]}", flush=True)
+        assert one[3] > 2048 + 4
+        assert many[0] == one[0]
+        assert many[1:5] == one[1:5]
+        for a, b in zip(one[5:], many[5:]):
+            assert np.array_equal(a, b)
+    finally:
+        e.close()
