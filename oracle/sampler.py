@@ -14,9 +14,11 @@ counter in words 12-13, stream 0 in words 14-15) keyed by rand_core 0.10.1's see
 
 Parity: the ChaCha block function is pinned by RFC 7539's block test vector and the zero-key
 keystream (tests/test_sampler.py); the distribution, draw and verify by hand-worked cases and an
-exact integration of verify's output distribution.  The seed expansion and the f32 conversion
-follow the crates' published algorithms; with no Rust here nothing checks them against the
-crates' own output: parity unpinned for those two.
+exact integration of verify's output distribution.  The seed expansion's PCG32 arithmetic (the
+LCG multiplier and the XSH-RR output) is pinned by the PCG reference implementation's demo outputs
+(pcg32_srandom_r(42, 54)); its increment and its advance-then-output order follow rand_core's
+published source, and the f32 conversion rand's: with no Rust here nothing checks those against
+the crates' own output, so parity is unpinned for those two.
 """
 from __future__ import annotations
 
@@ -57,11 +59,26 @@ def chacha_block(state: List[int], rounds: int) -> List[int]:
     return [(x[i] + state[i]) & M32 for i in range(16)]
 
 
-def pcg32(state: int) -> Tuple[int, int]:
-    state = (state * 6364136223846793005 + 11634580027462260723) & ((1 << 64) - 1)
+PCG_MUL = 6364136223846793005
+SEED_INC = 11634580027462260723  # the increment of rand_core's seed_from_u64
+
+
+def lcg(state: int, inc: int = SEED_INC) -> int:
+    """PCG32's state step."""
+    return (state * PCG_MUL + inc) & ((1 << 64) - 1)
+
+
+def xsh_rr(state: int) -> int:
+    """PCG32's output function (xorshift high, random rotation right)."""
     xorshifted = (((state >> 18) ^ state) >> 27) & M32
     rot = state >> 59
-    return state, ((xorshifted >> rot) | (xorshifted << ((32 - rot) & 31))) & M32
+    return ((xorshifted >> rot) | (xorshifted << ((32 - rot) & 31))) & M32
+
+
+def pcg32(state: int) -> Tuple[int, int]:
+    """One word of rand_core's seed_from_u64: the state advances first, then the new state's output."""
+    state = lcg(state)
+    return state, xsh_rr(state)
 
 
 class StdRng:

@@ -57,13 +57,28 @@ def test_rng_stream_matches_restatement(L, seed):
     assert all(float(f * 16777216.0).is_integer() for f in fs)
 
 
-def test_pcg32_seed_expansion_first_word():
-    # first PCG32 step from state 0: state = INC, output from the PCG output function
+def test_pcg32_known_answers():
+    """The PCG32 step and output function of the seed expansion against the PCG reference
+    implementation's demo program (pcg-c-basic): pcg32_srandom_r(42, 54), then six outputs of
+    pcg32_random_r (which outputs the old state, then advances)."""
+    inc = (54 << 1) | 1
+    s = S.lcg(0, inc)
+    s = S.lcg((s + 42) & ((1 << 64) - 1), inc)
+    out = []
+    for _ in range(6):
+        out.append(S.xsh_rr(s))
+        s = S.lcg(s, inc)
+    assert out == [0xA15C02B7, 0x7B47F409, 0xBA1D3330, 0x83D2F293, 0xBFA4784B, 0xCBED606E]
+
+
+def test_pcg32_seed_expansion_wiring():
+    # rand_core's seed_from_u64 advances first and outputs the new state: from state 0 the first
+    # state is the increment itself
     st, w = S.pcg32(0)
-    assert st == 11634580027462260723
-    xs = (((st >> 18) ^ st) >> 27) & 0xFFFFFFFF
-    rot = st >> 59
-    assert w == ((xs >> rot) | (xs << ((32 - rot) & 31))) & 0xFFFFFFFF
+    assert st == S.SEED_INC
+    assert w == S.xsh_rr(S.SEED_INC)
+    st2, w2 = S.pcg32(st)
+    assert st2 == S.lcg(S.SEED_INC) and w2 == S.xsh_rr(st2)
 
 
 def test_draw_hand_cases(L):
