@@ -516,6 +516,57 @@ def decode_leg(snl, cfg, prompt, ctx: int, warmup: int, steps: int, name: str, c
     return eng, res
 
 
+def context_sweep(snl, np, quant: int, lengths, steps: int) -> int:
+    """Step time against context length on one 9B engine allocated for 32768 positions: for each
+    prompt length a fresh random prompt (the decoder resets the engine), 8 untimed greedy MTP steps,
+    then `steps` timed ones in native calls of up to STEP_CHUNK; beside them the decode attention
+    op of a verify pass timed alone at the position reached.  Prints one JSON line."""
+    import torch
+
+    cfg = snl.nine_b_config()
+    eng = snl.Engine(cfg, seed=1, quant=quant, ctx=REF_CTX)
+    rng = np.random.default_rng(7)
+    rows = []
+    try:
+        for n in lengths:
+            if n + steps * 2 + 16 > REF_CTX:
+                raise ValueError(f"prompt of {n} tokens leaves no room for {steps} steps in {REF_CTX}")
+            prompt = rng.integers(0, cfg.vocab, n).tolist()
+            t0 = time.perf_counter()
+            dec = eng.decoder(prompt, spec=True)
+            pf = time.perf_counter() - t0
+            dec.steps(8)
+            st0 = dec.stats()
+            torch.cuda.synchronize()
+            emitted = 0
+            t0 = time.perf_counter()
+            for i0 in range(0, steps, STEP_CHUNK):
+                emitted += len(dec.steps(min(STEP_CHUNK, steps - i0)))
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            st1 = dec.stats()
+            dec.close()
+            drafted = max(st1["drafted"] - st0["drafted"], 1)
+            try:
+                attn_us = round(eng.time_op("attention", 8)[0] * 1e3, 2)
+            except snl.SnlError:
+                attn_us = None
+            row = {"prompt": n, "position_end": eng.pos, "ms_per_step": round(dt / steps * 1e3, 4),
+                   "tok_s": round(emitted / dt, 2),
+                   "draft_ms": round((st1["draft_s"] - st0["draft_s"]) / drafted * 1e3, 4),
+                   "verify_ms": round((st1["verify_s"] - st0["verify_s"]) / drafted * 1e3, 4),
+                   "attention_op_us": attn_us, "prefill_s": round(pf, 3)}
+            log(f"[sweep] prompt {n}: {row['ms_per_step']} ms/step ({row['tok_s']} tok/s), verify "
+                f"{row['verify_ms']} ms, attention op {attn_us} us, prefill {pf:.2f}s")
+            rows.append(row)
+    finally:
+        eng.close()
+    print(json.dumps({"sweep": "9B MTP greedy decode step against context length", "quant": "q8_0" if quant == 0 else "q4_0",
+                      "ctx": REF_CTX, "steps": steps, "data": "synthetic (random-init weights, uniform random prompt ids)",
+                      "rows": rows}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -540,8 +591,11 @@ def main() -> int:
     ap.add_argument("--summarize-sq", nargs=2, metavar=("CSV", "WHICH"),
                     help="print the instruction / busy counters of one SQ_COUNTERS run: WHICH = decode-q8, "
                          "decode-q4 or gemm")
+    ap.add_argument("--context-sweep", metavar="LENGTHS", default="",
+                    help="comma-separated prompt lengths: the decode step against context length on one "
+                         "engine sized for 32768 positions (with --quant; --steps timed steps each), then exit")
     ap.add_argument("--quant", type=int, default=0, choices=(0, 1),
-                    help="weights of the --pmc-decode workload: 0 Q8_0, 1 Q4_0")
+                    help="weights of the --pmc-decode and --context-sweep workloads: 0 Q8_0, 1 Q4_0")
     ap.add_argument("--gemm-probe", type=int, metavar="QUANT", default=-1,
                     help="counter workload: the prefill GEMM alone on the gate_up shape (M 512, N 24576, "
                          "K 4096), Q8_0 (0) or Q4_0 (1), 20 launches")
@@ -587,6 +641,8 @@ def main() -> int:
         return 0
     if args.long_context:
         return long_context(snl, np)
+    if args.context_sweep:
+        return context_sweep(snl, np, args.quant, [int(v) for v in args.context_sweep.split(",")], args.steps)
     if args.pmc_decode:
         return pmc_decode(snl, np, args.pmc_decode, quant=args.quant)
     if args.gemm_probe >= 0:
