@@ -95,9 +95,10 @@ private:
                     unsigned cp = 0;
                     for (int i = 0; i < 4; ++i) {
                         const char h = *p_++;
-                        cp = cp * 16 + (h >= '0' && h <= '9' ? h - '0' : h >= 'a' && h <= 'f' ? h - 'a' + 10
-                                        : h >= 'A' && h <= 'F' ? h - 'A' + 10 : 99);
-                        if (cp > 0xFFFF) return false;
+                        const int dv = h >= '0' && h <= '9' ? h - '0' : h >= 'a' && h <= 'f' ? h - 'a' + 10
+                                     : h >= 'A' && h <= 'F' ? h - 'A' + 10 : -1;
+                        if (dv < 0) return false;
+                        cp = cp * 16 + (unsigned)dv;
                     }
                     if (cp < 0x80) {
                         out->push_back((char)cp);
@@ -164,7 +165,8 @@ private:
         if (lit("false")) return v->type = JVal::BOOL, v->b = false, true;
         if (lit("null")) return v->type = JVal::NUL, true;
         const char* q = p_;
-        while (q < end_ && (strchr("+-0123456789.eE", *q) != nullptr)) ++q;
+        // (strchr also finds the terminator: a NUL byte is no part of a number)
+        while (q < end_ && *q != '\0' && strchr("+-0123456789.eE", *q) != nullptr) ++q;
         if (q == p_) return false;
         v->type = JVal::NUM;
         v->s.assign(p_, q);
@@ -195,7 +197,9 @@ bool get_int(const JVal& obj, const char* key, int64_t lo, int64_t hi, int32_t* 
 bool get_f32(const JVal& obj, const char* key, float* out, std::string* err) {
     const JVal* v = obj.get(key);
     if (!v || v->type != JVal::NUM) return failf(err, "header config: `%s` missing", key);
-    *out = strtof(v->s.c_str(), nullptr);
+    char* e = nullptr;
+    *out = strtof(v->s.c_str(), &e);
+    if (*e || !std::isfinite(*out)) return failf(err, "header config: `%s` is not a finite number", key);
     return true;
 }
 
@@ -357,7 +361,8 @@ bool SnlFile::open(const char* path, std::string* err) {
         else return failf(err, "%s: tensor `%s` has unknown dtype `%s`", path, kv.first.c_str(), d->s.c_str());
         for (const JVal& e : sh->a) {
             uint64_t x;
-            if (!get_u64(&e, &x) || x == 0 || x > (1ull << 31)) return failf(err, "%s: bad shape of `%s`", path, kv.first.c_str());
+            // (dims up to 2^30 keep rows * cols * 4 inside 64 bits for the bounds checks below)
+            if (!get_u64(&e, &x) || x == 0 || x > (1ull << 30)) return failf(err, "%s: bad shape of `%s`", path, kv.first.c_str());
             ft.shape.push_back((int64_t)x);
         }
         if (ft.dtype != FD_F32 && ft.cols() % 32)
