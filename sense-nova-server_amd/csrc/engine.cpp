@@ -1040,7 +1040,8 @@ int snl_engine::run(int kind, int M, int a, int b, int keys, bool upload) {
 
 // The rotary cos / sin of every text position (the three rotary components equal, as decode
 // positions are), bitwise as step_rope forms them, for the records the speculative step's control
-// kernel writes.  Built on the first speculative step, so engines that never draft hold none.
+// kernel writes.  Built with the first speculative step graph, so engines that never draft hold
+// none.
 int snl_engine::ensure_rope_tab() {
     if (rope_tab) return SNL_OK;
     const int rows = ctx + 4, half = cfg.rot_dim / 2;
